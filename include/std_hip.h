@@ -1,0 +1,200 @@
+/*
+ * std_hip.h — C ABI of libstdhip.so, the MI355X (gfx950) decode hot path of
+ * Sparse-to-Dense (STD) speculative decoding.
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers, element
+ * counts and strides, and returns an int status:
+ *     0            success
+ *     < 0          argument validation error (STD_E_*), nothing was launched
+ *     > 0          hipError_t reported by the HIP runtime at launch
+ * Calls are stream-ordered and asynchronous on `stream` (a hipStream_t passed
+ * as void*; NULL is the default stream). No call allocates or frees device
+ * memory: scratch space is a caller-owned workspace whose size is queried up
+ * front with the matching *_workspace_bytes() function. No call synchronizes
+ * the device. The library keeps no mutable global state, so distinct streams
+ * may be driven from distinct host threads.
+ *
+ * Layouts (batch size 1, as in the reference):
+ *   query     [n_q][q_len][d]         row stride d, head stride q_len*d
+ *   KV cache  [n_kv][capacity][d]     row stride d, head stride given per call
+ *             (the reference's per-layer view of a [2L,1,Hkv,max_len,D]
+ *             tensor has head stride max_len*D: read in place, no copy)
+ *   output    [n_q][q_len][d]
+ * Query head h reads KV head h / (n_q / n_kv)  (repeat_kv / enable_gqa order).
+ * Supported: d == 128, 1 <= n_q/n_kv <= 16, dtype STD_F32 or STD_BF16.
+ */
+#ifndef STD_HIP_H
+#define STD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+enum { STD_F32 = 0, STD_BF16 = 1 };
+
+/* validation errors (negative) */
+enum {
+  STD_OK = 0,
+  STD_E_NULL = -1,        /* a required pointer is NULL */
+  STD_E_DTYPE = -2,       /* unsupported dtype */
+  STD_E_SHAPE = -3,       /* unsupported or inconsistent sizes */
+  STD_E_WORKSPACE = -4,   /* workspace smaller than *_workspace_bytes() */
+  STD_E_ALIGN = -5,       /* pointer or stride misaligned for 16-byte access */
+  STD_E_RANGE = -6        /* length or index past the cache capacity */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* std_status_string(int status);
+
+/* Library version, e.g. 0x000100 for 0.1.0. */
+int std_version(void);
+
+/* ------------------------------------------------------------------------
+ * Draft / autoregressive GQA decode attention (q_len == 1, no mask).
+ *
+ * Replaces fused_gqa_attention(query, key, value)
+ *   (src/std_repro/triton_attention.py:83-112) and the draft dispatch to
+ *   F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+ *   (src/std_repro/std_qwen25vl.py:399-417).
+ * out[h][:] = sum_j softmax_j(q[h].k[g(h)][j] * scale) v[g(h)][j], j < kv_len.
+ * K and V are read in place through their head strides (elements); the
+ * reference's .contiguous() copy (std_qwen25vl.py:403-408) is not needed.
+ * ------------------------------------------------------------------------ */
+size_t std_gqa_decode_workspace_bytes(int n_q, int n_kv, int kv_len, int d);
+
+int std_gqa_decode(const void* q, const void* k, const void* v, void* out,
+                   int n_q, int n_kv, int kv_len, int d,
+                   long long k_head_stride, long long v_head_stride,
+                   float scale, int dtype,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dense verify attention for q_len appended query rows (offset-causal).
+ *
+ * Replaces the verify forward's attention: repeat_kv + math SDPA with the
+ *   additive causal mask (src/specvlm/models/modeling_qwen2_5_vl.py:1096-1132,
+ *   mask :65-126 and :1388-1399; backend std_qwen25vl.py:111-116, :802).
+ * kv_len counts every cached key including the q_len new rows, which the
+ * caller has already appended. Query row i (0-based) sees keys
+ * [0, kv_len - q_len + i], the offset_causal_mask of
+ * src/std_repro/sparse_verify_spike.py:24-42. Requires 1 <= q_len,
+ * q_len * (n_q/n_kv) <= 128, q_len <= kv_len.
+ * ------------------------------------------------------------------------ */
+size_t std_verify_attn_workspace_bytes(int n_q, int n_kv, int q_len, int kv_len, int d);
+
+int std_verify_attn(const void* q, const void* k, const void* v, void* out,
+                    int n_q, int n_kv, int q_len, int kv_len, int d,
+                    long long k_head_stride, long long v_head_stride,
+                    float scale, int dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Text-to-video top-K selection for one layer.
+ *
+ * Replaces the selection prefill's probability materialisation
+ *   (modeling_qwen2_5_vl.py:966-995 via :1115-1123) plus
+ *   build_sparse_selection (src/std_repro/std_qwen25vl.py:175-231).
+ * q_text  [n_q][text_len][d]: the text-suffix query rows (RoPE applied), row
+ *         i at absolute position text_start + i; text_len = prompt_len -
+ *         text_start.
+ * k       [n_kv][capacity][d] with head stride k_head_stride, keys
+ *         [0, prompt_len) valid.
+ * score[g][j] = sum over the n_q/n_kv query heads h of group g and text rows
+ *   i with j <= text_start + i of softmax_i(q[h][i].k[g][:] * scale)[j],
+ *   the causal text-row softmax over keys [0, text_start + i]. Logits, exp
+ *   and sums are computed in fp64 from the exact input values.
+ * visual_pos [n_visual] int32, strictly increasing absolute positions < prompt_len.
+ * topk_out [n_kv][k] int32: for every KV head the k visual positions with the
+ *   largest score (ties go to the lowest position), sorted ascending.
+ * scores_out (optional, may be NULL) [n_kv][prompt_len] fp64 column scores.
+ * ------------------------------------------------------------------------ */
+size_t std_select_topk_workspace_bytes(int n_q, int n_kv, int text_len, int prompt_len,
+                                       int n_visual, int d);
+
+int std_select_topk(const void* q_text, const void* k,
+                    int n_q, int n_kv, int text_len, int prompt_len, int text_start, int d,
+                    long long k_head_stride, int dtype,
+                    const int32_t* visual_pos, int n_visual, int k_select,
+                    int32_t* topk_out, double* scores_out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Compact-index construction: per KV head, the sorted union of the
+ * non-visual positions and that head's top-K visual positions
+ *   (std_qwen25vl.py:286-291: torch.unique(cat([non_visual, topk[h]]))).
+ * The two sets must be disjoint and each sorted ascending.
+ * idx_out [n_kv][n_nonvisual + k] int32.
+ * ------------------------------------------------------------------------ */
+int std_build_compact_index(const int32_t* non_visual, int n_nonvisual,
+                            const int32_t* topk, int k_select, int n_kv,
+                            int32_t* idx_out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Sparse-cache compaction gather for one layer, K and V together.
+ *
+ * Replaces copy_prompt_cache + compact_sparse_prompt_cache
+ *   (std_qwen25vl.py:265-320): sparse[g][s][:] = dense[g][idx[g][s]][:] for
+ *   s < compact_len, read straight from the dense cache (no full-prompt copy).
+ * Indices >= dense_rows are rejected with STD_E_RANGE only when checked on the
+ * host; the kernel itself skips any out-of-range index.
+ * ------------------------------------------------------------------------ */
+int std_compact_kv(const void* dense_k, const void* dense_v, void* sparse_k, void* sparse_v,
+                   const int32_t* idx, int n_kv, int compact_len, int d,
+                   long long dense_head_stride, int dense_rows,
+                   long long sparse_head_stride, int sparse_rows,
+                   int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * KV append at a device-resident length.
+ *
+ * Replaces KVCache.cat (src/specvlm/kv_cache/kv_cache.py:54-69) without the
+ * CPU-resident length: rows are written at positions *len_dev + r,
+ * r < rows. new_k/new_v are [n_kv][rows][d] with head stride new_head_stride
+ * and row stride new_row_stride (elements; the projection output viewed as
+ * [1, Hkv, q_len, D] has head stride D and row stride Hkv*D). Writes at or
+ * past `capacity` are skipped. The length itself is advanced separately with
+ * std_len_add so that every layer of a step appends at the same position.
+ * ------------------------------------------------------------------------ */
+int std_kv_append(void* cache_k, void* cache_v, const void* new_k, const void* new_v,
+                  int n_kv, int rows, int d,
+                  long long cache_head_stride, long long new_head_stride, long long new_row_stride,
+                  int capacity, const int32_t* len_dev, int dtype, void* stream);
+
+/* len[i] += delta for i < n (device int32). */
+int std_len_add(int32_t* len_dev, int n, int delta, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Greedy acceptance plus cache rollback on the device.
+ *
+ * Replaces the verify tail of std_generate_qwen25vl
+ *   (std_qwen25vl.py:806-815 and the rollback :923-928); the pure contract is
+ *   greedy_prefix (src/std_repro/hsd_spike.py:30-43).
+ * logits [q_rows][vocab] (row stride logits_row_stride elements).
+ * pred[r] = argmax(logits[r]) (first maximum; NaN counts as the maximum).
+ * predictions = pred                       if has_pending (q_rows == n_draft+1)
+ *             = [*dense_next] ++ pred      otherwise      (q_rows == n_draft)
+ * accept = longest prefix with draft[i] == predictions[i]; bonus = predictions[accept].
+ * out[0] = accept, out[1] = bonus, out[2 .. 2+n_draft] = predictions.
+ * Rollback: rollback_lens is a device int32 array of n_lens cache lengths
+ * (e.g. {dense_len, sparse_len}); each is decreased by (n_draft - accept),
+ * undoing the rejected draft rows appended to the dense cache by verify and
+ * to the sparse cache by drafting. n_lens may be 0.
+ * dense_next may be NULL when has_pending != 0.
+ * ------------------------------------------------------------------------ */
+size_t std_greedy_accept_workspace_bytes(int q_rows, int vocab);
+
+int std_greedy_accept(const void* logits, long long logits_row_stride, int q_rows, int vocab,
+                      int dtype, const int32_t* draft, int n_draft, int has_pending,
+                      const int32_t* dense_next, int32_t* out,
+                      int32_t* rollback_lens, int n_lens,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STD_HIP_H */

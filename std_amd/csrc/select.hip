@@ -1,0 +1,509 @@
+// Text-to-video top-K selection and sparse-cache compaction.
+//
+// Score of key j for KV head g (the reference sums the selection prefill's
+// attention probabilities over the group's query heads and the text rows,
+// src/std_repro/std_qwen25vl.py:204-218):
+//     score[g][j] = sum_{h in g} sum_{i : j <= text_start + i} exp(s_hij - lse_hi)
+//     s_hij = (q[h][i] . k[g][j]) * scale,  lse_hi = log sum_{j' <= text_start+i} exp(s_hij')
+// Everything is fp64. A bf16*bf16 (or fp32*fp32) product is exact in fp64, so a
+// 128-term fp64 dot product agrees with any other summation order to ~1e-16
+// relative; the column scores of two platforms then differ by ~1e-15 relative,
+// far below the gap between neighbouring scores, and the top-K index sets
+// agree except on exact ties, which both sides break toward the lowest index.
+// Every column is reduced by the same instruction sequence, so bit-identical
+// key columns get bit-identical scores.
+//
+//   pass 1  sel_rowstats: per (row, key block) partial (max, sum exp)    MFMA f64
+//   merge   sel_lse:      lse per row, blocks in fixed order
+//   pass 2  sel_colsum:   per (row group, key) partial column sums       MFMA f64
+//   keys    sel_keys:     column score of every visual position, row groups in order
+//   select  sel_topk:     radix select of the k-th largest (score, -position),
+//                         then an ordered scan that emits positions ascending
+#include <cfloat>
+
+#include "common.h"
+
+namespace stdhip {
+namespace {
+
+constexpr int D = kHeadDim;
+
+template <typename T> __device__ __forceinline__ double to_f64(T x) { return (double)to_f32<T>(x); }
+
+__device__ __forceinline__ f64x4 mfma_f64(double a, double b, f64x4 c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// v_mfma_f64_16x16x4f64 operand layout (lane l = 16*lg + ln): A[m = ln][k = lg],
+// B[k = lg][n = ln]; result element i of lane l is D[lg + 4*i][ln] (rows
+// interleaved by 4, unlike the fp32-accumulator 16x16 forms whose element i is
+// row 4*lg + i).
+//
+// Pass 1. grid (n_kb, n_kv, n_rg1), block 256 (4 waves x 4 row tiles of 16).
+// S^T tile = K Q^T: A[m = ln][k = lg] = K[key][4c + lg] from LDS (fp64),
+// B[k = lg][n = ln] = Q[row][4c + lg] from registers; lane holds row ln and
+// keys lg + 4i of the 16-key subtile.
+constexpr int P1_RTW = 4;
+constexpr int P1_WAVES = 4;
+constexpr int P1_ROWS = P1_WAVES * P1_RTW * 16;  // 256 rows per workgroup
+constexpr int P1_TK = 64;
+constexpr int KROW64 = D + 1;                    // LDS pitch in doubles
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+sel_rowstats_kernel(const T* __restrict__ q, const T* __restrict__ k, double2* __restrict__ part,
+                    int group, int text_len, int prompt_len, int text_start, long long k_hs,
+                    double scale, int keys_per_block, int n_kb) {
+  __shared__ double Ks[P1_TK * KROW64];
+  const int kbk = blockIdx.x, g = blockIdx.y, rg = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const int R = group * text_len;
+
+  float qf[P1_RTW][32];
+  int lim[P1_RTW];
+#pragma unroll
+  for (int j = 0; j < P1_RTW; ++j) {
+    const int r = (rg * P1_WAVES * P1_RTW + w * P1_RTW + j) * 16 + ln;
+    if (r < R) {
+      const int hl = r / text_len, i = r - hl * text_len;
+      const T* row = q + ((long long)(g * group + hl) * text_len + i) * D;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) qf[j][c] = to_f32<T>(row[4 * c + lg]);
+      lim[j] = text_start + i;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 32; ++c) qf[j][c] = 0.f;
+      lim[j] = -1;
+    }
+  }
+  double m_run[P1_RTW], l_run[P1_RTW];
+#pragma unroll
+  for (int j = 0; j < P1_RTW; ++j) { m_run[j] = -DBL_MAX; l_run[j] = 0.0; }
+
+  const T* kh = k + (long long)g * k_hs;
+  const int kbeg = kbk * keys_per_block;
+  const int kend = min(prompt_len, kbeg + keys_per_block);
+  for (int key0 = kbeg; key0 < kend; key0 += P1_TK) {
+    __syncthreads();
+    for (int e = tid; e < P1_TK * D; e += 256) {
+      const int kr = e / D, d = e - kr * D, key = key0 + kr;
+      Ks[kr * KROW64 + d] = key < kend ? to_f64<T>(kh[(long long)key * D + d]) : 0.0;
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int ks = 0; ks < P1_TK / 16; ++ks) {
+      f64x4 acc[P1_RTW];
+#pragma unroll
+      for (int j = 0; j < P1_RTW; ++j) acc[j] = f64x4{0.0, 0.0, 0.0, 0.0};
+      const double* arow = Ks + (ks * 16 + ln) * KROW64 + lg;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) {
+        const double a = arow[4 * c];
+#pragma unroll
+        for (int j = 0; j < P1_RTW; ++j) acc[j] = mfma_f64(a, (double)qf[j][c], acc[j]);
+      }
+      const int kb = key0 + ks * 16 + lg;
+#pragma unroll
+      for (int j = 0; j < P1_RTW; ++j) {
+        double s[4];
+        bool ok[4];
+        double mt = -DBL_MAX;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb + 4 * i;
+          ok[i] = key < kend && key <= lim[j];
+          s[i] = acc[j][i] * scale;
+          if (ok[i]) mt = fmax(mt, s[i]);
+        }
+        if (mt > m_run[j]) {
+          l_run[j] *= exp(m_run[j] - mt);
+          m_run[j] = mt;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (ok[i]) l_run[j] += exp(s[i] - m_run[j]);
+      }
+    }
+  }
+  // combine the four lane groups (disjoint keys of the same row)
+#pragma unroll
+  for (int j = 0; j < P1_RTW; ++j) {
+    double m = m_run[j], l = l_run[j];
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      const double mo = __shfl_xor(m, off), lo = __shfl_xor(l, off);
+      const double mm = fmax(m, mo);
+      l = l * exp(m - mm) + lo * exp(mo - mm);
+      m = mm;
+    }
+    const int r = (rg * P1_WAVES * P1_RTW + w * P1_RTW + j) * 16 + ln;
+    if (lg == 0 && r < R) part[((long long)g * n_kb + kbk) * R + r] = make_double2(m, l);
+  }
+}
+
+// lse[g][r] from the n_kb partials, in block order.
+__global__ void __launch_bounds__(256)
+sel_lse_kernel(const double2* __restrict__ part, double* __restrict__ lse, int R, int n_kb, int n_kv) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n_kv * R) return;
+  const int g = idx / R, r = idx - g * R;
+  const double2* p = part + (long long)g * n_kb * R + r;
+  double M = -DBL_MAX;
+  for (int b = 0; b < n_kb; ++b) M = fmax(M, p[(long long)b * R].x);
+  double L = 0.0;
+  for (int b = 0; b < n_kb; ++b) {
+    const double2 v = p[(long long)b * R];
+    L += v.y * exp(v.x - M);
+  }
+  lse[idx] = M + log(L);
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2. grid (n_kb2, n_kv, n_rg2), block 256. A row group of 128 rows is
+// staged in LDS; each wave takes 16-key column tiles, holds K^T in registers
+// and walks the 8 row tiles: S tile = Q K^T, A[m = ln][k = lg] = Q[row][4c+lg],
+// B[k = lg][n = ln] = K[key][4c + lg]; lane holds key ln and rows lg + 4i.
+constexpr int P2_RT = 8;
+constexpr int P2_ROWS = P2_RT * 16;
+constexpr int QROW = D + 4;
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+sel_colsum_kernel(const T* __restrict__ q, const T* __restrict__ k, const double* __restrict__ lse,
+                  double* __restrict__ colpart, int group, int text_len, int prompt_len, int text_start,
+                  long long k_hs, double scale, int keys_per_block, int n_kv) {
+  __shared__ float Qs[P2_ROWS * QROW];
+  __shared__ double Ls[P2_ROWS];
+  __shared__ int Lim[P2_ROWS];
+  const int kbk = blockIdx.x, g = blockIdx.y, rg = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ln = lane & 15, lg = lane >> 4;
+  const int R = group * text_len;
+  for (int e = tid; e < P2_ROWS * D; e += 256) {
+    const int rr = e / D, d = e - rr * D, r = rg * P2_ROWS + rr;
+    float v = 0.f;
+    if (r < R) {
+      const int hl = r / text_len, i = r - hl * text_len;
+      v = to_f32<T>(q[((long long)(g * group + hl) * text_len + i) * D + d]);
+    }
+    Qs[rr * QROW + d] = v;
+  }
+  for (int e = tid; e < P2_ROWS; e += 256) {
+    const int r = rg * P2_ROWS + e;
+    Ls[e] = r < R ? lse[(long long)g * R + r] : 0.0;
+    Lim[e] = r < R ? text_start + (r % text_len) : -1;
+  }
+  __syncthreads();
+
+  const T* kh = k + (long long)g * k_hs;
+  const int kbeg = kbk * keys_per_block;
+  const int kend = min(prompt_len, kbeg + keys_per_block);
+  for (int kt0 = kbeg + w * 16; kt0 < kend; kt0 += 4 * 16) {
+    const int key = kt0 + ln;
+    double bk[32];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) bk[c] = key < kend ? to_f64<T>(kh[(long long)key * D + 4 * c + lg]) : 0.0;
+    double colsum = 0.0;
+#pragma unroll 1
+    for (int rt = 0; rt < P2_RT; ++rt) {
+      f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+      const float* arow = Qs + (rt * 16 + ln) * QROW + lg;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) acc = mfma_f64((double)arow[4 * c], bk[c], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = rt * 16 + lg + 4 * i;
+        if (key < kend && key <= Lim[rr]) colsum += exp(acc[i] * scale - Ls[rr]);
+      }
+    }
+    colsum += __shfl_xor(colsum, 16);
+    colsum += __shfl_xor(colsum, 32);
+    if (lg == 0 && key < kend) colpart[((long long)rg * n_kv + g) * prompt_len + key] = colsum;
+  }
+}
+
+// Column score of each visual position as an order-preserving u64 key
+// (scores are >= 0, so the IEEE bit pattern orders like the value), and the
+// optional full score row. grid (ceil(max(n_vis, P) / 256), n_kv).
+__global__ void __launch_bounds__(256)
+sel_keys_kernel(const double* __restrict__ colpart, int n_rg2, int n_kv, int prompt_len,
+                const int32_t* __restrict__ vis, int n_vis, unsigned long long* __restrict__ keys,
+                double* __restrict__ scores_out) {
+  const int g = blockIdx.y;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n_vis) {
+    const int j = vis[t];
+    double s = 0.0;
+    if (j >= 0 && j < prompt_len)
+      for (int rg = 0; rg < n_rg2; ++rg) s += colpart[((long long)rg * n_kv + g) * prompt_len + j];
+    keys[(long long)g * n_vis + t] = (unsigned long long)__double_as_longlong(s);
+  }
+  if (scores_out != nullptr && t < prompt_len) {
+    double s = 0.0;
+    for (int rg = 0; rg < n_rg2; ++rg) s += colpart[((long long)rg * n_kv + g) * prompt_len + t];
+    scores_out[(long long)g * prompt_len + t] = s;
+  }
+}
+
+constexpr int TOPK_THREADS = 1024;
+
+// Exclusive prefix sum over the block (1024 threads) in thread order.
+__device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) wave_tot[w] = x;
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int i = 0; i < TOPK_THREADS / 64; ++i) {
+      const int t = wave_tot[i];
+      wave_tot[i] = acc;
+      acc += t;
+    }
+    *total = acc;
+  }
+  __syncthreads();
+  const int res = wave_tot[w] + x - v;
+  __syncthreads();
+  return res;
+}
+
+// grid (n_kv), block 1024.
+__global__ void __launch_bounds__(TOPK_THREADS)
+sel_topk_kernel(const unsigned long long* __restrict__ keys_all, const int32_t* __restrict__ vis, int n_vis,
+                int k_sel, int32_t* __restrict__ topk_out) {
+  __shared__ unsigned int hist[256];
+  __shared__ int wave_tot[TOPK_THREADS / 64];
+  __shared__ int s_total, s_digit, s_kk;
+  const int g = blockIdx.x, tid = threadIdx.x;
+  const unsigned long long* keys = keys_all + (long long)g * n_vis;
+
+  unsigned long long prefix = 0, mask = 0;
+  int kk = k_sel;  // rank (from the top) still to be located inside the current prefix
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int b = tid; b < 256; b += TOPK_THREADS) hist[b] = 0;
+    __syncthreads();
+    for (int t = tid; t < n_vis; t += TOPK_THREADS) {
+      const unsigned long long u = keys[t];
+      if ((u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int cum = 0, b = 255;
+      for (; b > 0; --b) {
+        if (cum + (int)hist[b] >= kk) break;
+        cum += (int)hist[b];
+      }
+      s_digit = b;
+      s_kk = kk - cum;
+    }
+    __syncthreads();
+    prefix |= (unsigned long long)s_digit << shift;
+    mask |= 255ull << shift;
+    kk = s_kk;
+    __syncthreads();
+  }
+  // prefix is the k-th largest key; take every key above it and the kk
+  // lowest-position keys equal to it, emitting positions in ascending order.
+  const int chunk = (n_vis + TOPK_THREADS - 1) / TOPK_THREADS;
+  const int t0 = min(n_vis, tid * chunk), t1 = min(n_vis, t0 + chunk);
+  int n_eq = 0;
+  for (int t = t0; t < t1; ++t) n_eq += keys[t] == prefix;
+  int eq_rank = block_exclusive_scan(n_eq, wave_tot, &s_total);
+  int n_sel = 0;
+  {
+    int r = eq_rank;
+    for (int t = t0; t < t1; ++t) {
+      const unsigned long long u = keys[t];
+      if (u > prefix) ++n_sel;
+      else if (u == prefix) { if (r < kk) ++n_sel; ++r; }
+    }
+  }
+  int off = block_exclusive_scan(n_sel, wave_tot, &s_total);
+  int32_t* out = topk_out + (long long)g * k_sel;
+  for (int t = t0; t < t1; ++t) {
+    const unsigned long long u = keys[t];
+    bool take = false;
+    if (u > prefix) take = true;
+    else if (u == prefix) { take = eq_rank < kk; ++eq_rank; }
+    if (take && off < k_sel) out[off++] = vis[t];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Compact index: sorted union of two disjoint sorted lists.
+__device__ __forceinline__ int count_below(const int32_t* a, int n, int v) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] < v) lo = mid + 1; else hi = mid;
+  }
+  return lo;
+}
+
+__global__ void __launch_bounds__(256)
+compact_index_kernel(const int32_t* __restrict__ nonvis, int n_nv, const int32_t* __restrict__ topk, int k_sel,
+                     int32_t* __restrict__ idx_out) {
+  const int g = blockIdx.y;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int total = n_nv + k_sel;
+  if (t >= total) return;
+  const int32_t* tk = topk + (long long)g * k_sel;
+  int32_t* out = idx_out + (long long)g * total;
+  if (t < n_nv) {
+    const int v = nonvis[t];
+    out[t + count_below(tk, k_sel, v)] = v;
+  } else {
+    const int j = t - n_nv, v = tk[j];
+    out[j + count_below(nonvis, n_nv, v)] = v;
+  }
+}
+
+// Row gather / scatter in 16-byte chunks (element-type agnostic).
+// grid (ceil(rows * cpr / 256), n_kv, 2 for K and V).
+__global__ void __launch_bounds__(256)
+compact_kv_kernel(const char* __restrict__ dk, const char* __restrict__ dv, char* __restrict__ sk,
+                  char* __restrict__ sv, const int32_t* __restrict__ idx, int compact_len, int row_bytes,
+                  long long dhs_bytes, int dense_rows, long long shs_bytes, int sparse_rows) {
+  const int g = blockIdx.y, kv = blockIdx.z;
+  const int cpr = row_bytes / 16;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int s = c / cpr, col = c - s * cpr;
+  if (s >= compact_len || s >= sparse_rows) return;
+  const int src_row = idx[(long long)g * compact_len + s];
+  if (src_row < 0 || src_row >= dense_rows) return;
+  const char* src = (kv ? dv : dk) + g * dhs_bytes + (long long)src_row * row_bytes + col * 16;
+  char* dst = (kv ? sv : sk) + g * shs_bytes + (long long)s * row_bytes + col * 16;
+  *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+}
+
+// ---------------------------------------------------------------------------
+struct SelectPlan {
+  int R, n_rg1, n_kb, kpb1, n_rg2, n_kb2, kpb2;
+  size_t off_part, off_lse, off_col, off_keys, total;
+};
+
+SelectPlan plan_select(int n_q, int n_kv, int text_len, int prompt_len, int n_vis) {
+  SelectPlan p;
+  p.R = (n_q / n_kv) * text_len;
+  p.n_rg1 = (p.R + P1_ROWS - 1) / P1_ROWS;
+  int per_kb = n_kv * p.n_rg1;
+  p.n_kb = (512 + per_kb - 1) / per_kb;
+  p.kpb1 = (int)round_up((size_t)((prompt_len + p.n_kb - 1) / p.n_kb), P1_TK);
+  p.n_kb = (prompt_len + p.kpb1 - 1) / p.kpb1;
+  p.n_rg2 = (p.R + P2_ROWS - 1) / P2_ROWS;
+  per_kb = n_kv * p.n_rg2;
+  p.n_kb2 = (1024 + per_kb - 1) / per_kb;
+  p.kpb2 = (int)round_up((size_t)((prompt_len + p.n_kb2 - 1) / p.n_kb2), 64);
+  p.n_kb2 = (prompt_len + p.kpb2 - 1) / p.kpb2;
+  p.off_part = 0;
+  p.off_lse = round_up(p.off_part + (size_t)n_kv * p.n_kb * p.R * sizeof(double2), 256);
+  p.off_col = round_up(p.off_lse + (size_t)n_kv * p.R * sizeof(double), 256);
+  p.off_keys = round_up(p.off_col + (size_t)p.n_rg2 * n_kv * prompt_len * sizeof(double), 256);
+  p.total = round_up(p.off_keys + (size_t)n_kv * n_vis * sizeof(unsigned long long), 256);
+  return p;
+}
+
+bool select_shape_ok(int n_q, int n_kv, int text_len, int prompt_len, int text_start, int d, int n_vis, int k_sel) {
+  if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0) return false;
+  if (text_len < 1 || text_start < 0 || prompt_len != text_start + text_len) return false;
+  if (n_vis < 1 || n_vis > prompt_len || k_sel < 1 || k_sel > n_vis) return false;
+  return true;
+}
+
+template <typename T>
+int launch_select(const void* q_text, const void* k, int n_q, int n_kv, int text_len, int prompt_len, int text_start,
+                  long long k_hs, const int32_t* vis, int n_vis, int k_sel, int32_t* topk_out, double* scores_out,
+                  void* ws, hipStream_t st) {
+  const SelectPlan p = plan_select(n_q, n_kv, text_len, prompt_len, n_vis);
+  char* base = static_cast<char*>(ws);
+  double2* part = reinterpret_cast<double2*>(base + p.off_part);
+  double* lse = reinterpret_cast<double*>(base + p.off_lse);
+  double* colpart = reinterpret_cast<double*>(base + p.off_col);
+  unsigned long long* keys = reinterpret_cast<unsigned long long*>(base + p.off_keys);
+  const int group = n_q / n_kv;
+  const double scale = 1.0 / sqrt((double)D);
+  const T* qt = static_cast<const T*>(q_text);
+  const T* kk = static_cast<const T*>(k);
+  hipLaunchKernelGGL((sel_rowstats_kernel<T>), dim3(p.n_kb, n_kv, p.n_rg1), dim3(256), 0, st, qt, kk, part, group,
+                     text_len, prompt_len, text_start, k_hs, scale, p.kpb1, p.n_kb);
+  int s = launch_status();
+  if (s) return s;
+  hipLaunchKernelGGL(sel_lse_kernel, dim3((n_kv * p.R + 255) / 256), dim3(256), 0, st, part, lse, p.R, p.n_kb, n_kv);
+  if ((s = launch_status())) return s;
+  hipLaunchKernelGGL((sel_colsum_kernel<T>), dim3(p.n_kb2, n_kv, p.n_rg2), dim3(256), 0, st, qt, kk, lse, colpart,
+                     group, text_len, prompt_len, text_start, k_hs, scale, p.kpb2, n_kv);
+  if ((s = launch_status())) return s;
+  const int n_cols = n_vis > prompt_len ? n_vis : prompt_len;
+  hipLaunchKernelGGL(sel_keys_kernel, dim3((n_cols + 255) / 256, n_kv), dim3(256), 0, st, colpart, p.n_rg2, n_kv,
+                     prompt_len, vis, n_vis, keys, scores_out);
+  if ((s = launch_status())) return s;
+  hipLaunchKernelGGL(sel_topk_kernel, dim3(n_kv), dim3(TOPK_THREADS), 0, st, keys, vis, n_vis, k_sel, topk_out);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace stdhip
+
+using namespace stdhip;
+
+extern "C" size_t std_select_topk_workspace_bytes(int n_q, int n_kv, int text_len, int prompt_len, int n_visual,
+                                                  int d) {
+  if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || text_len < 1 || prompt_len < text_len || n_visual < 1)
+    return 0;
+  return plan_select(n_q, n_kv, text_len, prompt_len, n_visual).total;
+}
+
+extern "C" int std_select_topk(const void* q_text, const void* k, int n_q, int n_kv, int text_len, int prompt_len,
+                               int text_start, int d, long long k_head_stride, int dtype, const int32_t* visual_pos,
+                               int n_visual, int k_select, int32_t* topk_out, double* scores_out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (!q_text || !k || !visual_pos || !topk_out || !workspace) return STD_E_NULL;
+  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (!select_shape_ok(n_q, n_kv, text_len, prompt_len, text_start, d, n_visual, k_select)) return STD_E_SHAPE;
+  if (n_kv > 1 && k_head_stride < (long long)prompt_len * D) return STD_E_SHAPE;
+  if (workspace_bytes < plan_select(n_q, n_kv, text_len, prompt_len, n_visual).total) return STD_E_WORKSPACE;
+  if (!aligned16(workspace)) return STD_E_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == STD_BF16)
+    return launch_select<bf16_t>(q_text, k, n_q, n_kv, text_len, prompt_len, text_start, k_head_stride, visual_pos,
+                                 n_visual, k_select, topk_out, scores_out, workspace, st);
+  return launch_select<float>(q_text, k, n_q, n_kv, text_len, prompt_len, text_start, k_head_stride, visual_pos,
+                              n_visual, k_select, topk_out, scores_out, workspace, st);
+}
+
+extern "C" int std_build_compact_index(const int32_t* non_visual, int n_nonvisual, const int32_t* topk, int k_select,
+                                       int n_kv, int32_t* idx_out, void* stream) {
+  if (!topk || !idx_out || (n_nonvisual > 0 && !non_visual)) return STD_E_NULL;
+  if (n_nonvisual < 0 || k_select < 1 || n_kv < 1) return STD_E_SHAPE;
+  const int total = n_nonvisual + k_select;
+  hipLaunchKernelGGL(compact_index_kernel, dim3((total + 255) / 256, n_kv), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), non_visual, n_nonvisual, topk, k_select, idx_out);
+  return launch_status();
+}
+
+extern "C" int std_compact_kv(const void* dense_k, const void* dense_v, void* sparse_k, void* sparse_v,
+                              const int32_t* idx, int n_kv, int compact_len, int d, long long dense_head_stride,
+                              int dense_rows, long long sparse_head_stride, int sparse_rows, int dtype,
+                              void* stream) {
+  if (!dense_k || !dense_v || !sparse_k || !sparse_v || !idx) return STD_E_NULL;
+  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (d != D || n_kv < 1 || compact_len < 1 || dense_rows < 1 || sparse_rows < 1) return STD_E_SHAPE;
+  if (compact_len > sparse_rows) return STD_E_RANGE;
+  const int es = dtype_size(dtype);
+  if (!aligned16(dense_k) || !aligned16(dense_v) || !aligned16(sparse_k) || !aligned16(sparse_v)) return STD_E_ALIGN;
+  if ((dense_head_stride * es) % 16 || (sparse_head_stride * es) % 16) return STD_E_ALIGN;
+  const int row_bytes = D * es, cpr = row_bytes / 16;
+  const long long chunks = (long long)compact_len * cpr;
+  hipLaunchKernelGGL(compact_kv_kernel, dim3((unsigned)((chunks + 255) / 256), n_kv, 2), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const char*>(dense_k),
+                     static_cast<const char*>(dense_v), static_cast<char*>(sparse_k), static_cast<char*>(sparse_v),
+                     idx, compact_len, row_bytes, dense_head_stride * es, dense_rows, sparse_head_stride * es,
+                     sparse_rows);
+  return launch_status();
+}

@@ -1,0 +1,303 @@
+"""Tensor-level wrappers of the HIP hot path (torch on ROCm is only the
+allocator and stream provider here; all compute runs in libstdhip.so).
+
+Every function validates dtype, device, shape and strides on the host, then
+calls the C ABI on the tensors' device and current stream. Nonzero statuses
+raise ``StdHipError`` (a RuntimeError), as the reference raises
+RuntimeError/ValueError on unsupported calls (std_qwen25vl.py:379-402).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return _lib.STD_F32
+    if t.dtype == torch.bfloat16:
+        return _lib.STD_BF16
+    raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16")
+
+
+def _check_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError("the HIP hot path needs tensors on a ROCm device (got %s)" % dev)
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _workspace(nbytes: int, dev: torch.device) -> Tuple[int, torch.Tensor]:
+    if nbytes == 0:
+        return 0, None
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    return buf.data_ptr(), buf
+
+
+def _check_cache_view(name: str, t: torch.Tensor) -> None:
+    """[1, Hkv, S, D] with contiguous rows; any head stride (cache view)."""
+    if t.dim() != 4 or t.shape[0] != 1:
+        raise ValueError(f"{name} must be [1, n_kv, seq, head_dim], got {tuple(t.shape)}")
+    if t.shape[3] != HEAD_DIM:
+        raise ValueError(f"{name}: head_dim {t.shape[3]} unsupported (only {HEAD_DIM})")
+    if t.stride(3) != 1 or t.stride(2) != HEAD_DIM:
+        raise ValueError(f"{name}: rows must be contiguous (strides {t.stride()})")
+
+
+def _check_rows_contiguous(name: str, t: torch.Tensor) -> None:
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def gqa_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+               scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Single-query GQA attention, the draft / AR decode step.
+
+    query [1, n_q, 1, D]; key, value [1, n_kv, S, D] (cache views, read in
+    place through their head stride). Returns [1, n_q, 1, D] in query dtype.
+    Same contract as fused_gqa_attention (triton_attention.py:83-112) and
+    F.scaled_dot_product_attention(q, k, v, enable_gqa=True) with q_len = 1
+    (std_qwen25vl.py:409-417).
+    """
+    if query.dim() != 4 or query.shape[0] != 1 or query.shape[2] != 1:
+        raise ValueError(f"Expected q_len=1 query [1, n_q, 1, D], got {tuple(query.shape)}")
+    return _attention("std_gqa_decode", query, key, value, scale, out)
+
+
+def verify_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                     scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense verify attention for q_len appended rows with the offset-causal mask.
+
+    query [1, n_q, Q, D]; key, value [1, n_kv, kv_len, D] including the Q new
+    rows. Row i sees keys [0, kv_len - Q + i] (sparse_verify_spike.py:24-42,
+    the math-SDPA verify of modeling_qwen2_5_vl.py:1096-1132).
+    """
+    if query.dim() != 4 or query.shape[0] != 1:
+        raise ValueError(f"Expected query [1, n_q, Q, D], got {tuple(query.shape)}")
+    return _attention("std_verify_attn", query, key, value, scale, out)
+
+
+def _attention(fn: str, query, key, value, scale, out):
+    dev = _check_device(query, key, value)
+    code = _dtype_code(query)
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise TypeError("query, key and value must share a dtype")
+    _check_cache_view("key", key)
+    _check_cache_view("value", value)
+    _check_rows_contiguous("query", query)
+    _, n_q, q_len, d = query.shape
+    n_kv, kv_len = key.shape[1], key.shape[2]
+    if value.shape != key.shape:
+        raise ValueError(f"key {tuple(key.shape)} and value {tuple(value.shape)} differ")
+    if d != HEAD_DIM:
+        raise ValueError(f"head_dim {d} unsupported")
+    if n_q % n_kv != 0:
+        raise ValueError(f"n_q={n_q} is not a multiple of n_kv={n_kv}")
+    if q_len > kv_len:
+        raise ValueError(f"q_len={q_len} exceeds kv_len={kv_len}")
+    if out is None:
+        out = torch.empty_like(query)
+    elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like query")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    lib = _lib.load_library()
+    if fn == "std_gqa_decode":
+        ws_bytes = lib.std_gqa_decode_workspace_bytes(n_q, n_kv, kv_len, d)
+    else:
+        ws_bytes = lib.std_verify_attn_workspace_bytes(n_q, n_kv, q_len, kv_len, d)
+    ws_ptr, ws = _workspace(ws_bytes, dev)
+    hs_k, hs_v = key.stride(1), value.stride(1)
+    if fn == "std_gqa_decode":
+        _lib.call(fn, query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), n_q, n_kv, kv_len, d,
+                  hs_k, hs_v, float(scale), code, ws_ptr, ws_bytes, _stream(dev))
+    else:
+        _lib.call(fn, query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), n_q, n_kv, q_len, kv_len,
+                  d, hs_k, hs_v, float(scale), code, ws_ptr, ws_bytes, _stream(dev))
+    return out
+
+
+def fused_gqa_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+    """Drop-in for std_repro.triton_attention.fused_gqa_attention (same
+    signature and output allocation: a new tensor in query dtype)."""
+    return gqa_decode(query, key, value)
+
+
+def select_topk(q_text: torch.Tensor, key: torch.Tensor, text_start: int, visual_positions: torch.Tensor,
+                k: int, return_scores: bool = False):
+    """Per-KV-head top-k visual positions from causal text-row attention.
+
+    q_text [1, n_q, T, D] (text-suffix queries, RoPE applied); key
+    [1, n_kv, >= P, D] cache view with P = text_start + T valid keys;
+    visual_positions int32 [n_visual] sorted ascending. Returns int32
+    [n_kv, k] sorted ascending (and fp64 scores [n_kv, P] if requested).
+    Restates build_sparse_selection (std_qwen25vl.py:175-231) on the exact
+    softmax of the selection prefill.
+    """
+    dev = _check_device(q_text, key, visual_positions)
+    code = _dtype_code(q_text)
+    if key.dtype != q_text.dtype:
+        raise TypeError("q_text and key must share a dtype")
+    if q_text.dim() != 4 or q_text.shape[0] != 1:
+        raise ValueError(f"q_text must be [1, n_q, T, D], got {tuple(q_text.shape)}")
+    _check_rows_contiguous("q_text", q_text)
+    _check_cache_view("key", key)
+    if visual_positions.dtype != torch.int32 or visual_positions.dim() != 1:
+        raise TypeError("visual_positions must be a 1-D int32 tensor")
+    visual_positions = visual_positions.contiguous()
+    _, n_q, text_len, d = q_text.shape
+    n_kv = key.shape[1]
+    prompt_len = int(text_start) + text_len
+    if key.shape[2] < prompt_len:
+        raise ValueError(f"key holds {key.shape[2]} rows, prompt needs {prompt_len}")
+    n_vis = visual_positions.numel()
+    if not (1 <= k <= n_vis):
+        raise ValueError(f"k={k} must be in [1, n_visual={n_vis}]")
+    lib = _lib.load_library()
+    ws_bytes = lib.std_select_topk_workspace_bytes(n_q, n_kv, text_len, prompt_len, n_vis, d)
+    if ws_bytes == 0:
+        raise ValueError("unsupported selection shape")
+    ws_ptr, ws = _workspace(ws_bytes, dev)
+    topk = torch.empty(n_kv, k, dtype=torch.int32, device=dev)
+    scores = torch.empty(n_kv, prompt_len, dtype=torch.float64, device=dev) if return_scores else None
+    _lib.call("std_select_topk", q_text.data_ptr(), key.data_ptr(), n_q, n_kv, text_len, prompt_len, int(text_start),
+              d, key.stride(1), code, visual_positions.data_ptr(), n_vis, int(k), topk.data_ptr(),
+              scores.data_ptr() if scores is not None else None, ws_ptr, ws_bytes, _stream(dev))
+    return (topk, scores) if return_scores else topk
+
+
+def build_compact_index(non_visual: torch.Tensor, topk: torch.Tensor) -> torch.Tensor:
+    """Sorted union of the non-visual positions and each head's top-k
+    (std_qwen25vl.py:286-291). Returns int32 [n_kv, n_nonvisual + k]."""
+    dev = _check_device(topk, non_visual) if non_visual.numel() else _check_device(topk)
+    if topk.dtype != torch.int32 or topk.dim() != 2:
+        raise TypeError("topk must be int32 [n_kv, k]")
+    if non_visual.dtype != torch.int32 or non_visual.dim() != 1:
+        raise TypeError("non_visual must be 1-D int32")
+    topk = topk.contiguous()
+    non_visual = non_visual.contiguous()
+    n_kv, k = topk.shape
+    n_nv = non_visual.numel()
+    idx = torch.empty(n_kv, n_nv + k, dtype=torch.int32, device=dev)
+    _lib.call("std_build_compact_index", non_visual.data_ptr() if n_nv else None, n_nv, topk.data_ptr(), k, n_kv,
+              idx.data_ptr(), _stream(dev))
+    return idx
+
+
+def compact_kv(dense_k: torch.Tensor, dense_v: torch.Tensor, sparse_k: torch.Tensor, sparse_v: torch.Tensor,
+               index: torch.Tensor) -> None:
+    """sparse[:, g, s] = dense[:, g, index[g, s]] for one layer, K and V.
+
+    dense_*, sparse_* are full cache buffers [1, n_kv, capacity, D]; index is
+    int32 [n_kv, compact_len] (std_qwen25vl.py:265-298 without the
+    full-prompt copy)."""
+    dev = _check_device(dense_k, dense_v, sparse_k, sparse_v, index)
+    code = _dtype_code(dense_k)
+    for name, t in (("dense_k", dense_k), ("dense_v", dense_v), ("sparse_k", sparse_k), ("sparse_v", sparse_v)):
+        _check_cache_view(name, t)
+        if t.dtype != dense_k.dtype:
+            raise TypeError("all caches must share a dtype")
+    if dense_v.stride(1) != dense_k.stride(1) or sparse_v.stride(1) != sparse_k.stride(1):
+        raise ValueError("K and V caches must share a head stride")
+    if index.dtype != torch.int32 or index.dim() != 2 or index.shape[0] != dense_k.shape[1]:
+        raise TypeError("index must be int32 [n_kv, compact_len]")
+    index = index.contiguous()
+    n_kv, compact_len = index.shape
+    if compact_len > sparse_k.shape[2]:
+        raise ValueError(f"compact_len {compact_len} exceeds sparse capacity {sparse_k.shape[2]}")
+    _lib.call("std_compact_kv", dense_k.data_ptr(), dense_v.data_ptr(), sparse_k.data_ptr(), sparse_v.data_ptr(),
+              index.data_ptr(), n_kv, compact_len, HEAD_DIM, dense_k.stride(1), dense_k.shape[2],
+              sparse_k.stride(1), sparse_k.shape[2], code, _stream(dev))
+
+
+def kv_append(cache_k: torch.Tensor, cache_v: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor,
+              length: torch.Tensor) -> None:
+    """Write new rows at positions length[0] + r (KVCache.cat, kv_cache.py:54-69,
+    with the length on the device). cache_* [1, n_kv, capacity, D] buffers;
+    new_* [1, n_kv, rows, D] with contiguous rows (any head/row stride)."""
+    dev = _check_device(cache_k, cache_v, new_k, new_v, length)
+    code = _dtype_code(cache_k)
+    _check_cache_view("cache_k", cache_k)
+    _check_cache_view("cache_v", cache_v)
+    if cache_v.stride(1) != cache_k.stride(1):
+        raise ValueError("K and V caches must share a head stride")
+    for name, t in (("new_k", new_k), ("new_v", new_v)):
+        if t.dim() != 4 or t.shape[0] != 1 or t.shape[1] != cache_k.shape[1] or t.shape[3] != HEAD_DIM:
+            raise ValueError(f"{name} must be [1, n_kv, rows, D], got {tuple(t.shape)}")
+        if t.stride(3) != 1 or t.dtype != cache_k.dtype:
+            raise ValueError(f"{name} must have contiguous head_dim and the cache dtype")
+    if new_v.stride() != new_k.stride() or new_v.shape != new_k.shape:
+        raise ValueError("new_k and new_v must share shape and strides")
+    if length.dtype != torch.int32:
+        raise TypeError("length must be a device int32 tensor")
+    rows = new_k.shape[2]
+    _lib.call("std_kv_append", cache_k.data_ptr(), cache_v.data_ptr(), new_k.data_ptr(), new_v.data_ptr(),
+              cache_k.shape[1], rows, HEAD_DIM, cache_k.stride(1), new_k.stride(1), new_k.stride(2),
+              cache_k.shape[2], length.data_ptr(), code, _stream(dev))
+
+
+def len_add(length: torch.Tensor, delta: int) -> None:
+    """length[:] += delta on the device."""
+    dev = _check_device(length)
+    if length.dtype != torch.int32 or not length.is_contiguous():
+        raise TypeError("length must be a contiguous int32 tensor")
+    _lib.call("std_len_add", length.data_ptr(), length.numel(), int(delta), _stream(dev))
+
+
+def greedy_accept(logits: torch.Tensor, draft: torch.Tensor, has_pending: bool,
+                  dense_next: Optional[torch.Tensor] = None,
+                  rollback_lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Greedy verification of a draft (std_qwen25vl.py:806-815 and rollback
+    :923-928; pure form greedy_prefix, hsd_spike.py:30-43).
+
+    logits [Q, V] (or [1, Q, V]) with Q = len(draft) + has_pending; draft int32
+    [n_draft]; dense_next int32 [1] when has_pending is False. Returns int32
+    [2 + n_draft + 1] = [accept_len, bonus, predictions...] on the device and
+    decreases every entry of rollback_lengths by n_draft - accept_len.
+    """
+    if logits.dim() == 3:
+        if logits.shape[0] != 1:
+            raise ValueError("batch size 1 only")
+        logits = logits[0]
+    dev = _check_device(logits, draft)
+    code = _dtype_code(logits)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [Q, vocab] with contiguous rows")
+    if draft.dtype != torch.int32 or draft.dim() != 1:
+        raise TypeError("draft must be 1-D int32")
+    draft = draft.contiguous()
+    q_rows, vocab = logits.shape
+    n_draft = draft.numel()
+    if q_rows != n_draft + (1 if has_pending else 0):
+        raise ValueError(f"logits rows {q_rows} != n_draft {n_draft} + has_pending {int(has_pending)}")
+    if not has_pending:
+        if dense_next is None or dense_next.dtype != torch.int32:
+            raise TypeError("dense_next (int32) is required without a pending token")
+        _check_device(logits, dense_next)
+    n_lens = 0
+    if rollback_lengths is not None:
+        if rollback_lengths.dtype != torch.int32 or not rollback_lengths.is_contiguous():
+            raise TypeError("rollback_lengths must be contiguous int32")
+        _check_device(logits, rollback_lengths)
+        n_lens = rollback_lengths.numel()
+    out = torch.empty(2 + n_draft + 1, dtype=torch.int32, device=dev)
+    lib = _lib.load_library()
+    ws_bytes = lib.std_greedy_accept_workspace_bytes(q_rows, vocab)
+    ws_ptr, ws = _workspace(ws_bytes, dev)
+    _lib.call("std_greedy_accept", logits.data_ptr(), logits.stride(0), q_rows, vocab, code, draft.data_ptr(),
+              n_draft, 1 if has_pending else 0, dense_next.data_ptr() if dense_next is not None else None,
+              out.data_ptr(), rollback_lengths.data_ptr() if n_lens else None, n_lens, ws_ptr, ws_bytes, _stream(dev))
+    return out

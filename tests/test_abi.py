@@ -1,0 +1,120 @@
+"""The C-ABI library loads, exports every function include/std_hip.h declares,
+and rejects bad arguments on the host before any device work (no GPU needed:
+only validation paths and host-only queries are called here). Every call in
+this file must fail validation: the pointers are placeholders, never memory."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from std_amd import _lib, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "std_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(std_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declarations_match_binding_table():
+    assert _declared() == _lib.exported_symbols()
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load_library()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.library_path())], capture_output=True, text=True)
+    exported = set(re.findall(r" T (std_\w+)", out.stdout))
+    assert set(_declared()) <= exported
+
+
+def test_status_strings_and_version():
+    lib = _lib.load_library()
+    assert lib.std_version() == 0x000100
+    assert lib.std_status_string(0) == b"success"
+    for code in range(-6, 0):
+        assert b"unknown" not in lib.std_status_string(code)
+
+
+def test_workspace_queries():
+    lib = _lib.load_library()
+    assert lib.std_gqa_decode_workspace_bytes(28, 4, 1024, 128) > 0
+    assert lib.std_gqa_decode_workspace_bytes(28, 4, 64, 128) == 0        # one tile: no split, no workspace
+    assert lib.std_verify_attn_workspace_bytes(28, 4, 10, 131082, 128) > 0
+    assert lib.std_verify_attn_workspace_bytes(28, 4, 10, 131082, 64) == 0   # unsupported head dim
+    assert lib.std_select_topk_workspace_bytes(28, 4, 128, 4096, 3968, 128) > 0
+    assert lib.std_greedy_accept_workspace_bytes(10, 152064) >= 10 * 75 * 8
+
+
+NULL = None
+
+
+@pytest.mark.parametrize("args,expected", [
+    ((NULL, NULL, NULL, NULL, 28, 4, 1024, 128, 0, 0, 1.0, 1, NULL, 0, NULL), -1),
+    ((16, 16, 16, 16, 28, 4, 1024, 64, 1024 * 128, 1024 * 128, 1.0, 1, NULL, 0, NULL), -3),   # head_dim
+    ((16, 16, 16, 16, 28, 5, 1024, 128, 1024 * 128, 1024 * 128, 1.0, 1, NULL, 0, NULL), -3),  # 28 % 5
+    ((16, 16, 16, 16, 28, 4, 1024, 128, 1024 * 128, 1024 * 128, 1.0, 7, NULL, 0, NULL), -2),  # dtype
+    ((16, 16, 16, 16, 28, 4, 1024, 128, 100, 1024 * 128, 1.0, 1, NULL, 0, NULL), -3),        # head stride < rows
+    ((8, 16, 16, 16, 28, 4, 1024, 128, 1024 * 128, 1024 * 128, 1.0, 1, 16, 1 << 30, NULL), -5),  # misaligned q
+    ((16, 16, 16, 16, 28, 4, 1024, 128, 1024 * 128, 1024 * 128, 1.0, 1, NULL, 0, NULL), -4),  # no workspace
+])
+def test_decode_validation(args, expected):
+    assert _lib.load_library().std_gqa_decode(*args) == expected
+
+
+def test_verify_validation():
+    lib = _lib.load_library()
+    hs = 4106 * 128
+    assert lib.std_verify_attn(16, 16, 16, 16, 28, 4, 20, 4106, 128, hs, hs, 1.0, 1, NULL, 0, NULL) == -3  # 7*20 rows
+    assert lib.std_verify_attn(16, 16, 16, 16, 28, 4, 11, 10, 128, hs, hs, 1.0, 1, NULL, 0, NULL) == -3   # q > kv
+
+
+def test_select_validation():
+    lib = _lib.load_library()
+    hs = 4096 * 128
+    # k > n_visual, and prompt_len != text_start + text_len
+    assert lib.std_select_topk(16, 16, 28, 4, 128, 4096, 3968, 128, hs, 1, 16, 3968, 4000, 16, NULL, 16, 1 << 30,
+                               NULL) == -3
+    assert lib.std_select_topk(16, 16, 28, 4, 128, 4096, 3900, 128, hs, 1, 16, 3968, 896, 16, NULL, 16, 1 << 30,
+                               NULL) == -3
+    assert lib.std_select_topk(16, 16, 28, 4, 128, 4096, 3968, 128, hs, 1, 16, 3968, 896, 16, NULL, 16, 10,
+                               NULL) == -4
+
+
+def test_accept_and_append_validation():
+    lib = _lib.load_library()
+    # q_rows must be n_draft + has_pending
+    assert lib.std_greedy_accept(16, 152064, 9, 152064, 1, 16, 9, 1, NULL, 16, NULL, 0, 16, 1 << 20, NULL) == -3
+    # dense_next is required without a pending token
+    assert lib.std_greedy_accept(16, 152064, 9, 152064, 1, 16, 9, 0, NULL, 16, NULL, 0, 16, 1 << 20, NULL) == -1
+    assert lib.std_kv_append(16, 16, 16, 16, 4, 1, 128, 128 * 100, 128, 512, 100, NULL, 1, NULL) == -1
+    assert lib.std_kv_append(16, 16, 16, 16, 4, 1, 128, 128 * 100, 128, 3, 100, 16, 1, NULL) == -5  # row stride
+    assert lib.std_compact_kv(16, 16, 16, 16, 16, 4, 2000, 128, 128 * 4096, 4096, 128 * 1024, 1024, 1, NULL) == -6
+
+
+def test_python_shim_rejects_cpu_tensors_before_the_library():
+    q = torch.zeros(1, 28, 1, 128)
+    k = torch.zeros(1, 4, 64, 128)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ops.gqa_decode(q, k, k)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ops.verify_attention(torch.zeros(1, 28, 10, 128), k, k)
+
+
+def test_python_shim_shape_errors():
+    # shape checks run before the device check only for q_len, mirroring the
+    # reference's q_len assertion (triton_attention.py:89)
+    with pytest.raises(ValueError, match="q_len=1"):
+        ops.gqa_decode(torch.zeros(1, 28, 2, 128), torch.zeros(1, 4, 8, 128), torch.zeros(1, 4, 8, 128))
+
+
+def test_status_error_is_runtime_error():
+    with pytest.raises(RuntimeError, match="STD_E_NULL"):
+        _lib.check("std_gqa_decode", -1)

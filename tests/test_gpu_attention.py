@@ -1,0 +1,145 @@
+"""GPU parity of the draft/AR decode attention and the dense verify attention
+against the oracle (math SDPA in fp64 on the same inputs)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as ref
+from std_amd import ops
+from std_amd.workloads import WORKLOADS, make_layer
+from tests.gpu_helpers import announce, assert_close, cache_buffer, dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode_case(wname, layer, kv_len, capacity_extra=37):
+    w = WORKLOADS[wname]
+    x = make_layer(w, layer, prompt_len=max(kv_len, w.text_len + 1) if kv_len > w.prompt_len else None)
+    k, v = x["k"][:, :, :kv_len], x["v"][:, :, :kv_len]
+    if k.shape[2] < kv_len:  # longer than the workload prompt: extend with more seeded rows
+        gen = torch.Generator().manual_seed(99)
+        extra = kv_len - k.shape[2]
+        k = torch.cat([k, torch.randn(1, w.n_kv, extra, w.head_dim, generator=gen).to(w.dtype)], 2)
+        v = torch.cat([v, torch.randn(1, w.n_kv, extra, w.head_dim, generator=gen).to(w.dtype)], 2)
+    return w, x["q_draft"], k, v
+
+
+@pytest.mark.parametrize("wname,kv_len", [
+    ("c1", 1024), ("c1", 1), ("c1", 63), ("c1", 64), ("c1", 65), ("c1", 4096),
+    ("c2", 1024), ("c2", 1033), ("c2", 2600), ("c2", 16384),
+    ("c3", 4096),
+])
+def test_decode_matches_oracle(wname, kv_len):
+    w, q, k, v = _decode_case(wname, 0, kv_len)
+    announce(f"decode {wname} kv_len={kv_len} dtype={w.dtype}")
+    kb = cache_buffer(k, kv_len + 37)
+    vb = cache_buffer(v, kv_len + 37)
+    out = ops.gqa_decode(q.to(dev()), kb[:, :, :kv_len], vb[:, :, :kv_len])
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and out.dtype == q.dtype
+    assert_close(out, ref.gqa_sdpa(q, k, v), w.dtype)
+
+
+def test_decode_dense_ar_131072():
+    """D2: the same kernel over a full 128k dense cache (split-K + merge)."""
+    w = WORKLOADS["c4"]
+    kv_len = 131072
+    announce("decode c4 dense AR kv_len=131072 bf16")
+    x = make_layer(w, 3)
+    kb = cache_buffer(x["k"], kv_len + 16)
+    vb = cache_buffer(x["v"], kv_len + 16)
+    out = ops.gqa_decode(x["q_draft"].to(dev()), kb[:, :, :kv_len], vb[:, :, :kv_len])
+    torch.cuda.synchronize()
+    assert_close(out, ref.gqa_sdpa(x["q_draft"], x["k"], x["v"]), w.dtype)
+
+
+def test_fused_gqa_attention_dropin_contiguous():
+    """Reference self-test shape (triton_attention.py:117-132): 28/4 heads, S=2600."""
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 28, 1, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(1, 4, 2600, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(1, 4, 2600, 128, generator=gen).to(torch.bfloat16)
+    announce("fused_gqa_attention drop-in 28/4/2600 bf16 contiguous")
+    out = ops.fused_gqa_attention(q.to(dev()), k.to(dev()), v.to(dev()))
+    torch.cuda.synchronize()
+    assert_close(out, ref.gqa_sdpa(q, k, v), torch.bfloat16)
+
+
+@pytest.mark.parametrize("wname,q_len", [("c1", 10), ("c1", 9), ("c2", 10), ("c2", 1), ("c2", 16), ("c2", 3)])
+def test_verify_matches_oracle(wname, q_len):
+    w = WORKLOADS[wname]
+    x = make_layer(w, 1)
+    P = w.prompt_len
+    new_k = x["new_k"][:, :, :q_len] if q_len <= w.verify_rows else torch.cat([x["new_k"]] * 2, 2)[:, :, :q_len]
+    new_v = x["new_v"][:, :, :q_len] if q_len <= w.verify_rows else torch.cat([x["new_v"]] * 2, 2)[:, :, :q_len]
+    q = x["q_verify"][:, :, :q_len] if q_len <= w.verify_rows else torch.cat([x["q_verify"]] * 2, 2)[:, :, :q_len]
+    k = torch.cat([x["k"], new_k], 2)
+    v = torch.cat([x["v"], new_v], 2)
+    kv_len = P + q_len
+    announce(f"verify {wname} q_len={q_len} kv_len={kv_len} dtype={w.dtype}")
+    kb = cache_buffer(k, kv_len + 64)
+    vb = cache_buffer(v, kv_len + 64)
+    out = ops.verify_attention(q.contiguous().to(dev()), kb[:, :, :kv_len], vb[:, :, :kv_len])
+    torch.cuda.synchronize()
+    assert_close(out, ref.verify_attention(q, k, v), w.dtype)
+
+
+def test_verify_131082_one_layer():
+    """V unit at 128k: Q=10 over 131072 + 10 keys."""
+    w = WORKLOADS["c4"]
+    x = make_layer(w, 0)
+    k = torch.cat([x["k"], x["new_k"]], 2)
+    v = torch.cat([x["v"], x["new_v"]], 2)
+    kv_len = k.shape[2]
+    announce(f"verify c4 q_len=10 kv_len={kv_len} bf16")
+    kb = cache_buffer(k, kv_len + 118)
+    vb = cache_buffer(v, kv_len + 118)
+    out = ops.verify_attention(x["q_verify"].to(dev()), kb[:, :, :kv_len], vb[:, :, :kv_len])
+    torch.cuda.synchronize()
+    assert_close(out, ref.verify_attention(x["q_verify"], k, v), w.dtype)
+
+
+def test_verify_batched_equals_sequential_decode():
+    """Row i of verify == decode of query i over keys [0, kv_len - Q + i]
+    (the batched == sequential property of the reference's verify spike)."""
+    gen = torch.Generator().manual_seed(7)
+    Q, kv_len = 10, 700
+    q = torch.randn(1, 28, Q, 128, generator=gen)
+    k = torch.randn(1, 4, kv_len, 128, generator=gen)
+    v = torch.randn(1, 4, kv_len, 128, generator=gen)
+    announce("verify batched == sequential fp32 kv_len=700")
+    kb, vb = cache_buffer(k, kv_len), cache_buffer(v, kv_len)
+    batched = ops.verify_attention(q.to(dev()), kb, vb)
+    rows = []
+    for i in range(Q):
+        n = kv_len - Q + i + 1
+        rows.append(ops.gqa_decode(q[:, :, i:i + 1].contiguous().to(dev()), kb[:, :, :n], vb[:, :, :n]))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(batched.cpu().numpy(), torch.cat(rows, 2).cpu().numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_verify_no_future_leakage():
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn(1, 28, 2, 128, generator=gen)
+    k = torch.randn(1, 4, 5, 128, generator=gen)
+    v = torch.randn(1, 4, 5, 128, generator=gen)
+    announce("verify no future leakage fp32")
+    base = ops.verify_attention(q.to(dev()), k.to(dev()), v.to(dev())).cpu()
+    changed = v.clone()
+    changed[:, :, -1] += 10000
+    altered = ops.verify_attention(q.to(dev()), k.to(dev()), changed.to(dev())).cpu()
+    torch.cuda.synchronize()
+    assert torch.allclose(base[:, :, :1], altered[:, :, :1], atol=1e-5, rtol=1e-5)
+    assert not torch.allclose(base[:, :, 1:], altered[:, :, 1:], atol=1e-5, rtol=1e-5)
+
+
+def test_decode_is_deterministic():
+    w = WORKLOADS["c2"]
+    x = make_layer(w, 5)
+    kb, vb = x["k"].to(dev()), x["v"].to(dev())
+    q = x["q_draft"].to(dev())
+    announce("decode determinism c2 kv_len=16384 x5")
+    outs = [ops.gqa_decode(q, kb, vb) for _ in range(5)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
