@@ -1,0 +1,335 @@
+"""Benchmark of the STD decode hot path on one MI355X.
+
+One step = one speculative round of the attention hot path at the 128k-context
+workload (28 layers, 28 query / 4 KV heads, head_dim 128, context 131072 =
+130944 visual + 128 text, K+text = 1024, gamma = 9), in the reference's order
+(src/std_repro/std_qwen25vl.py:766-939):
+  draft   gamma sparse steps; each appends one K/V row per layer to the compact
+          cache (device length) and runs GQA decode attention over it
+  verify  per layer: append gamma+1 rows to the dense cache, offset-causal
+          verify attention over all 131072 + 10 keys
+  accept  argmax over [gamma+1, 152064] logits, greedy prefix, bonus, device
+          rollback of both cache lengths, one 8-byte readback
+Inputs are synthetic, generated on the device and resident in HBM before the
+timed region; the compact cache comes from the real selection + compaction.
+
+Prints one JSON line (value = draft tokens/s of the attention hot path).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "draft/verify attn µs per step + HBM GB/s (% peak) at 128k ctx; draft tokens/sec"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c4", choices=["c2", "c3", "c4"])
+    ap.add_argument("--layers", type=int, default=None, help="override the layer count (default: workload's)")
+    ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cold-iters", type=int, default=10)
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def draft_bytes(n_q, n_kv, s, d, es):
+    return 2 * n_kv * s * d * es + 2 * n_q * d * es
+
+
+def verify_bytes(n_q, n_kv, q, kv, d, es):
+    return 2 * n_kv * kv * d * es + 2 * n_q * q * d * es
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
+                                   "design note, not a measured configuration)"}))
+        sys.exit(2)
+    import torch
+
+    from std_amd import ops
+    from std_amd.workloads import WORKLOADS, non_visual_positions, visual_positions
+
+    w = WORKLOADS[args.workload]
+    L = args.layers or w.n_layers
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    D, Hq, Hkv, T, P, G = w.head_dim, w.n_q, w.n_kv, w.text_len, w.prompt_len, w.gamma
+    Q = G + 1
+    es = 2
+    dense_cap = P + 64
+    sparse_cap = w.compact_len + 64
+    gen = torch.Generator(device=dev).manual_seed(w.seed_base)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32).to(w.dtype)
+
+    # ---- resident inputs (device-generated, workload recipe) ----
+    dense_k = torch.empty(L, 1, Hkv, dense_cap, D, dtype=w.dtype, device=dev)
+    dense_v = torch.empty_like(dense_k)
+    for l in range(L):
+        k = torch.randn(1, Hkv, P, D, generator=gen, device=dev)
+        if w.keys == "lognormal":
+            norms = math.sqrt(D) * torch.exp(0.5 * torch.randn(1, Hkv, P, 1, generator=gen, device=dev))
+            k = k / k.norm(dim=-1, keepdim=True) * norms
+        dense_k[l, :, :, :P] = k.to(w.dtype)
+        dense_v[l, :, :, :P] = randn(1, Hkv, P, D)
+    q_text = randn(L, 1, Hq, T, D)
+    q_draft = randn(L, 1, Hq, 1, D)
+    new_k_draft = randn(L, 1, Hkv, 1, D)
+    new_v_draft = randn(L, 1, Hkv, 1, D)
+    q_verify = randn(L, 1, Hq, Q, D)
+    new_k_verify = randn(L, 1, Hkv, Q, D)
+    new_v_verify = randn(L, 1, Hkv, Q, D)
+    logits = randn(Q, w.vocab)
+    preds = torch.argmax(logits.float(), dim=-1).to(torch.int32)
+    draft = preds[:G].clone()
+    draft[6] = (draft[6] + 1) % w.vocab          # accept 6 of 9: a mid-length round
+    draft_out = torch.empty(L, 1, Hq, 1, D, dtype=w.dtype, device=dev)
+    verify_out = torch.empty(L, 1, Hq, Q, D, dtype=w.dtype, device=dev)
+
+    log(f"inputs resident: {L} layers, dense cache {tuple(dense_k.shape)}")
+    # ---- selection + compaction (once per prompt) -> compact sparse cache ----
+    sparse_k = torch.empty(L, 1, Hkv, sparse_cap, D, dtype=w.dtype, device=dev)
+    sparse_v = torch.empty_like(sparse_k)
+    vis = visual_positions(w, "cuda")
+    nonvis = non_visual_positions(w, "cuda")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for l in range(L):
+        topk = ops.select_topk(q_text[l], dense_k[l, :, :, :P], P - T, vis, w.k)
+        idx = ops.build_compact_index(nonvis, topk)
+        ops.compact_kv(dense_k[l], dense_v[l], sparse_k[l], sparse_v[l], idx)
+    torch.cuda.synchronize()
+    select_ms_first = (time.perf_counter() - t0) * 1e3
+    t0 = time.perf_counter()
+    for l in range(L):
+        topk = ops.select_topk(q_text[l], dense_k[l, :, :, :P], P - T, vis, w.k)
+        idx = ops.build_compact_index(nonvis, topk)
+        ops.compact_kv(dense_k[l], dense_v[l], sparse_k[l], sparse_v[l], idx)
+    torch.cuda.synchronize()
+    select_ms = (time.perf_counter() - t0) * 1e3
+
+    S0 = w.compact_len
+    lengths0 = torch.tensor([P, S0], dtype=torch.int32, device=dev)     # [dense_len, sparse_len]
+    lengths = lengths0.clone()
+    dense_len, sparse_len = lengths[0:1], lengths[1:2]
+    stream = torch.cuda.current_stream()
+
+    def draft_phase(ev=None):
+        for t in range(G):
+            S = S0 + t + 1
+            for l in range(L):
+                ops.kv_append(sparse_k[l], sparse_v[l], new_k_draft[l], new_v_draft[l], sparse_len)
+                if ev is not None:
+                    ev[0].append(torch.cuda.Event(enable_timing=True))
+                    ev[0][-1].record(stream)
+                ops.gqa_decode(q_draft[l], sparse_k[l][:, :, :S], sparse_v[l][:, :, :S], out=draft_out[l])
+                if ev is not None:
+                    ev[1].append(torch.cuda.Event(enable_timing=True))
+                    ev[1][-1].record(stream)
+            ops.len_add(sparse_len, 1)
+
+    def verify_phase(ev=None):
+        kv = P + Q
+        for l in range(L):
+            ops.kv_append(dense_k[l], dense_v[l], new_k_verify[l], new_v_verify[l], dense_len)
+            if ev is not None:
+                ev[0].append(torch.cuda.Event(enable_timing=True))
+                ev[0][-1].record(stream)
+            ops.verify_attention(q_verify[l], dense_k[l][:, :, :kv], dense_v[l][:, :, :kv], out=verify_out[l])
+            if ev is not None:
+                ev[1].append(torch.cuda.Event(enable_timing=True))
+                ev[1][-1].record(stream)
+        ops.len_add(dense_len, Q)
+
+    def step(dev_ev=None, ver_ev=None):
+        draft_phase(dev_ev)
+        verify_phase(ver_ev)
+        res = ops.greedy_accept(logits, draft, True, rollback_lengths=lengths)
+        a = int(res[0].item())                           # the one readback per round
+        lengths.copy_(lengths0)                          # steady state: same shapes every round
+        return a
+
+    log(f"selection+compaction {select_ms:.2f} ms for {L} layers")
+    for _ in range(args.warmup):
+        a = step()
+    torch.cuda.synchronize()
+    assert a == 6, f"acceptance length {a} != 6"
+
+    dev_ev, ver_ev = ([], []), ([], [])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(dev_ev, ver_ev)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+
+    draft_us = [a.elapsed_time(b) * 1e3 for a, b in zip(*dev_ev)]      # per layer-call
+    verify_us = [a.elapsed_time(b) * 1e3 for a, b in zip(*ver_ev)]
+    draft_call_us = statistics.mean(draft_us)
+    verify_call_us = statistics.mean(verify_us)
+    S_mid = S0 + (G + 1) // 2
+    d_bytes = draft_bytes(Hq, Hkv, S_mid, D, es)
+    v_bytes = verify_bytes(Hq, Hkv, Q, P + Q, D, es)
+    verify_gbps = v_bytes / (verify_call_us * 1e-6) / 1e9
+    draft_gbps_warm = d_bytes / (draft_call_us * 1e-6) / 1e9
+
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
+    # ---- cold-cache draft step: flush (write 1 GiB) before each 28-layer step ----
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    cold = []
+    for _ in range(args.cold_iters):
+        flush.fill_(1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for l in range(L):
+            ops.gqa_decode(q_draft[l], sparse_k[l][:, :, :S0], sparse_v[l][:, :, :S0], out=draft_out[l])
+        e1.record(stream)
+        torch.cuda.synchronize()
+        cold.append(e0.elapsed_time(e1) * 1e3)
+    draft_step_cold_us = statistics.median(cold)
+    draft_step_cold_gbps = L * draft_bytes(Hq, Hkv, S0, D, es) / (draft_step_cold_us * 1e-6) / 1e9
+    del flush
+
+    draft_tokens_per_s = G * args.steps / elapsed
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"verify_attn_{w.name}_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(draft_tokens_per_s, 2),
+        "unit": "draft tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (device-generated, seeded; selection + compaction run on it)",
+        "config": {
+            "workload": f"{w.name}: {L}-layer attention stack, {Hq}q/{Hkv}kv heads, d={D}, context {P} "
+                        f"({P - T} visual + {T} text), K+text={w.k_plus_text}, gamma={G}, vocab={w.vocab}",
+            "step": "gamma draft decode steps over the compact cache + dense verify (q=gamma+1) + greedy "
+                    "accept/rollback, all layers",
+            "parallelism": "single GPU",
+        },
+        "draft_attn_us_per_step": round(draft_call_us * L, 2),
+        "draft_attn_us_per_layer": round(draft_call_us, 3),
+        "draft_attn_us_per_step_cold": round(draft_step_cold_us, 2),
+        "draft_hbm_gbps_cold_step": round(draft_step_cold_gbps, 1),
+        "draft_pct_peak_cold_step": round(100 * draft_step_cold_gbps / HBM_PEAK_GBPS, 2),
+        "verify_attn_us_per_step": round(verify_call_us * L, 2),
+        "verify_attn_us_per_layer": round(verify_call_us, 3),
+        "verify_hbm_gbps": round(verify_gbps, 1),
+        "verify_pct_peak": round(100 * verify_gbps / HBM_PEAK_GBPS, 2),
+        "select_compact_ms_all_layers": round(select_ms, 3),
+        "select_compact_ms_first_call": round(select_ms_first, 3),
+        "roofline": {
+            "kernel": "verify attention (attn_split_kernel<bf16,5> + attn_merge_kernel), one layer",
+            "bound": "hbm",
+            "achieved": round(verify_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(verify_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": v_bytes,
+            "avg_launch_us": round(verify_call_us, 3),
+        },
+    }
+    if not args.skip_cpu:
+        log("cpu baseline (oracle) on the host cores")
+        result["cpu_baseline"] = cpu_baseline(w, L)
+    print(json.dumps(result))
+
+
+def cpu_baseline(w, L):
+    """The oracle (fp32 numpy/BLAS restatement of the reference operators) on
+    the host cores, on a bounded sample of the same round: 2 layers of verify
+    attention at the full context, 2 layers x gamma draft decode steps over the
+    compact cache, one accept; scaled to the L-layer round."""
+    import numpy as np
+    import torch
+
+    from oracle import accept as ref_accept
+    from oracle import attention as ref_attn
+    from std_amd.workloads import make_layer, make_logits
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    sample_layers = 6
+    t_verify = t_draft = 0.0
+    for l in range(sample_layers):
+        x = make_layer(w, l)
+        kf = torch.cat([x["k"], x["new_k"]], 2).float().numpy()
+        vf = torch.cat([x["v"], x["new_v"]], 2).float().numpy()
+        qv = x["q_verify"].float().numpy()
+        qd = x["q_draft"].float().numpy()
+        ks, vs = kf[:, :, :w.compact_len], vf[:, :, :w.compact_len]
+        t0 = time.perf_counter()
+        ref_attn.verify_attention(qv, kf, vf, dtype=np.float32)
+        t_verify += time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for _ in range(w.gamma):
+            ref_attn.gqa_sdpa(qd, ks, vs, dtype=np.float32)
+        t_draft += time.perf_counter() - t0
+    logits = make_logits(w, w.gamma + 1, seed=1).float().numpy()
+    t0 = time.perf_counter()
+    preds = ref_accept.verify_predictions(logits, True)
+    ref_accept.greedy_prefix(preds[:w.gamma], preds)
+    t_accept = time.perf_counter() - t0
+    round_s = (t_verify + t_draft) * L / sample_layers + t_accept
+    cpu_name = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(w.gamma / round_s, 3),
+        "unit": "draft tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{sample_layers} of {L} layers (verify q={w.gamma + 1} over {w.prompt_len + w.gamma + 1} keys, "
+                  f"{w.gamma} draft steps over {w.compact_len} keys) + 1 accept over {w.vocab} x {w.gamma + 1}, "
+                  f"fp32 numpy oracle, scaled x{L / sample_layers:g}; host CPU: {cpu_name}",
+        "sample_seconds": round(t_verify + t_draft + t_accept, 2),
+        "verify_ms_per_layer": round(t_verify * 1e3 / sample_layers, 2),
+        "draft_ms_per_layer_step": round(t_draft * 1e3 / (sample_layers * w.gamma), 3),
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -10,9 +10,10 @@
  * Calls are stream-ordered and asynchronous on `stream` (a hipStream_t passed
  * as void*; NULL is the default stream). No call allocates or frees device
  * memory: scratch space is a caller-owned workspace whose size is queried up
- * front with the matching *_workspace_bytes() function. No call synchronizes
- * the device. The library keeps no mutable global state, so distinct streams
- * may be driven from distinct host threads.
+ * front with the matching *_workspace_bytes() function; its contents need no
+ * initialisation, and calls that can run concurrently need distinct
+ * workspaces. No call synchronizes the device. The library keeps no mutable
+ * global state, so distinct streams may be driven from distinct host threads.
  *
  * Layouts (batch size 1, as in the reference):
  *   query     [n_q][q_len][d]         row stride d, head stride q_len*d
@@ -82,7 +83,8 @@ int std_gqa_decode(const void* q, const void* k, const void* v, void* out,
  * caller has already appended. Query row i (0-based) sees keys
  * [0, kv_len - q_len + i], the offset_causal_mask of
  * src/std_repro/sparse_verify_spike.py:24-42. Requires 1 <= q_len,
- * q_len * (n_q/n_kv) <= 128, q_len <= kv_len.
+ * q_len * (n_q/n_kv) <= 96 (gamma + 1 <= 13 at 7 query heads per KV head),
+ * q_len <= kv_len.
  * ------------------------------------------------------------------------ */
 size_t std_verify_attn_workspace_bytes(int n_q, int n_kv, int q_len, int kv_len, int d);
 

@@ -1,22 +1,35 @@
 // GQA attention over a strided KV cache for the STD decode loop.
 //
-// One split-K kernel serves both the sparse draft / dense AR decode
+// One split-K design serves both the sparse draft / dense AR decode
 // (q_len = 1) and the dense verify (q_len = gamma + 1, offset-causal): the
-// n_q/n_kv query heads of a KV head and their q_len positions form R <= 128
+// n_q/n_kv query heads of a KV head and their q_len positions form R <= 96
 // query rows that are carried through the key stream together, so each K/V
 // row is read from HBM exactly once per launch (no repeat_kv, no per-head
 // re-reads).
 //
-// Workgroup = (split of the key range, KV head), 4 wavefronts. K/V tiles of
-// 64 keys are loaded with coalesced 16-byte loads (16 lanes per 256-byte bf16
-// row), staged in LDS with register double buffering, and wave w owns keys
-// [16w, 16w+16) of every tile. Scores are computed transposed, S^T = K Q^T,
-// on 16x16 MFMA tiles, so a lane holds one query row and four keys: the
-// online-softmax row statistics stay in-lane (two cross-lane max steps per
-// tile), and the probabilities are already laid out as the B operand of the
-// O^T += V^T P^T MFMA. The four waves' partial states are merged in LDS; with
-// more than one split per head, (m, l, O) partials go to the workspace and a
-// second kernel merges them in split order (deterministic).
+// Workgroup = (split of the key range, KV head). Four key-waves own keys
+// [16w, 16w+16) of every 64-key tile; for verify-sized row counts a second
+// group of four waves takes the other half of the row tiles, so that each
+// SIMD runs two waves that hide each other's MFMA/LDS latency. Scores are computed transposed,
+// S^T = K Q^T, on 16x16 MFMA tiles, so a lane holds one query row and four
+// keys: the online-softmax row statistics stay in-lane, and the
+// probabilities are already laid out as the B operand of O^T += V^T P^T.
+//
+// bf16 (the production path): K/V tiles stream HBM -> LDS through a 4-stage
+// ring of global_load_lds_dwordx4 (no staging registers, three tiles in
+// flight per workgroup). Rows are 256 bytes with their 16-byte chunks XOR
+// swizzled so that the K operand reads (ds_read_b128, one key row per lane)
+// and the V^T operand reads (ds_read_b64_tr_b16, four keys of one head-dim
+// column per lane) are free of bank conflicts. QK^T uses 16x16x32 bf16 MFMA,
+// PV 16x16x16 bf16 MFMA with fp32 accumulation.
+// fp32: the same algorithm with register-staged LDS tiles and 16x16x4 fp32
+// MFMA (exactness path for fp32 caches).
+//
+// Splits: the key tiles of a head are spread evenly over n_split workgroups;
+// each merges its key-waves in LDS, then writes (m, l, O) partials that a
+// merge kernel combines in split order, so results are deterministic. (A
+// last-arriving-workgroup merge inside the split kernel was measured slower:
+// its device-scope fences write back L2 in every workgroup.)
 #include <climits>
 
 #include "common.h"
@@ -25,63 +38,438 @@ namespace stdhip {
 namespace {
 
 constexpr int D = kHeadDim;
-constexpr int TK = 64;              // keys per LDS tile
+constexpr int TK = 64;              // keys per tile
 constexpr int WAVES = 4;            // wave w owns keys [16w, 16w + 16) of each tile
 constexpr int NTHREADS = 64 * WAVES;
-constexpr int LROW = D + 4;         // LDS row pitch (elements) of staged K/V rows
+constexpr int LROW = D + 4;         // LDS row pitch (elements) of register-staged K/V rows
 constexpr int OROW = D + 4;         // LDS row pitch (floats) of the output merge
-constexpr int kMaxRows = 128;       // R = (n_q / n_kv) * q_len limit (8 row tiles)
-constexpr int kTargetWorkgroups = 512;
+constexpr int OTILE_BYTES = 16 * OROW * 4;   // one 16-row tile of merged O
+constexpr int kMaxRows = 96;        // R = (n_q / n_kv) * q_len limit (6 row tiles)
+constexpr int kMaxSplit = 512;
+constexpr float kRescaleSlack = 8.f; // bf16 path: raise the running max only past this (log2)
 
-// MFMA fragments -------------------------------------------------------------
-// Lane l = 16*lg + ln. A 16x16 fp32 accumulator tile holds C[4*lg + i][ln] in
-// element i. For S^T = K Q^T the M index is the key (16 keys of the wave) and
-// N the query row; for O^T = V^T P^T the M index is the head-dim row and N
-// the query row. The contraction slots of A and B are paired identically, so
-// any d-to-slot assignment is valid as long as A and B use the same one.
-template <typename T> struct Frag;
-
-template <> struct Frag<bf16_t> {
-  // 16x16x16 bf16: each lane supplies 4 contraction elements.
-  struct QFrag { i16x4 c[8]; };   // q[16c + 4lg + j]
-  struct KFrag { i16x4 c[8]; };   // K[key][16c + 4lg + j]
-  struct VFrag { i16x4 t[8]; };   // V[kb + 4lg + j][16t + ln]
-
-  static __device__ __forceinline__ void load_q(QFrag& f, const bf16_t* row, int lg) {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) f.c[c] = *(const i16x4*)(row + 16 * c + 4 * lg);
-  }
-  static __device__ __forceinline__ void zero_q(QFrag& f) {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) f.c[c] = i16x4{0, 0, 0, 0};
-  }
-  static __device__ __forceinline__ void load_k(KFrag& f, const bf16_t* lrow, int lg) {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) f.c[c] = *(const i16x4*)(lrow + 16 * c + 4 * lg);
-  }
-  static __device__ __forceinline__ void load_v(VFrag& f, const bf16_t* vt, int kb, int ln, int lg) {
-    const bf16_t* base = vt + (kb + 4 * lg) * LROW + ln;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      f.t[t] = i16x4{(short)base[16 * t], (short)base[LROW + 16 * t],
-                     (short)base[2 * LROW + 16 * t], (short)base[3 * LROW + 16 * t]};
-    }
-  }
-  static __device__ __forceinline__ f32x4 qk(const KFrag& k, const QFrag& q) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < 8; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(k.c[c], q.c[c], acc, 0, 0, 0);
-    return acc;
-  }
-  static __device__ __forceinline__ void pv(f32x4* acc, const VFrag& v, const float* p) {
-    const i16x4 b = {(short)f32_to_bf16(p[0]), (short)f32_to_bf16(p[1]),
-                     (short)f32_to_bf16(p[2]), (short)f32_to_bf16(p[3])};
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v.t[t], b, acc[t], 0, 0, 0);
-  }
+// ---------------------------------------------------------------------------
+// Split plan and workspace layout (shared by host and device code).
+struct SplitPlan {
+  int ntiles;
+  int n_split;
 };
 
-template <> struct Frag<float> {
+SplitPlan plan_splits(int n_kv, int rows, int kv_len, int dtype) {
+  SplitPlan p;
+  p.ntiles = (kv_len + TK - 1) / TK;
+  const int target_wg = dtype == STD_BF16 ? 256 : 512;   // bf16: one LDS-heavy workgroup per CU
+  int per_head = target_wg / n_kv;
+  if (per_head < 1) per_head = 1;
+  p.n_split = p.ntiles < per_head ? p.ntiles : per_head;
+  (void)rows;
+  return p;
+}
+
+struct WsLayout {
+  size_t o_off, ml_off, total;
+};
+
+WsLayout ws_layout(int n_kv, int rows, const SplitPlan& p) {
+  WsLayout l{0, 0, 0};
+  if (p.n_split <= 1) return l;
+  const size_t n = (size_t)n_kv * p.n_split * rows;
+  l.o_off = 0;
+  l.ml_off = round_up(l.o_off + n * D * sizeof(float), 256);
+  l.total = round_up(l.ml_off + n * sizeof(float2), 256);
+  return l;
+}
+
+__device__ __forceinline__ int split_tile(int split, int ntiles, int n_split) {
+  return (int)((long long)split * ntiles / n_split);
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue shared by both kernels: the key-waves' merged rows are in LDS
+// (So(r) -> row r of O, unnormalised; ml_f[r] = (m, l), log2 domain).
+template <typename T, typename OPtr>
+__device__ void finish_split(OPtr So, const float2* ml_f, T* __restrict__ out, float* __restrict__ ws_o,
+                             float2* __restrict__ ws_ml, int g, int split, int n_split, int q_len, int group,
+                             int nthreads) {
+  const int tid = threadIdx.x;
+  const int R = group * q_len;
+  const long long head_row0 = (long long)g * n_split * R;
+  for (int idx = tid; idx < R * (D / 4); idx += nthreads) {
+    const int r = idx / (D / 4), d4 = idx - r * (D / 4);
+    const f32x4 o = *reinterpret_cast<const f32x4*>(So(r) + 4 * d4);
+    if (n_split == 1) {
+      const float L = ml_f[r].y;
+      const int hl = r / q_len, i = r - hl * q_len;
+      T* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(o[e] / L);
+    } else {
+      const long long row = head_row0 + (long long)split * R + r;
+      *reinterpret_cast<f32x4*>(ws_o + row * D + 4 * d4) = o;
+      if (d4 == 0) ws_ml[row] = ml_f[r];
+    }
+  }
+}
+
+// Standalone merge: grid (R, n_kv), block D. Weights of the n_split partials
+// of one row are computed once in LDS, then every head-dim element sums its
+// column in split order.
+template <typename T>
+__global__ void __launch_bounds__(D)
+attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
+                  int n_split, int q_len, int group) {
+  __shared__ float wts[kMaxSplit];
+  __shared__ float red[D / 64];
+  const int r = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int R = group * q_len;
+  const long long base = (long long)g * n_split * R + r;
+  float m = -1e30f;
+  for (int s = tid; s < n_split; s += D) m = fmaxf(m, ws_ml[base + (long long)s * R].x);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (lane == 0) red[wv] = m;
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int i = 1; i < D / 64; ++i) M = fmaxf(M, red[i]);
+  __syncthreads();
+  float l = 0.f;
+  for (int s = tid; s < n_split; s += D) {
+    const float2 ml = ws_ml[base + (long long)s * R];
+    const float e = fast_exp2(ml.x - M);
+    wts[s] = e;
+    l += ml.y * e;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
+  if (lane == 0) red[wv] = l;
+  __syncthreads();
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) L += red[i];
+  float o = 0.f;
+  const float* col = ws_o + base * D + tid;
+  const long long step = (long long)R * D;
+  int s = 0;
+  for (; s + 4 <= n_split; s += 4) {
+    const float a0 = col[(s + 0) * step], a1 = col[(s + 1) * step];
+    const float a2 = col[(s + 2) * step], a3 = col[(s + 3) * step];
+    o += a0 * wts[s];
+    o += a1 * wts[s + 1];
+    o += a2 * wts[s + 2];
+    o += a3 * wts[s + 3];
+  }
+  for (; s < n_split; ++s) o += col[s * step] * wts[s];
+  const int hl = r / q_len, i = r - hl * q_len;
+  out[((long long)(g * group + hl) * q_len + i) * D + tid] = from_f32<T>(o / L);
+}
+
+// ===========================================================================
+// bf16 kernel: DMA ring + swizzled LDS + MFMA.
+constexpr int NSTAGE = 4;
+constexpr int ROWB = D * 2;               // bytes per bf16 row
+constexpr int TILEB = TK * ROWB;          // 16 KiB of K (or V) per tile
+constexpr int STAGEB = 2 * TILEB;         // K then V
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// 16-byte chunk c of row r lives at chunk c ^ swz(r): sixteen consecutive
+// rows map one logical chunk to sixteen distinct positions (K reads), and
+// four consecutive rows map a chunk pair to eight (V transpose reads).
+__device__ __forceinline__ int swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
+__device__ __forceinline__ int sw_off(int row, int chunk) { return row * ROWB + ((chunk ^ swz(row)) << 4); }
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory
+// operations of this wave are outstanding, leaving the other counters alone.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Wait until the tile `ahead` tiles before the newest issued one has landed
+// (each tile is `per_tile` DMA instructions per wave).
+template <int PER_TILE>
+__device__ __forceinline__ void wait_vm_ahead(int ahead) {
+  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * PER_TILE));
+  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(PER_TILE));
+  else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+}
+
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+
+// NT row tiles of 16 query rows, RG row groups of four key-waves each; a wave
+// carries NTW = ceil(NT / RG) row tiles (padding tiles have zero queries and
+// are never written out).
+template <int NT, int RG>
+struct Bf16Cfg {
+  static constexpr int kWaves = 4 * RG;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int NTW = (NT + RG - 1) / RG;
+  static constexpr int kRowTiles = NTW * RG;            // including padding tiles
+  static constexpr bool kQLds = kRowTiles > 1;
+  static constexpr int kQBytes = kQLds ? kRowTiles * 16 * ROWB : 16;
+  static constexpr int kSegsPerWave = 16 / kWaves;       // 1 KiB K segments (and V) per wave per tile
+  static constexpr int kLoadsPerTile = 2 * kSegsPerWave;
+};
+
+template <int NT, int RG>
+__global__ void __launch_bounds__(256 * RG)
+attn_bf16_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc,
+                 bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
+                 int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
+                 int n_split, int causal_off) {
+  using C = Bf16Cfg<NT, RG>;
+  constexpr int NTW = C::NTW;
+  __shared__ __align__(16) char st0[STAGEB];
+  __shared__ __align__(16) char st1[STAGEB];
+  __shared__ __align__(16) char st2[STAGEB];
+  __shared__ __align__(16) char st3[STAGEB];
+  __shared__ __align__(16) char qs[C::kQBytes];
+  __shared__ float2 ml_w[WAVES * C::kRowTiles * 16];
+  __shared__ float2 ml_f[C::kRowTiles * 16];
+
+  const int g = blockIdx.y, split = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = w & 3;          // key group: keys [16kg, 16kg + 16) of each tile
+  const int rg = w >> 2;         // row group: row tiles [rg*NTW, rg*NTW + NTW)
+  const int ln = lane & 15, lg = lane >> 4;
+  const int R = group * q_len;
+  const int t_begin = split_tile(split, ntiles_total, n_split);
+  const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
+  const int key_begin = t_begin * TK;
+  const int key_end = min(kv_len, key_begin + ntiles * TK);
+  const bf16_t* kh = kc + (long long)g * k_hs;
+  const bf16_t* vh = vc + (long long)g * v_hs;
+
+  int lim[NTW];
+#pragma unroll
+  for (int rt = 0; rt < NTW; ++rt) {
+    const int r = (rg * NTW + rt) * 16 + ln;
+    lim[rt] = r < R ? causal_off + (r % q_len) : INT_MAX;
+  }
+  bf16x8 qreg[4];
+  if constexpr (!C::kQLds) {
+    const int r = ln;
+    if (r < R) {
+      const int hl = r / q_len, i = r - hl * q_len;
+      const bf16_t* row = q + ((long long)(g * group + hl) * q_len + i) * D;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qreg[c] = *reinterpret_cast<const bf16x8*>(row + 32 * c + 8 * lg);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) qreg[c] = bf16x8{};
+    }
+  } else {
+    for (int idx = tid; idx < C::kRowTiles * 16 * 16; idx += C::kThreads) {
+      const int r = idx >> 4, ch = idx & 15;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (r < R) {
+        const int hl = r / q_len, i = r - hl * q_len;
+        val = *reinterpret_cast<const uint4*>(q + ((long long)(g * group + hl) * q_len + i) * D + ch * 8);
+      }
+      *reinterpret_cast<uint4*>(qs + sw_off(r, ch)) = val;
+    }
+    __syncthreads();
+  }
+
+  float m_run[NTW], l_run[NTW];
+  f32x4 acc[NTW][8];
+#pragma unroll
+  for (int rt = 0; rt < NTW; ++rt) {
+    m_run[rt] = -1e30f;
+    l_run[rt] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Each wave DMAs kSegsPerWave 1 KiB segments (4 rows) of K and of V per
+  // tile. Lane l fills row 4*seg + l/16 at physical chunk l%16, i.e. logical
+  // chunk (l%16) ^ swz(row). Rows past the split's last key re-read that key
+  // (their scores are masked), so no read leaves the valid range.
+  auto issue = [&](int tt, char* stage) {
+    const int key0 = key_begin + tt * TK;
+#pragma unroll
+    for (int j = 0; j < C::kSegsPerWave; ++j) {
+      const int seg = w * C::kSegsPerWave + j;
+      const int r = seg * 4 + (lane >> 4);
+      const int lc = (lane & 15) ^ swz(r);
+      const int key = min(key0 + r, key_end - 1);
+      const long long off = (long long)key * D + lc * 8;
+      __builtin_amdgcn_global_load_lds(kh + off, stage + seg * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vh + off, stage + TILEB + seg * 1024, 16, 0, 0);
+    }
+  };
+
+  auto compute = [&](int tt, const char* stage) {
+    const char* Ks = stage;
+    const char* Vs = stage + TILEB;
+    const int tile_base = key_begin + tt * TK;
+    const int kb = kg * 16;
+    const int rk = kb + ln;
+    bf16x8 kf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kf[c] = *reinterpret_cast<const bf16x8*>(Ks + sw_off(rk, 4 * c + lg));
+    // V^T operand of d-tile t: lane (ln, lg) gets V[kb + 4lg + j][16t + ln], j < 4
+    const int rv = kb + 4 * lg + (ln >> 2);
+    i16x4 vf[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const char* p = Vs + sw_off(rv, 2 * t + ((ln >> 1) & 1)) + ((ln & 1) << 3);
+      vf[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+    }
+    // S^T for every row tile of the wave, the accumulation chains interleaved
+    f32x4 s[NTW];
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt) s[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int rt = 0; rt < NTW; ++rt) {
+        bf16x8 b;
+        if constexpr (C::kQLds) b = *reinterpret_cast<const bf16x8*>(qs + sw_off((rg * NTW + rt) * 16 + ln, 4 * c + lg));
+        else b = qreg[c];
+        s[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[c], b, s[rt], 0, 0, 0);
+      }
+    }
+    const bool need_mask = (tile_base + TK > key_end) || (tile_base + TK - 1 > causal_off);
+    const int key0 = tile_base + kb + 4 * lg;
+    float mt[NTW];
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[rt][i] *= scale_log2;
+        if (need_mask) {
+          const int key = key0 + i;
+          if (key >= key_end || key > lim[rt]) s[rt][i] = -INFINITY;
+        }
+      }
+      mt[rt] = xor32_max(xor16_max(fmaxf(fmaxf(s[rt][0], s[rt][1]), fmaxf(s[rt][2], s[rt][3]))));
+    }
+    // The running max is raised only when a score exceeds it by more than
+    // kRescaleSlack (log2 units): probabilities stay <= 2^kRescaleSlack and the
+    // accumulators are rescaled rarely (one wave-uniform branch per tile).
+    bool rise = false;
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt) rise |= mt[rt] > m_run[rt] + kRescaleSlack;
+    if (__ballot(rise)) {
+#pragma unroll
+      for (int rt = 0; rt < NTW; ++rt) {
+        const float m_new = mt[rt] > m_run[rt] + kRescaleSlack ? mt[rt] : m_run[rt];
+        const float alpha = fast_exp2(m_run[rt] - m_new);
+        l_run[rt] *= alpha;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[rt][d] *= alpha;
+        m_run[rt] = m_new;
+      }
+    }
+    i16x4 pb[NTW];
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt) {
+      f32x4 p;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[rt][i] - m_run[rt]);
+      l_run[rt] += (p[0] + p[1]) + (p[2] + p[3]);
+      pb[rt] = __builtin_bit_cast(i16x4, __builtin_convertvector(p, bf16x4));
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int rt = 0; rt < NTW; ++rt)
+        acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[t], pb[rt], acc[rt][t], 0, 0, 0);
+  };
+
+  // Tile tt: wait for its DMA, barrier (every wave is also done reading the
+  // stage of tile tt-1), compute, then refill that stage with tile tt+3. The
+  // refill is issued after the compute's LDS reads so that none of them has
+  // to wait for it.
+  auto step = [&](int tt, const char* cur, char* nxt) {
+    if (tt >= ntiles) return;
+    wait_vm_ahead<C::kLoadsPerTile>(min(ntiles - 1 - tt, 2));
+    __builtin_amdgcn_s_barrier();
+    compute(tt, cur);
+    if (tt + 3 < ntiles) issue(tt + 3, nxt);
+  };
+
+  issue(0, st0);
+  if (ntiles > 1) issue(1, st1);
+  if (ntiles > 2) issue(2, st2);
+  for (int t = 0; t < ntiles; t += NSTAGE) {
+    step(t, st0, st3);
+    step(t + 1, st1, st0);
+    step(t + 2, st2, st1);
+    step(t + 3, st3, st2);
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  __syncthreads();
+
+  // ---- merge the four key-waves of each row group: row tiles 0-2 in st0, 3-5 in st1 ----
+#pragma unroll
+  for (int rt = 0; rt < NTW; ++rt) l_run[rt] = xor32_sum(xor16_sum(l_run[rt]));
+  if (lg == 0) {
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt)
+      ml_w[kg * C::kRowTiles * 16 + (rg * NTW + rt) * 16 + ln] = make_float2(m_run[rt], l_run[rt]);
+  }
+  __syncthreads();
+  float scl[NTW];
+#pragma unroll
+  for (int rt = 0; rt < NTW; ++rt) {
+    const int r = (rg * NTW + rt) * 16 + ln;
+    float M = ml_w[r].x;
+#pragma unroll
+    for (int kk = 1; kk < WAVES; ++kk) M = fmaxf(M, ml_w[kk * C::kRowTiles * 16 + r].x);
+    float L = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < WAVES; ++kk) {
+      const float2 ml = ml_w[kk * C::kRowTiles * 16 + r];
+      L += ml.y * fast_exp2(ml.x - M);
+    }
+    scl[rt] = fast_exp2(m_run[rt] - M);
+    if (kg == 0 && lg == 0) ml_f[r] = make_float2(M, L);
+  }
+  auto orow = [&](int r) -> float* {
+    const int rt = r >> 4;
+    char* base = rt < 3 ? st0 + rt * OTILE_BYTES : st1 + (rt - 3) * OTILE_BYTES;
+    return reinterpret_cast<float*>(base) + (r & 15) * OROW;
+  };
+#pragma unroll
+  for (int kk = 0; kk < WAVES; ++kk) {
+    if (kg == kk) {
+#pragma unroll
+      for (int rt = 0; rt < NTW; ++rt) {
+        float* rowp = orow((rg * NTW + rt) * 16 + ln);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+          f32x4* dst = reinterpret_cast<f32x4*>(rowp + 16 * d + 4 * lg);
+          const f32x4 o = acc[rt][d] * scl[rt];
+          if (kk == 0) *dst = o; else *dst += o;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  finish_split<bf16_t>(orow, ml_f, out, ws_o, ws_ml, g, split, n_split, q_len, group, C::kThreads);
+}
+
+// ===========================================================================
+// fp32 kernel: register-staged double buffer, 16x16x4 fp32 MFMA.
+struct F32Frag {
   // 16x16x4 fp32: each lane supplies 1 contraction element per step.
   struct QFrag { float c[32]; };    // q[4c + lg]
   struct KFrag { float c[32]; };    // K[key][4c + lg]
@@ -120,69 +508,52 @@ template <> struct Frag<float> {
   }
 };
 
-template <typename T, int NT>
-struct SplitSmem {
+template <int NT>
+struct F32Smem {
   static constexpr int kTileElems = TK * LROW;
-  static constexpr int kKVBytes = 2 * 2 * kTileElems * (int)sizeof(T);   // K,V x double buffer
-  // Query rows live in LDS (not registers) once the accumulators of NT row
-  // tiles crowd the register file; bf16 only, fp32 would not fit in LDS.
-  static constexpr bool kQLds = sizeof(T) == 2 && NT > 2;
-  static constexpr int kQBytes = kQLds ? NT * 16 * LROW * (int)sizeof(T) : 0;
-  static constexpr int kOBytes = NT * 16 * OROW * 4;
-  static constexpr int kMLOff = kKVBytes + kQBytes > kOBytes ? kKVBytes + kQBytes : kOBytes;
+  static constexpr int kKVBytes = 2 * 2 * kTileElems * 4;   // K,V x double buffer
+  static constexpr int kOBytes = NT * OTILE_BYTES;
+  static constexpr int kMLOff = kKVBytes > kOBytes ? kKVBytes : kOBytes;
   static constexpr int kBytes = kMLOff + (WAVES + 1) * NT * 16 * 8;
 };
 
-// grid (n_split, n_kv), block NTHREADS.
-template <typename T, int NT>
+template <int NT>
 __global__ void __launch_bounds__(NTHREADS)
-attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
-                  T* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml,
-                  int q_len, int kv_len, int group, long long k_hs, long long v_hs,
-                  float scale_log2, int tiles_per_split, int n_split, int causal_off) {
-  using F = Frag<T>;
-  using S = SplitSmem<T, NT>;
-  constexpr int EPC = 16 / (int)sizeof(T);      // elements per 16-byte chunk
-  constexpr int CPR = D / EPC;                  // chunks per K/V row
+attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+                float* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
+                int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
+                int n_split, int causal_off) {
+  using F = F32Frag;
+  using S = F32Smem<NT>;
+  constexpr int CPR = D / 4;                    // 16-byte chunks per fp32 row
   constexpr int CPT = TK * CPR / NTHREADS;      // chunks per thread per tile
   __shared__ __align__(16) unsigned char smem[S::kBytes];
-  T* Ks = reinterpret_cast<T*>(smem);
-  T* Vs = Ks + 2 * S::kTileElems;
+  float* Ks = reinterpret_cast<float*>(smem);
+  float* Vs = Ks + 2 * S::kTileElems;
 
   const int g = blockIdx.y, split = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
   const int R = group * q_len;
-  const int key_begin = split * tiles_per_split * TK;
-  const int key_end = min(kv_len, key_begin + tiles_per_split * TK);
-  const int ntiles = (key_end - key_begin + TK - 1) / TK;
-  const T* kh = kc + (long long)g * k_hs;
-  const T* vh = vc + (long long)g * v_hs;
+  const int t_begin = split_tile(split, ntiles_total, n_split);
+  const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
+  const int key_begin = t_begin * TK;
+  const int key_end = min(kv_len, key_begin + ntiles * TK);
+  const float* kh = kc + (long long)g * k_hs;
+  const float* vh = vc + (long long)g * v_hs;
 
-  T* Qs = reinterpret_cast<T*>(smem + S::kKVBytes);                // [NT*16][LROW] if kQLds
-  typename F::QFrag qf[S::kQLds ? 1 : NT];
+  typename F::QFrag qf[NT];
   int lim[NT];
 #pragma unroll
   for (int rt = 0; rt < NT; ++rt) {
     const int r = rt * 16 + ln;
-    const int hl = r / q_len, i = r - hl * q_len;
-    lim[rt] = r < R ? causal_off + i : INT_MAX;
-    if constexpr (!S::kQLds) {
-      if (r < R) F::load_q(qf[rt], q + ((long long)(g * group + hl) * q_len + i) * D, lg);
-      else F::zero_q(qf[rt]);
-    }
-  }
-  if constexpr (S::kQLds) {
-    for (int c = tid; c < NT * 16 * CPR; c += NTHREADS) {
-      const int r = c / CPR, col = c - r * CPR;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (r < R) {
-        const int hl = r / q_len, i = r - hl * q_len;
-        val = *reinterpret_cast<const uint4*>(q + ((long long)(g * group + hl) * q_len + i) * D + col * EPC);
-      }
-      uint2* dq = reinterpret_cast<uint2*>(Qs + r * LROW + col * EPC);
-      dq[0] = make_uint2(val.x, val.y);
-      dq[1] = make_uint2(val.z, val.w);
+    if (r < R) {
+      const int hl = r / q_len, i = r - hl * q_len;
+      F::load_q(qf[rt], q + ((long long)(g * group + hl) * q_len + i) * D, lg);
+      lim[rt] = causal_off + i;
+    } else {
+      F::zero_q(qf[rt]);
+      lim[rt] = INT_MAX;
     }
   }
 
@@ -205,8 +576,8 @@ attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* __
       const int row = c / CPR, col = c - row * CPR;
       const int key = base + row;
       if (key < key_end) {
-        kreg[j] = *reinterpret_cast<const uint4*>(kh + (long long)key * D + col * EPC);
-        vreg[j] = *reinterpret_cast<const uint4*>(vh + (long long)key * D + col * EPC);
+        kreg[j] = *reinterpret_cast<const uint4*>(kh + (long long)key * D + col * 4);
+        vreg[j] = *reinterpret_cast<const uint4*>(vh + (long long)key * D + col * 4);
       } else {
         kreg[j] = make_uint4(0, 0, 0, 0);
         vreg[j] = make_uint4(0, 0, 0, 0);
@@ -214,30 +585,25 @@ attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* __
     }
   };
   auto lstore = [&](int buf) {
-    T* kd = Ks + buf * S::kTileElems;
-    T* vd = Vs + buf * S::kTileElems;
+    float* kd = Ks + buf * S::kTileElems;
+    float* vd = Vs + buf * S::kTileElems;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int c = tid + j * NTHREADS;
       const int row = c / CPR, col = c - row * CPR;
-      uint2* pk = reinterpret_cast<uint2*>(kd + row * LROW + col * EPC);
-      uint2* pv = reinterpret_cast<uint2*>(vd + row * LROW + col * EPC);
-      pk[0] = make_uint2(kreg[j].x, kreg[j].y);
-      pk[1] = make_uint2(kreg[j].z, kreg[j].w);
-      pv[0] = make_uint2(vreg[j].x, vreg[j].y);
-      pv[1] = make_uint2(vreg[j].z, vreg[j].w);
+      *reinterpret_cast<uint4*>(kd + row * LROW + col * 4) = kreg[j];
+      *reinterpret_cast<uint4*>(vd + row * LROW + col * 4) = vreg[j];
     }
   };
 
   gload(0);
   lstore(0);
   __syncthreads();
-
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     if (t + 1 < ntiles) gload(t + 1);
-    const T* Kt = Ks + buf * S::kTileElems;
-    const T* Vt = Vs + buf * S::kTileElems;
+    const float* Kt = Ks + buf * S::kTileElems;
+    const float* Vt = Vs + buf * S::kTileElems;
     const int tile_base = key_begin + t * TK;
     const bool need_mask = (tile_base + TK > key_end) || (tile_base + TK - 1 > causal_off);
     typename F::KFrag kf;
@@ -247,14 +613,7 @@ attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* __
     const int key0 = tile_base + w * 16 + 4 * lg;
 #pragma unroll
     for (int rt = 0; rt < NT; ++rt) {
-      f32x4 s;
-      if constexpr (S::kQLds) {
-        typename F::QFrag qt;
-        F::load_q(qt, Qs + (rt * 16 + ln) * LROW, lg);
-        s = F::qk(kf, qt);
-      } else {
-        s = F::qk(kf, qf[rt]);
-      }
+      const f32x4 s = F::qk(kf, qf[rt]);
       float sv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) sv[i] = s[i] * scale_log2;
@@ -283,15 +642,14 @@ attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* __
     __syncthreads();
   }
 
-  // ---- merge the four waves (each saw a different quarter of every tile) ----
 #pragma unroll
   for (int rt = 0; rt < NT; ++rt) {
     l_run[rt] += __shfl_xor(l_run[rt], 16);
     l_run[rt] += __shfl_xor(l_run[rt], 32);
   }
-  float* So = reinterpret_cast<float*>(smem);                       // [NT*16][OROW]
-  float2* ml_w = reinterpret_cast<float2*>(smem + S::kMLOff);       // [WAVES][NT*16]
-  float2* ml_f = ml_w + WAVES * NT * 16;                            // [NT*16]
+  float* So = reinterpret_cast<float*>(smem);
+  float2* ml_w = reinterpret_cast<float2*>(smem + S::kMLOff);
+  float2* ml_f = ml_w + WAVES * NT * 16;
   if (lg == 0) {
 #pragma unroll
     for (int rt = 0; rt < NT; ++rt) ml_w[w * NT * 16 + rt * 16 + ln] = make_float2(m_run[rt], l_run[rt]);
@@ -328,125 +686,78 @@ attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* __
     }
     __syncthreads();
   }
-
-  for (int idx = tid; idx < R * (D / 4); idx += NTHREADS) {
-    const int r = idx / (D / 4), d4 = idx - r * (D / 4);
-    const f32x4 o = *reinterpret_cast<const f32x4*>(So + r * OROW + 4 * d4);
-    const float2 ml = ml_f[r];
-    if (n_split == 1) {
-      const int hl = r / q_len, i = r - hl * q_len;
-      T* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(o[e] / ml.y);
-    } else {
-      const long long row = (long long)(g * n_split + split) * R + r;
-      *reinterpret_cast<f32x4*>(ws_o + row * D + 4 * d4) = o;
-      if (d4 == 0) ws_ml[row] = ml;
-    }
-  }
+  auto orow = [&](int r) -> float* { return So + r * OROW; };
+  finish_split<float>(orow, ml_f, out, ws_o, ws_ml, g, split, n_split, q_len, group, NTHREADS);
 }
 
-// grid (R, n_kv), block D: combine the split partials of one query row.
-template <typename T>
-__global__ void __launch_bounds__(D)
-attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
-                  int n_split, int q_len, int group) {
-  const int r = blockIdx.x, g = blockIdx.y, d = threadIdx.x;
+// ===========================================================================
+template <int NT>
+int launch_nt(const void* q, const void* k, const void* v, void* out, int n_kv, int q_len, int kv_len, int group,
+              long long k_hs, long long v_hs, float scale, int dtype, void* ws, hipStream_t st) {
   const int R = group * q_len;
-  const long long base = (long long)g * n_split * R + r;
-  float M = -1e30f;
-  for (int s = 0; s < n_split; ++s) M = fmaxf(M, ws_ml[base + (long long)s * R].x);
-  float L = 0.f, o = 0.f;
-  for (int s = 0; s < n_split; ++s) {
-    const long long row = base + (long long)s * R;
-    const float2 ml = ws_ml[row];
-    const float e = fast_exp2(ml.x - M);
-    L += ml.y * e;
-    o += ws_o[row * D + d] * e;
-  }
-  const int hl = r / q_len, i = r - hl * q_len;
-  out[((long long)(g * group + hl) * q_len + i) * D + d] = from_f32<T>(o / L);
-}
-
-struct SplitPlan {
-  int tiles_per_split;
-  int n_split;
-};
-
-SplitPlan plan_splits(int n_kv, int kv_len) {
-  const int ntiles = (kv_len + TK - 1) / TK;
-  const int target = (kTargetWorkgroups + n_kv - 1) / n_kv;
-  int tps = (ntiles + target - 1) / target;
-  if (tps < 1) tps = 1;
-  SplitPlan p;
-  p.tiles_per_split = tps;
-  p.n_split = (ntiles + tps - 1) / tps;
-  return p;
-}
-
-size_t attn_workspace_bytes(int n_kv, int rows, int kv_len) {
-  const SplitPlan p = plan_splits(n_kv, kv_len);
-  if (p.n_split <= 1) return 0;
-  const size_t n = (size_t)n_kv * p.n_split * rows;
-  return round_up(n * D * sizeof(float), 256) + n * sizeof(float2);
-}
-
-template <typename T, int NT>
-int launch_attn_t(const void* q, const void* k, const void* v, void* out, int n_kv, int q_len, int kv_len,
-                  int group, long long k_hs, long long v_hs, float scale, void* ws, hipStream_t st) {
-  const int R = group * q_len;
-  const SplitPlan p = plan_splits(n_kv, kv_len);
-  const size_t n = (size_t)n_kv * p.n_split * R;
-  float* ws_o = static_cast<float*>(ws);
-  float2* ws_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + round_up(n * D * sizeof(float), 256));
+  const SplitPlan p = plan_splits(n_kv, R, kv_len, dtype);
+  const WsLayout wl = ws_layout(n_kv, R, p);
+  char* base = static_cast<char*>(ws);
+  float* ws_o = p.n_split > 1 ? reinterpret_cast<float*>(base + wl.o_off) : nullptr;
+  float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL((attn_split_kernel<T, NT>), dim3(p.n_split, n_kv), dim3(NTHREADS), 0, st,
-                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
-                     static_cast<T*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
-                     p.tiles_per_split, p.n_split, kv_len - q_len);
-  int st0 = launch_status();
-  if (st0 != 0 || p.n_split == 1) return st0;
-  hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(R, n_kv), dim3(D), 0, st, ws_o, ws_ml,
-                     static_cast<T*>(out), p.n_split, q_len, group);
+  const dim3 grid(p.n_split, n_kv);
+  if (dtype == STD_BF16) {
+    constexpr int RG = NT >= 3 ? 2 : 1;   // second row group of waves once a wave would carry > 2 row tiles
+    hipLaunchKernelGGL((attn_bf16_kernel<NT, RG>), grid, dim3(Bf16Cfg<NT, RG>::kThreads), 0, st,
+                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
+                       static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
+                       p.ntiles, p.n_split, kv_len - q_len);
+  } else {
+    hipLaunchKernelGGL((attn_f32_kernel<NT>), grid, dim3(NTHREADS), 0, st, static_cast<const float*>(q),
+                       static_cast<const float*>(k), static_cast<const float*>(v), static_cast<float*>(out), ws_o,
+                       ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len);
+  }
+  int s = launch_status();
+  if (s != 0 || p.n_split == 1) return s;
+  if (dtype == STD_BF16)
+    hipLaunchKernelGGL((attn_merge_kernel<bf16_t>), dim3(R, n_kv), dim3(D), 0, st, ws_o, ws_ml,
+                       static_cast<bf16_t*>(out), p.n_split, q_len, group);
+  else
+    hipLaunchKernelGGL((attn_merge_kernel<float>), dim3(R, n_kv), dim3(D), 0, st, ws_o, ws_ml,
+                       static_cast<float*>(out), p.n_split, q_len, group);
   return launch_status();
 }
 
-template <typename T>
-int launch_attn(const void* q, const void* k, const void* v, void* out, int n_kv, int q_len, int kv_len,
-                int group, long long k_hs, long long v_hs, float scale, void* ws, hipStream_t st) {
-  const int nt = (group * q_len + 15) / 16;
-  switch (nt) {
-    case 1: return launch_attn_t<T, 1>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
-    case 2: return launch_attn_t<T, 2>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
-    case 3: return launch_attn_t<T, 3>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
-    case 4: return launch_attn_t<T, 4>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
-    case 5: return launch_attn_t<T, 5>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
-    case 6: return launch_attn_t<T, 6>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
-    case 7: return launch_attn_t<T, 7>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
-    case 8: return launch_attn_t<T, 8>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
+int launch_attn(const void* q, const void* k, const void* v, void* out, int n_kv, int q_len, int kv_len, int group,
+                long long k_hs, long long v_hs, float scale, int dtype, void* ws, hipStream_t st) {
+  switch ((group * q_len + 15) / 16) {
+    case 1: return launch_nt<1>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
+    case 2: return launch_nt<2>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
+    case 3: return launch_nt<3>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
+    case 4: return launch_nt<4>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
+    case 5: return launch_nt<5>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
+    case 6: return launch_nt<6>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
     default: return STD_E_SHAPE;
   }
 }
 
-int attn_entry(const void* q, const void* k, const void* v, void* out, int n_q, int n_kv, int q_len,
-               int kv_len, int d, long long k_hs, long long v_hs, float scale, int dtype, void* ws,
-               size_t ws_bytes, void* stream) {
+size_t attn_workspace_bytes(int n_kv, int rows, int kv_len, int dtype) {
+  return ws_layout(n_kv, rows, plan_splits(n_kv, rows, kv_len, dtype)).total;
+}
+
+int attn_entry(const void* q, const void* k, const void* v, void* out, int n_q, int n_kv, int q_len, int kv_len,
+               int d, long long k_hs, long long v_hs, float scale, int dtype, void* ws, size_t ws_bytes,
+               void* stream) {
   if (!q || !k || !v || !out) return STD_E_NULL;
   if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
   if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len) return STD_E_SHAPE;
   const int group = n_q / n_kv;
   if ((long long)group * q_len > kMaxRows) return STD_E_SHAPE;
   const int es = dtype_size(dtype);
-  if (k_hs < (long long)kv_len * D || v_hs < (long long)kv_len * D) return STD_E_SHAPE;
+  if (n_kv > 1 && (k_hs < (long long)kv_len * D || v_hs < (long long)kv_len * D)) return STD_E_SHAPE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return STD_E_ALIGN;
   if ((k_hs * es) % 16 != 0 || (v_hs * es) % 16 != 0) return STD_E_ALIGN;
-  const size_t need = attn_workspace_bytes(n_kv, group * q_len, kv_len);
+  const size_t need = attn_workspace_bytes(n_kv, group * q_len, kv_len, dtype);
   if (need > 0 && (ws == nullptr || ws_bytes < need)) return STD_E_WORKSPACE;
   if (need > 0 && !aligned16(ws)) return STD_E_ALIGN;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == STD_BF16)
-    return launch_attn<bf16_t>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
-  return launch_attn<float>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, ws, st);
+  return launch_attn(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws,
+                     static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -456,19 +767,24 @@ using namespace stdhip;
 
 extern "C" size_t std_gqa_decode_workspace_bytes(int n_q, int n_kv, int kv_len, int d) {
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || kv_len < 1 || d != D) return 0;
-  return attn_workspace_bytes(n_kv, n_q / n_kv, kv_len);
+  // the larger of the two dtype plans, so one query serves both
+  const size_t a = attn_workspace_bytes(n_kv, n_q / n_kv, kv_len, STD_BF16);
+  const size_t b = attn_workspace_bytes(n_kv, n_q / n_kv, kv_len, STD_F32);
+  return a > b ? a : b;
 }
 
 extern "C" int std_gqa_decode(const void* q, const void* k, const void* v, void* out, int n_q, int n_kv,
                               int kv_len, int d, long long k_head_stride, long long v_head_stride, float scale,
                               int dtype, void* workspace, size_t workspace_bytes, void* stream) {
-  return attn_entry(q, k, v, out, n_q, n_kv, 1, kv_len, d, k_head_stride, v_head_stride, scale, dtype,
-                    workspace, workspace_bytes, stream);
+  return attn_entry(q, k, v, out, n_q, n_kv, 1, kv_len, d, k_head_stride, v_head_stride, scale, dtype, workspace,
+                    workspace_bytes, stream);
 }
 
 extern "C" size_t std_verify_attn_workspace_bytes(int n_q, int n_kv, int q_len, int kv_len, int d) {
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len || d != D) return 0;
-  return attn_workspace_bytes(n_kv, (n_q / n_kv) * q_len, kv_len);
+  const size_t a = attn_workspace_bytes(n_kv, (n_q / n_kv) * q_len, kv_len, STD_BF16);
+  const size_t b = attn_workspace_bytes(n_kv, (n_q / n_kv) * q_len, kv_len, STD_F32);
+  return a > b ? a : b;
 }
 
 extern "C" int std_verify_attn(const void* q, const void* k, const void* v, void* out, int n_q, int n_kv,

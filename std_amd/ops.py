@@ -41,10 +41,28 @@ def _stream(dev: torch.device) -> int:
 
 
 def _workspace(nbytes: int, dev: torch.device) -> Tuple[int, torch.Tensor]:
+    """Per-call scratch (selection, acceptance): no initial contents needed."""
     if nbytes == 0:
         return 0, None
     buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     return buf.data_ptr(), buf
+
+
+_ATTN_WS = {}
+
+
+def _attn_workspace(nbytes: int, dev: torch.device) -> int:
+    """Persistent attention workspace per (device, stream): calls on one stream
+    are ordered and may share it (no per-call allocation on the decode path);
+    another stream gets its own."""
+    if nbytes == 0:
+        return 0
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    buf = _ATTN_WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _ATTN_WS[key] = buf
+    return buf.data_ptr()
 
 
 def _check_cache_view(name: str, t: torch.Tensor) -> None:
@@ -119,7 +137,7 @@ def _attention(fn: str, query, key, value, scale, out):
         ws_bytes = lib.std_gqa_decode_workspace_bytes(n_q, n_kv, kv_len, d)
     else:
         ws_bytes = lib.std_verify_attn_workspace_bytes(n_q, n_kv, q_len, kv_len, d)
-    ws_ptr, ws = _workspace(ws_bytes, dev)
+    ws_ptr = _attn_workspace(ws_bytes, dev)
     hs_k, hs_v = key.stride(1), value.stride(1)
     if fn == "std_gqa_decode":
         _lib.call(fn, query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), n_q, n_kv, kv_len, d,

@@ -72,7 +72,7 @@ def test_decode_validation(args, expected):
 def test_verify_validation():
     lib = _lib.load_library()
     hs = 4106 * 128
-    assert lib.std_verify_attn(16, 16, 16, 16, 28, 4, 20, 4106, 128, hs, hs, 1.0, 1, NULL, 0, NULL) == -3  # 7*20 rows
+    assert lib.std_verify_attn(16, 16, 16, 16, 28, 4, 20, 4106, 128, hs, hs, 1.0, 1, NULL, 0, NULL) == -3  # 7*20 rows > 96
     assert lib.std_verify_attn(16, 16, 16, 16, 28, 4, 11, 10, 128, hs, hs, 1.0, 1, NULL, 0, NULL) == -3   # q > kv
 
 
