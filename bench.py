@@ -5,9 +5,9 @@ workload (28 layers, 28 query / 4 KV heads, head_dim 128, context 131072 =
 130944 visual + 128 text, K+text = 1024, gamma = 9), in the reference's order
 (src/std_repro/std_qwen25vl.py:766-939):
   draft   gamma sparse steps; each appends one K/V row per layer to the compact
-          cache (device length) and runs GQA decode attention over it
-  verify  per layer: append gamma+1 rows to the dense cache, offset-causal
-          verify attention over all 131072 + 10 keys
+          cache and runs GQA decode attention over it (one fused launch)
+  verify  per layer: append gamma+1 rows to the dense cache and run the
+          offset-causal verify attention over all 131072 + 10 keys (one launch)
   accept  argmax over [gamma+1, 152064] logits, greedy prefix, bonus, device
           rollback of both cache lengths, one 8-byte readback
 Inputs are synthetic, generated on the device and resident in HBM before the
@@ -133,84 +133,108 @@ def main():
     lengths0 = torch.tensor([P, S0], dtype=torch.int32, device=dev)     # [dense_len, sparse_len]
     lengths = lengths0.clone()
     dense_len, sparse_len = lengths[0:1], lengths[1:2]
-    stream = torch.cuda.current_stream()
 
-    def draft_phase(ev=None):
+    # Each layer call appends its new K/V row(s) and attends in one launch
+    # (KVCache.cat + attention); the device lengths advance once per step.
+    def draft_phase():
         for t in range(G):
             S = S0 + t + 1
             for l in range(L):
-                ops.kv_append(sparse_k[l], sparse_v[l], new_k_draft[l], new_v_draft[l], sparse_len)
-                if ev is not None:
-                    ev[0].append(torch.cuda.Event(enable_timing=True))
-                    ev[0][-1].record(stream)
-                ops.gqa_decode(q_draft[l], sparse_k[l][:, :, :S], sparse_v[l][:, :, :S], out=draft_out[l])
-                if ev is not None:
-                    ev[1].append(torch.cuda.Event(enable_timing=True))
-                    ev[1][-1].record(stream)
+                ops.gqa_decode_append(q_draft[l], sparse_k[l], sparse_v[l], new_k_draft[l], new_v_draft[l], S,
+                                      out=draft_out[l])
             ops.len_add(sparse_len, 1)
 
-    def verify_phase(ev=None):
+    def verify_phase():
         kv = P + Q
         for l in range(L):
-            ops.kv_append(dense_k[l], dense_v[l], new_k_verify[l], new_v_verify[l], dense_len)
-            if ev is not None:
-                ev[0].append(torch.cuda.Event(enable_timing=True))
-                ev[0][-1].record(stream)
-            ops.verify_attention(q_verify[l], dense_k[l][:, :, :kv], dense_v[l][:, :, :kv], out=verify_out[l])
-            if ev is not None:
-                ev[1].append(torch.cuda.Event(enable_timing=True))
-                ev[1][-1].record(stream)
+            ops.verify_attention_append(q_verify[l], dense_k[l], dense_v[l], new_k_verify[l], new_v_verify[l], kv,
+                                        out=verify_out[l])
         ops.len_add(dense_len, Q)
 
-    def step(dev_ev=None, ver_ev=None):
-        draft_phase(dev_ev)
-        verify_phase(ver_ev)
-        res = ops.greedy_accept(logits, draft, True, rollback_lengths=lengths)
-        a = int(res[0].item())                           # the one readback per round
+    def round_kernels():
         lengths.copy_(lengths0)                          # steady state: same shapes every round
-        return a
+        draft_phase()
+        verify_phase()
+        return ops.greedy_accept(logits, draft, True, rollback_lengths=lengths)
+
+    def capture(fn):
+        """Capture fn into a HIP graph (after one eager warm-up on a side stream)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            res = fn()
+        return graph, res
 
     log(f"selection+compaction {select_ms:.2f} ms for {L} layers")
+    # eager round: the reference result for the captured graph
+    res_eager = round_kernels()
+    torch.cuda.synchronize()
+    a_eager = int(res_eager[0])
+    draft_eager, verify_eager = draft_out.clone(), verify_out.clone()
+    assert a_eager == 6, f"acceptance length {a_eager} != 6"
+    round_graph, res_graph = capture(round_kernels)
+
+    def step():
+        round_graph.replay()
+        return int(res_graph[0].item())                  # the one readback per round
+
     for _ in range(args.warmup):
         a = step()
     torch.cuda.synchronize()
-    assert a == 6, f"acceptance length {a} != 6"
+    # every replay must reproduce the eager round exactly (same kernels, same inputs)
+    assert a == a_eager and torch.equal(draft_out, draft_eager) and torch.equal(verify_out, verify_eager), \
+        "graph replay differs from the eager round"
 
-    dev_ev, ver_ev = ([], []), ([], [])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(dev_ev, ver_ev)
+        step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
-
-    draft_us = [a.elapsed_time(b) * 1e3 for a, b in zip(*dev_ev)]      # per layer-call
-    verify_us = [a.elapsed_time(b) * 1e3 for a, b in zip(*ver_ev)]
-    draft_call_us = statistics.mean(draft_us)
-    verify_call_us = statistics.mean(verify_us)
-    S_mid = S0 + (G + 1) // 2
-    d_bytes = draft_bytes(Hq, Hkv, S_mid, D, es)
-    v_bytes = verify_bytes(Hq, Hkv, Q, P + Q, D, es)
-    verify_gbps = v_bytes / (verify_call_us * 1e-6) / 1e9
-    draft_gbps_warm = d_bytes / (draft_call_us * 1e-6) / 1e9
-
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
-    # ---- cold-cache draft step: flush (write 1 GiB) before each 28-layer step ----
-    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    cold = []
-    for _ in range(args.cold_iters):
-        flush.fill_(1)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
+
+    # ---- per-kernel timing: graphs of one phase's attention calls, HIP events on the replay stream ----
+    kv = P + Q
+
+    def verify_only():
+        for l in range(L):
+            ops.verify_attention(q_verify[l], dense_k[l][:, :, :kv], dense_v[l][:, :, :kv], out=verify_out[l])
+
+    def draft_only():
         for l in range(L):
             ops.gqa_decode(q_draft[l], sparse_k[l][:, :, :S0], sparse_v[l][:, :, :S0], out=draft_out[l])
-        e1.record(stream)
-        torch.cuda.synchronize()
-        cold.append(e0.elapsed_time(e1) * 1e3)
-    draft_step_cold_us = statistics.median(cold)
-    draft_step_cold_gbps = L * draft_bytes(Hq, Hkv, S0, D, es) / (draft_step_cold_us * 1e-6) / 1e9
+
+    def time_graph(graph, iters, flush=None):
+        stream = torch.cuda.current_stream()
+        times = []
+        for _ in range(iters):
+            if flush is not None:
+                flush.fill_(1)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3)
+        return statistics.median(times)
+
+    verify_graph, _ = capture(verify_only)
+    draft_graph, _ = capture(draft_only)
+    verify_call_us = time_graph(verify_graph, 10) / L
+    draft_call_us = time_graph(draft_graph, 50) / L
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    draft_step_cold_us = time_graph(draft_graph, args.cold_iters, flush)      # 1 GiB written before each
     del flush
+    d_bytes = draft_bytes(Hq, Hkv, S0, D, es)
+    v_bytes = verify_bytes(Hq, Hkv, Q, P + Q, D, es)
+    verify_gbps = v_bytes / (verify_call_us * 1e-6) / 1e9
+    draft_step_cold_gbps = L * d_bytes / (draft_step_cold_us * 1e-6) / 1e9
 
     draft_tokens_per_s = G * args.steps / elapsed
     traffic = None
@@ -236,11 +260,12 @@ def main():
             "workload": f"{w.name}: {L}-layer attention stack, {Hq}q/{Hkv}kv heads, d={D}, context {P} "
                         f"({P - T} visual + {T} text), K+text={w.k_plus_text}, gamma={G}, vocab={w.vocab}",
             "step": "gamma draft decode steps over the compact cache + dense verify (q=gamma+1) + greedy "
-                    "accept/rollback, all layers",
+                    "accept/rollback, all layers; replayed as one HIP graph plus one 8-byte readback",
             "parallelism": "single GPU",
         },
         "draft_attn_us_per_step": round(draft_call_us * L, 2),
         "draft_attn_us_per_layer": round(draft_call_us, 3),
+        "draft_hbm_gbps_warm": round(d_bytes / (draft_call_us * 1e-6) / 1e9, 1),
         "draft_attn_us_per_step_cold": round(draft_step_cold_us, 2),
         "draft_hbm_gbps_cold_step": round(draft_step_cold_gbps, 1),
         "draft_pct_peak_cold_step": round(100 * draft_step_cold_gbps / HBM_PEAK_GBPS, 2),
@@ -251,7 +276,7 @@ def main():
         "select_compact_ms_all_layers": round(select_ms, 3),
         "select_compact_ms_first_call": round(select_ms_first, 3),
         "roofline": {
-            "kernel": "verify attention (attn_split_kernel<bf16,5> + attn_merge_kernel), one layer",
+            "kernel": "verify attention, one layer (attn_bf16_kernel<5,2> + attn_merge_kernel<bf16>)",
             "bound": "hbm",
             "achieved": round(verify_gbps, 1),
             "peak": HBM_PEAK_GBPS,

@@ -73,6 +73,18 @@ int std_gqa_decode(const void* q, const void* k, const void* v, void* out,
                    float scale, int dtype,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Append + decode in one launch: the single new K/V row (new_k/new_v
+ * [n_kv][1][d], head stride new_head_stride) is written to cache row
+ * kv_len - 1, then the call attends over kv_len keys exactly as
+ * std_gqa_decode. Replaces the draft attention's KVCache.cat followed by the
+ * attention call (std_qwen25vl.py:395-417). */
+int std_gqa_decode_append(const void* q, void* k_cache, void* v_cache,
+                          const void* new_k, const void* new_v, void* out,
+                          int n_q, int n_kv, int kv_len, int d,
+                          long long k_head_stride, long long v_head_stride,
+                          long long new_head_stride, float scale, int dtype,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Dense verify attention for q_len appended query rows (offset-causal).
  *
@@ -93,6 +105,19 @@ int std_verify_attn(const void* q, const void* k, const void* v, void* out,
                     long long k_head_stride, long long v_head_stride,
                     float scale, int dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Append + verify in one launch: the q_len new K/V rows (new_k/new_v
+ * [n_kv][q_len][d], strides in elements) are written to cache rows
+ * [kv_len - q_len, kv_len), then the call attends exactly as std_verify_attn.
+ * Replaces the verify forward's KVCache.cat followed by its attention
+ * (modeling_qwen2_5_vl.py:1057-1132). Workspace: std_verify_attn_workspace_bytes. */
+int std_verify_attn_append(const void* q, void* k_cache, void* v_cache,
+                           const void* new_k, const void* new_v, void* out,
+                           int n_q, int n_kv, int q_len, int kv_len, int d,
+                           long long k_head_stride, long long v_head_stride,
+                           long long new_head_stride, long long new_row_stride,
+                           float scale, int dtype,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Text-to-video top-K selection for one layer.

@@ -84,6 +84,27 @@ __device__ __forceinline__ int split_tile(int split, int ntiles, int n_split) {
   return (int)((long long)split * ntiles / n_split);
 }
 
+// Fused append: cache rows [kv_len - n_new, kv_len) receive the n_new new
+// rows (new_*[g][r], strides in elements). Each workgroup writes the rows that
+// fall inside its own key range, before it reads that range (the caller puts a
+// barrier between the two), so no other workgroup depends on these writes.
+template <typename T>
+__device__ void append_rows(T* __restrict__ kh, T* __restrict__ vh, const T* __restrict__ nk,
+                            const T* __restrict__ nv, long long n_hs, long long n_rs, int g, int n_new, int kv_len,
+                            int key_begin, int key_end, int nthreads) {
+  constexpr int EPC = 16 / (int)sizeof(T);
+  constexpr int CPR = D / EPC;
+  const int first = max(kv_len - n_new, key_begin), last = min(kv_len, key_end);
+  for (int idx = threadIdx.x; idx < (last - first) * CPR; idx += nthreads) {
+    const int row = first + idx / CPR, col = idx % CPR;
+    const long long src = (long long)g * n_hs + (long long)(row - (kv_len - n_new)) * n_rs + col * EPC;
+    const uint4 k4 = *reinterpret_cast<const uint4*>(nk + src);
+    const uint4 v4 = *reinterpret_cast<const uint4*>(nv + src);
+    *reinterpret_cast<uint4*>(kh + (long long)row * D + col * EPC) = k4;
+    *reinterpret_cast<uint4*>(vh + (long long)row * D + col * EPC) = v4;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Epilogue shared by both kernels: the key-waves' merged rows are in LDS
 // (So(r) -> row r of O, unnormalised; ml_f[r] = (m, l), log2 domain).
@@ -228,10 +249,11 @@ struct Bf16Cfg {
 
 template <int NT, int RG>
 __global__ void __launch_bounds__(256 * RG)
-attn_bf16_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc,
+attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
                  bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
-                 int n_split, int causal_off) {
+                 int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
+                 long long n_hs, long long n_rs, int n_new) {
   using C = Bf16Cfg<NT, RG>;
   constexpr int NTW = C::NTW;
   __shared__ __align__(16) char st0[STAGEB];
@@ -253,8 +275,12 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, co
   const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
   const int key_begin = t_begin * TK;
   const int key_end = min(kv_len, key_begin + ntiles * TK);
-  const bf16_t* kh = kc + (long long)g * k_hs;
-  const bf16_t* vh = vc + (long long)g * v_hs;
+  bf16_t* kh = kc + (long long)g * k_hs;
+  bf16_t* vh = vc + (long long)g * v_hs;
+  if (n_new > 0) {
+    append_rows<bf16_t>(kh, vh, new_k, new_v, n_hs, n_rs, g, n_new, kv_len, key_begin, key_end, C::kThreads);
+    __syncthreads();
+  }
 
   int lim[NTW];
 #pragma unroll
@@ -519,10 +545,11 @@ struct F32Smem {
 
 template <int NT>
 __global__ void __launch_bounds__(NTHREADS)
-attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __restrict__ vc,
                 float* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                 int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
-                int n_split, int causal_off) {
+                int n_split, int causal_off, const float* __restrict__ new_k, const float* __restrict__ new_v,
+                long long n_hs, long long n_rs, int n_new) {
   using F = F32Frag;
   using S = F32Smem<NT>;
   constexpr int CPR = D / 4;                    // 16-byte chunks per fp32 row
@@ -539,8 +566,12 @@ attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc, const
   const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
   const int key_begin = t_begin * TK;
   const int key_end = min(kv_len, key_begin + ntiles * TK);
-  const float* kh = kc + (long long)g * k_hs;
-  const float* vh = vc + (long long)g * v_hs;
+  float* kh = kc + (long long)g * k_hs;
+  float* vh = vc + (long long)g * v_hs;
+  if (n_new > 0) {
+    append_rows<float>(kh, vh, new_k, new_v, n_hs, n_rs, g, n_new, kv_len, key_begin, key_end, NTHREADS);
+    __syncthreads();
+  }
 
   typename F::QFrag qf[NT];
   int lim[NT];
@@ -692,8 +723,9 @@ attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc, const
 
 // ===========================================================================
 template <int NT>
-int launch_nt(const void* q, const void* k, const void* v, void* out, int n_kv, int q_len, int kv_len, int group,
-              long long k_hs, long long v_hs, float scale, int dtype, void* ws, hipStream_t st) {
+int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
+              long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
+              long long n_hs, long long n_rs, int n_new, hipStream_t st) {
   const int R = group * q_len;
   const SplitPlan p = plan_splits(n_kv, R, kv_len, dtype);
   const WsLayout wl = ws_layout(n_kv, R, p);
@@ -705,13 +737,15 @@ int launch_nt(const void* q, const void* k, const void* v, void* out, int n_kv, 
   if (dtype == STD_BF16) {
     constexpr int RG = NT >= 3 ? 2 : 1;   // second row group of waves once a wave would carry > 2 row tiles
     hipLaunchKernelGGL((attn_bf16_kernel<NT, RG>), grid, dim3(Bf16Cfg<NT, RG>::kThreads), 0, st,
-                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v),
+                       static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                        static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
-                       p.ntiles, p.n_split, kv_len - q_len);
+                       p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
+                       static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new);
   } else {
     hipLaunchKernelGGL((attn_f32_kernel<NT>), grid, dim3(NTHREADS), 0, st, static_cast<const float*>(q),
-                       static_cast<const float*>(k), static_cast<const float*>(v), static_cast<float*>(out), ws_o,
-                       ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len);
+                       static_cast<float*>(k), static_cast<float*>(v), static_cast<float*>(out), ws_o, ws_ml, q_len,
+                       kv_len, group, k_hs, v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len,
+                       static_cast<const float*>(nk), static_cast<const float*>(nv), n_hs, n_rs, n_new);
   }
   int s = launch_status();
   if (s != 0 || p.n_split == 1) return s;
@@ -724,27 +758,32 @@ int launch_nt(const void* q, const void* k, const void* v, void* out, int n_kv, 
   return launch_status();
 }
 
-int launch_attn(const void* q, const void* k, const void* v, void* out, int n_kv, int q_len, int kv_len, int group,
-                long long k_hs, long long v_hs, float scale, int dtype, void* ws, hipStream_t st) {
+int launch_attn(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
+                long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
+                long long n_hs, long long n_rs, int n_new, hipStream_t st) {
+#define STD_LAUNCH_NT(N) \
+  launch_nt<N>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs, n_new, st)
   switch ((group * q_len + 15) / 16) {
-    case 1: return launch_nt<1>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
-    case 2: return launch_nt<2>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
-    case 3: return launch_nt<3>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
-    case 4: return launch_nt<4>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
-    case 5: return launch_nt<5>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
-    case 6: return launch_nt<6>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, st);
+    case 1: return STD_LAUNCH_NT(1);
+    case 2: return STD_LAUNCH_NT(2);
+    case 3: return STD_LAUNCH_NT(3);
+    case 4: return STD_LAUNCH_NT(4);
+    case 5: return STD_LAUNCH_NT(5);
+    case 6: return STD_LAUNCH_NT(6);
     default: return STD_E_SHAPE;
   }
+#undef STD_LAUNCH_NT
 }
 
 size_t attn_workspace_bytes(int n_kv, int rows, int kv_len, int dtype) {
   return ws_layout(n_kv, rows, plan_splits(n_kv, rows, kv_len, dtype)).total;
 }
 
-int attn_entry(const void* q, const void* k, const void* v, void* out, int n_q, int n_kv, int q_len, int kv_len,
-               int d, long long k_hs, long long v_hs, float scale, int dtype, void* ws, size_t ws_bytes,
-               void* stream) {
+int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, int q_len, int kv_len, int d,
+               long long k_hs, long long v_hs, float scale, int dtype, void* ws, size_t ws_bytes, const void* nk,
+               const void* nv, long long n_hs, long long n_rs, int n_new, void* stream) {
   if (!q || !k || !v || !out) return STD_E_NULL;
+  if (n_new > 0 && (!nk || !nv)) return STD_E_NULL;
   if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
   if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len) return STD_E_SHAPE;
   const int group = n_q / n_kv;
@@ -753,11 +792,13 @@ int attn_entry(const void* q, const void* k, const void* v, void* out, int n_q, 
   if (n_kv > 1 && (k_hs < (long long)kv_len * D || v_hs < (long long)kv_len * D)) return STD_E_SHAPE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return STD_E_ALIGN;
   if ((k_hs * es) % 16 != 0 || (v_hs * es) % 16 != 0) return STD_E_ALIGN;
+  if (n_new > 0 && (!aligned16(nk) || !aligned16(nv) || (n_hs * es) % 16 != 0 || (n_rs * es) % 16 != 0))
+    return STD_E_ALIGN;
   const size_t need = attn_workspace_bytes(n_kv, group * q_len, kv_len, dtype);
   if (need > 0 && (ws == nullptr || ws_bytes < need)) return STD_E_WORKSPACE;
   if (need > 0 && !aligned16(ws)) return STD_E_ALIGN;
-  return launch_attn(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws,
-                     static_cast<hipStream_t>(stream));
+  return launch_attn(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs,
+                     n_new, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -776,8 +817,16 @@ extern "C" size_t std_gqa_decode_workspace_bytes(int n_q, int n_kv, int kv_len, 
 extern "C" int std_gqa_decode(const void* q, const void* k, const void* v, void* out, int n_q, int n_kv,
                               int kv_len, int d, long long k_head_stride, long long v_head_stride, float scale,
                               int dtype, void* workspace, size_t workspace_bytes, void* stream) {
-  return attn_entry(q, k, v, out, n_q, n_kv, 1, kv_len, d, k_head_stride, v_head_stride, scale, dtype, workspace,
-                    workspace_bytes, stream);
+  return attn_entry(q, const_cast<void*>(k), const_cast<void*>(v), out, n_q, n_kv, 1, kv_len, d, k_head_stride,
+                    v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0, 0, stream);
+}
+
+extern "C" int std_gqa_decode_append(const void* q, void* k_cache, void* v_cache, const void* new_k, const void* new_v,
+                                     void* out, int n_q, int n_kv, int kv_len, int d, long long k_head_stride,
+                                     long long v_head_stride, long long new_head_stride, float scale, int dtype,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  return attn_entry(q, k_cache, v_cache, out, n_q, n_kv, 1, kv_len, d, k_head_stride, v_head_stride, scale, dtype,
+                    workspace, workspace_bytes, new_k, new_v, new_head_stride, 0, 1, stream);
 }
 
 extern "C" size_t std_verify_attn_workspace_bytes(int n_q, int n_kv, int q_len, int kv_len, int d) {
@@ -790,6 +839,15 @@ extern "C" size_t std_verify_attn_workspace_bytes(int n_q, int n_kv, int q_len, 
 extern "C" int std_verify_attn(const void* q, const void* k, const void* v, void* out, int n_q, int n_kv,
                                int q_len, int kv_len, int d, long long k_head_stride, long long v_head_stride,
                                float scale, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
-  return attn_entry(q, k, v, out, n_q, n_kv, q_len, kv_len, d, k_head_stride, v_head_stride, scale, dtype,
-                    workspace, workspace_bytes, stream);
+  return attn_entry(q, const_cast<void*>(k), const_cast<void*>(v), out, n_q, n_kv, q_len, kv_len, d, k_head_stride,
+                    v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0, 0, stream);
+}
+
+extern "C" int std_verify_attn_append(const void* q, void* k_cache, void* v_cache, const void* new_k,
+                                      const void* new_v, void* out, int n_q, int n_kv, int q_len, int kv_len, int d,
+                                      long long k_head_stride, long long v_head_stride, long long new_head_stride,
+                                      long long new_row_stride, float scale, int dtype, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  return attn_entry(q, k_cache, v_cache, out, n_q, n_kv, q_len, kv_len, d, k_head_stride, v_head_stride, scale, dtype,
+                    workspace, workspace_bytes, new_k, new_v, new_head_stride, new_row_stride, q_len, stream);
 }

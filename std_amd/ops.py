@@ -108,7 +108,32 @@ def verify_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
     return _attention("std_verify_attn", query, key, value, scale, out)
 
 
-def _attention(fn: str, query, key, value, scale, out):
+def gqa_decode_append(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                      new_key: torch.Tensor, new_value: torch.Tensor, kv_len: int,
+                      scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """KVCache.cat of one new row at position kv_len - 1, then single-query
+    attention over kv_len keys, in one launch (std_qwen25vl.py:395-417).
+    key_cache/value_cache: full [1, n_kv, capacity, D] buffers; new_key/new_value
+    [1, n_kv, 1, D] with contiguous head_dim."""
+    if query.dim() != 4 or query.shape[0] != 1 or query.shape[2] != 1:
+        raise ValueError(f"Expected q_len=1 query [1, n_q, 1, D], got {tuple(query.shape)}")
+    return _attention("std_gqa_decode_append", query, key_cache, value_cache, scale, out,
+                      new_key=new_key, new_value=new_value, kv_len=kv_len)
+
+
+def verify_attention_append(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                            new_key: torch.Tensor, new_value: torch.Tensor, kv_len: int,
+                            scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """KVCache.cat of the Q new rows at [kv_len - Q, kv_len), then the
+    offset-causal verify attention over kv_len keys, in one launch
+    (modeling_qwen2_5_vl.py:1057-1132). new_key/new_value [1, n_kv, Q, D]."""
+    if query.dim() != 4 or query.shape[0] != 1:
+        raise ValueError(f"Expected query [1, n_q, Q, D], got {tuple(query.shape)}")
+    return _attention("std_verify_attn_append", query, key_cache, value_cache, scale, out,
+                      new_key=new_key, new_value=new_value, kv_len=kv_len)
+
+
+def _attention(fn: str, query, key, value, scale, out, new_key=None, new_value=None, kv_len=None):
     dev = _check_device(query, key, value)
     code = _dtype_code(query)
     if key.dtype != query.dtype or value.dtype != query.dtype:
@@ -117,7 +142,22 @@ def _attention(fn: str, query, key, value, scale, out):
     _check_cache_view("value", value)
     _check_rows_contiguous("query", query)
     _, n_q, q_len, d = query.shape
-    n_kv, kv_len = key.shape[1], key.shape[2]
+    appending = new_key is not None
+    if appending:
+        if kv_len is None or not (q_len <= kv_len <= key.shape[2]):
+            raise ValueError(f"kv_len={kv_len} must be in [q_len, cache capacity {key.shape[2]}]")
+        for name, t in (("new_key", new_key), ("new_value", new_value)):
+            if t.dim() != 4 or tuple(t.shape) != (1, key.shape[1], q_len, HEAD_DIM) or t.stride(3) != 1:
+                raise ValueError(f"{name} must be [1, n_kv, {q_len}, {HEAD_DIM}] with contiguous rows")
+            if t.dtype != query.dtype or t.device != query.device:
+                raise TypeError(f"{name} must match the query dtype and device")
+        if new_value.stride() != new_key.stride():
+            raise ValueError("new_key and new_value must share strides")
+        if value.stride(1) != key.stride(1):
+            raise ValueError("key and value caches must share a head stride")
+    n_kv = key.shape[1]
+    if not appending:
+        kv_len = key.shape[2]
     if value.shape != key.shape:
         raise ValueError(f"key {tuple(key.shape)} and value {tuple(value.shape)} differ")
     if d != HEAD_DIM:
@@ -133,18 +173,24 @@ def _attention(fn: str, query, key, value, scale, out):
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     lib = _lib.load_library()
-    if fn == "std_gqa_decode":
+    if q_len == 1 and fn.startswith("std_gqa_decode"):
         ws_bytes = lib.std_gqa_decode_workspace_bytes(n_q, n_kv, kv_len, d)
     else:
         ws_bytes = lib.std_verify_attn_workspace_bytes(n_q, n_kv, q_len, kv_len, d)
     ws_ptr = _attn_workspace(ws_bytes, dev)
     hs_k, hs_v = key.stride(1), value.stride(1)
+    qp, kp, vp, op, st = query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), _stream(dev)
     if fn == "std_gqa_decode":
-        _lib.call(fn, query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), n_q, n_kv, kv_len, d,
-                  hs_k, hs_v, float(scale), code, ws_ptr, ws_bytes, _stream(dev))
+        _lib.call(fn, qp, kp, vp, op, n_q, n_kv, kv_len, d, hs_k, hs_v, float(scale), code, ws_ptr, ws_bytes, st)
+    elif fn == "std_verify_attn":
+        _lib.call(fn, qp, kp, vp, op, n_q, n_kv, q_len, kv_len, d, hs_k, hs_v, float(scale), code, ws_ptr, ws_bytes,
+                  st)
+    elif fn == "std_gqa_decode_append":
+        _lib.call(fn, qp, kp, vp, new_key.data_ptr(), new_value.data_ptr(), op, n_q, n_kv, kv_len, d, hs_k, hs_v,
+                  new_key.stride(1), float(scale), code, ws_ptr, ws_bytes, st)
     else:
-        _lib.call(fn, query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), n_q, n_kv, q_len, kv_len,
-                  d, hs_k, hs_v, float(scale), code, ws_ptr, ws_bytes, _stream(dev))
+        _lib.call(fn, qp, kp, vp, new_key.data_ptr(), new_value.data_ptr(), op, n_q, n_kv, q_len, kv_len, d, hs_k,
+                  hs_v, new_key.stride(1), new_key.stride(2), float(scale), code, ws_ptr, ws_bytes, st)
     return out
 
 

@@ -143,3 +143,50 @@ def test_decode_is_deterministic():
     torch.cuda.synchronize()
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
+
+
+@pytest.mark.parametrize("dtype,kv_len", [(torch.float32, 1024), (torch.bfloat16, 1034), (torch.bfloat16, 65),
+                                          (torch.bfloat16, 131072)])
+def test_decode_append_matches_separate_append_and_oracle(dtype, kv_len):
+    """Fused KVCache.cat + decode: row kv_len-1 is written, then attended."""
+    gen = torch.Generator().manual_seed(kv_len)
+    k = torch.randn(1, 4, kv_len, 128, generator=gen).to(dtype)
+    v = torch.randn(1, 4, kv_len, 128, generator=gen).to(dtype)
+    q = torch.randn(1, 28, 1, 128, generator=gen).to(dtype)
+    announce(f"decode_append {dtype} kv_len={kv_len}")
+    kb = cache_buffer(k[:, :, :kv_len - 1], kv_len + 20)
+    vb = cache_buffer(v[:, :, :kv_len - 1], kv_len + 20)
+    nk, nv = k[:, :, kv_len - 1:].to(dev()), v[:, :, kv_len - 1:].to(dev())
+    out = ops.gqa_decode_append(q.to(dev()), kb, vb, nk, nv, kv_len)
+    torch.cuda.synchronize()
+    assert torch.equal(kb[:, :, kv_len - 1].cpu(), k[:, :, kv_len - 1])
+    assert torch.equal(vb[:, :, kv_len - 1].cpu(), v[:, :, kv_len - 1])
+    assert torch.isnan(kb[:, :, kv_len:].float()).all()          # nothing past the new row
+    assert_close(out, ref.gqa_sdpa(q, k, v), dtype)
+    sep = ops.gqa_decode(q.to(dev()), kb[:, :, :kv_len], vb[:, :, :kv_len])
+    torch.cuda.synchronize()
+    assert torch.equal(out, sep)
+
+
+@pytest.mark.parametrize("dtype,kv_len", [(torch.float32, 4106), (torch.bfloat16, 16394), (torch.bfloat16, 130),
+                                          (torch.bfloat16, 131082)])
+def test_verify_append_matches_oracle(dtype, kv_len):
+    """Fused append of the Q=10 verify rows + verify; kv_len=130 puts the new
+    rows [120, 130) across a tile and a split boundary (splits own 64 keys)."""
+    Q = 10
+    gen = torch.Generator().manual_seed(kv_len)
+    k = torch.randn(1, 4, kv_len, 128, generator=gen).to(dtype)
+    v = torch.randn(1, 4, kv_len, 128, generator=gen).to(dtype)
+    q = torch.randn(1, 28, Q, 128, generator=gen).to(dtype)
+    announce(f"verify_append {dtype} kv_len={kv_len}")
+    kb = cache_buffer(k[:, :, :kv_len - Q], kv_len + 7)
+    vb = cache_buffer(v[:, :, :kv_len - Q], kv_len + 7)
+    # projection-shaped new rows: [1, Q, n_kv, D] viewed as [1, n_kv, Q, D]
+    nk = k[:, :, kv_len - Q:].transpose(1, 2).contiguous().to(dev()).transpose(1, 2)
+    nv = v[:, :, kv_len - Q:].transpose(1, 2).contiguous().to(dev()).transpose(1, 2)
+    out = ops.verify_attention_append(q.to(dev()), kb, vb, nk, nv, kv_len)
+    torch.cuda.synchronize()
+    assert torch.equal(kb[:, :, kv_len - Q:kv_len].cpu(), k[:, :, kv_len - Q:])
+    assert torch.equal(vb[:, :, kv_len - Q:kv_len].cpu(), v[:, :, kv_len - Q:])
+    assert torch.isnan(vb[:, :, kv_len:].float()).all()
+    assert_close(out, ref.verify_attention(q, k, v), dtype)
