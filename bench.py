@@ -43,7 +43,40 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=None, help="override the layer count (default: workload's)")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cold-iters", type=int, default=10)
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="short run for rocprofv3 counter passes: a 1 GiB copy (calibration), then 5 verify and "
+                         "5 draft-decode launches at the workload's shapes")
     return ap.parse_args()
+
+
+def pmc_run(w) -> None:
+    """Dispatches for counter collection: calibration copy of known size, then
+    the verify and draft attention kernels on resident synthetic inputs."""
+    import torch
+
+    from std_amd import ops
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)          # 1 GiB
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log("calibration copy: 1073741824 bytes read, 1073741824 bytes written")
+    del src, dst
+    D, Hq, Hkv, P, Q = w.head_dim, w.n_q, w.n_kv, w.prompt_len, w.gamma + 1
+    gen = torch.Generator(device=dev).manual_seed(w.seed_base)
+    k = torch.randn(1, Hkv, P + Q, D, generator=gen, device=dev).to(w.dtype)
+    v = torch.randn(1, Hkv, P + Q, D, generator=gen, device=dev).to(w.dtype)
+    qv = torch.randn(1, Hq, Q, D, generator=gen, device=dev).to(w.dtype)
+    qd = torch.randn(1, Hq, 1, D, generator=gen, device=dev).to(w.dtype)
+    for _ in range(5):
+        ops.verify_attention(qv, k, v)
+    torch.cuda.synchronize()
+    S = w.compact_len
+    for _ in range(5):
+        ops.gqa_decode(qd, k[:, :, :S], v[:, :, :S])
+    torch.cuda.synchronize()
+    log(f"pmc run done: 5 verify launches (kv={P + Q}), 5 decode launches (kv={S})")
 
 
 def log(msg: str) -> None:
@@ -70,6 +103,9 @@ def main():
     from std_amd.workloads import WORKLOADS, non_visual_positions, visual_positions
 
     w = WORKLOADS[args.workload]
+    if args.pmc_run:
+        pmc_run(w)
+        return
     L = args.layers or w.n_layers
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
