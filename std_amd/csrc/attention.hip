@@ -206,6 +206,39 @@ __device__ __forceinline__ int sw_off(int row, int chunk) { return row * ROWB + 
 // operations of this wave are outstanding, leaving the other counters alone.
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from
+// sbase + voff (a wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane
+// byte offset, the global saddr form) to LDS byte lds_base + 16 i. Issued through inline asm on purpose:
+// the compiler's own LDS-DMA tracking cannot tell the ring stages apart and
+// would put s_waitcnt vmcnt(0) before every LDS read, draining the whole
+// prefetch each tile. Completion is instead ordered explicitly by
+// wait_vm_ahead (vmcnt) followed by a workgroup barrier before any wave
+// reads the stage; the "memory" clobber keeps the compiler from moving LDS
+// accesses across the issue. The compiler inserts no hazard wait states for
+// inline asm, so the asm carries its own: s_nop 4 (5 wait states) covers both
+// the M0 write before an LDS DMA and an SGPR operand written by a VALU
+// instruction (v_readfirstlane) shortly before a VMEM instruction reads it.
+__device__ __forceinline__ void lds_dma16_sbase(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  typedef const __attribute__((address_space(3))) char* lds_cptr;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr)(p)));
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (which would
+// wait for every outstanding load); the empty asm statements keep the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Wait until the tile `ahead` tiles before the newest issued one has landed
 // (each tile is `per_tile` DMA instructions per wave).
 template <int PER_TILE>
@@ -213,6 +246,16 @@ __device__ __forceinline__ void wait_vm_ahead(int ahead) {
   if (ahead >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * PER_TILE));
   else if (ahead == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(PER_TILE));
   else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+}
+
+// Four floats -> four bf16 (RNE); the two-wide conversions compile to
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ i16x4 pack_bf16x4(float a, float b, float c, float d) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+  const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{c, d}, bf16x2_t));
+  return __builtin_bit_cast(i16x4, (uint64_t)lo | ((uint64_t)hi << 32));
 }
 
 __device__ __forceinline__ float xor16_max(float x) {
@@ -234,27 +277,29 @@ __device__ __forceinline__ float xor32_sum(float x) {
 
 // NT row tiles of 16 query rows, RG row groups of four key-waves each; a wave
 // carries NTW = ceil(NT / RG) row tiles (padding tiles have zero queries and
-// are never written out).
-template <int NT, int RG>
+// are never written out). QL: the Q^T operand is re-read from LDS every tile
+// instead of being held in registers (needed when two waves share a SIMD
+// and each may hold only 256 registers).
+template <int NT, int RG, bool QL>
 struct Bf16Cfg {
   static constexpr int kWaves = 4 * RG;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int NTW = (NT + RG - 1) / RG;
   static constexpr int kRowTiles = NTW * RG;            // including padding tiles
-  static constexpr bool kQLds = kRowTiles > 1;
-  static constexpr int kQBytes = kQLds ? kRowTiles * 16 * ROWB : 16;
   static constexpr int kSegsPerWave = 16 / kWaves;       // 1 KiB K segments (and V) per wave per tile
   static constexpr int kLoadsPerTile = 2 * kSegsPerWave;
+  static constexpr int kQBytes = QL ? kRowTiles * 16 * ROWB : 16;
+  static constexpr int kQRegTiles = QL ? 1 : NTW;
 };
 
-template <int NT, int RG>
+template <int NT, int RG, bool QL>
 __global__ void __launch_bounds__(256 * RG)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
                  bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                  int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
                  long long n_hs, long long n_rs, int n_new) {
-  using C = Bf16Cfg<NT, RG>;
+  using C = Bf16Cfg<NT, RG, QL>;
   constexpr int NTW = C::NTW;
   __shared__ __align__(16) char st0[STAGEB];
   __shared__ __align__(16) char st1[STAGEB];
@@ -288,19 +333,10 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     const int r = (rg * NTW + rt) * 16 + ln;
     lim[rt] = r < R ? causal_off + (r % q_len) : INT_MAX;
   }
-  bf16x8 qreg[4];
-  if constexpr (!C::kQLds) {
-    const int r = ln;
-    if (r < R) {
-      const int hl = r / q_len, i = r - hl * q_len;
-      const bf16_t* row = q + ((long long)(g * group + hl) * q_len + i) * D;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) qreg[c] = *reinterpret_cast<const bf16x8*>(row + 32 * c + 8 * lg);
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) qreg[c] = bf16x8{};
-    }
-  } else {
+  // Q^T operand of row tile rt, 32-wide chunk c: lane (ln, lg) holds
+  // q[row][32c + 8lg, +8) of row (rg*NTW + rt)*16 + ln; padding rows are 0.
+  bf16x8 qf[C::kQRegTiles][4];
+  if constexpr (QL) {
     for (int idx = tid; idx < C::kRowTiles * 16 * 16; idx += C::kThreads) {
       const int r = idx >> 4, ch = idx & 15;
       uint4 val = make_uint4(0, 0, 0, 0);
@@ -311,45 +347,95 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       *reinterpret_cast<uint4*>(qs + sw_off(r, ch)) = val;
     }
     __syncthreads();
+  } else {
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt) {
+      const int r = (rg * NTW + rt) * 16 + ln;
+      if (r < R) {
+        const int hl = r / q_len, i = r - hl * q_len;
+        const bf16_t* row = q + ((long long)(g * group + hl) * q_len + i) * D;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qf[rt][c] = *reinterpret_cast<const bf16x8*>(row + 32 * c + 8 * lg);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qf[rt][c] = bf16x8{};
+      }
+    }
+    // Retire the query loads before the DMA ring starts: the compiler counts
+    // only its own loads, and a wait for them placed after ring DMAs would
+    // drain the ring.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
 
-  float m_run[NTW], l_run[NTW];
-  f32x4 acc[NTW][8];
+  // Running statistics in the log2 domain (scores pre-multiplied by
+  // scale*log2(e)): m_run is the running max, and the row sums are
+  // accumulated by an MFMA against a ones operand (all rows of lsum equal the
+  // row sum of the bf16 probabilities used for PV).
+  float m_run[NTW];
+  f32x4 acc[NTW][8], lsum[NTW];
 #pragma unroll
   for (int rt = 0; rt < NTW; ++rt) {
     m_run[rt] = -1e30f;
-    l_run[rt] = 0.f;
+    lsum[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const i16x4 ones = {0x3f80, 0x3f80, 0x3f80, 0x3f80};   // bf16 1.0
 
   // Each wave DMAs kSegsPerWave 1 KiB segments (4 rows) of K and of V per
   // tile. Lane l fills row 4*seg + l/16 at physical chunk l%16, i.e. logical
   // chunk (l%16) ^ swz(row). Rows past the split's last key re-read that key
   // (their scores are masked), so no read leaves the valid range.
+  int dma_row[C::kSegsPerWave], dma_chunk[C::kSegsPerWave];
+#pragma unroll
+  for (int j = 0; j < C::kSegsPerWave; ++j) {
+    const int seg = w * C::kSegsPerWave + j;
+    dma_row[j] = seg * 4 + (lane >> 4);
+    dma_chunk[j] = ((lane & 15) ^ swz(dma_row[j])) * 16;
+  }
   auto issue = [&](int tt, char* stage) {
     const int key0 = key_begin + tt * TK;
+    const int last = key_end - 1 - key0;               // wave-uniform
+    const bf16_t* kt = kh + (long long)key0 * D;
+    const bf16_t* vt = vh + (long long)key0 * D;
 #pragma unroll
     for (int j = 0; j < C::kSegsPerWave; ++j) {
-      const int seg = w * C::kSegsPerWave + j;
-      const int r = seg * 4 + (lane >> 4);
-      const int lc = (lane & 15) ^ swz(r);
-      const int key = min(key0 + r, key_end - 1);
-      const long long off = (long long)key * D + lc * 8;
-      __builtin_amdgcn_global_load_lds(kh + off, stage + seg * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vh + off, stage + TILEB + seg * 1024, 16, 0, 0);
+      const uint32_t off = (uint32_t)(min(dma_row[j], last) * ROWB + dma_chunk[j]);
+      const uint32_t dst = lds_addr(stage) + (w * C::kSegsPerWave + j) * 1024;
+      lds_dma16_sbase(kt, off, dst);
+      lds_dma16_sbase(vt, off, dst + TILEB);
     }
   };
 
-  auto compute = [&](int tt, const char* stage) {
-    const char* Ks = stage;
+  // Software pipeline, one step per tile u (steps 0..ntiles): after the
+  // barrier, tile u+2 is prefetched into the stage tile u-2 used (every wave
+  // finished tile u-2's PV before this barrier), the QK^T MFMAs of tile u are
+  // issued into one score buffer, then the softmax and PV of tile u-1 run on
+  // the other, so matrix and vector work of neighbouring tiles overlap inside
+  // a wave and two tiles stay in flight during the step.
+  f32x4 sA[NTW], sB[NTW];
+  auto qk = [&](const char* stage, f32x4* s) {
+    const int rk = kg * 16 + ln;
+    bf16x8 kf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kf[c] = *reinterpret_cast<const bf16x8*>(stage + sw_off(rk, 4 * c + lg));
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt) s[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int rt = 0; rt < NTW; ++rt) {
+        bf16x8 b;
+        if constexpr (QL) b = *reinterpret_cast<const bf16x8*>(qs + sw_off((rg * NTW + rt) * 16 + ln, 4 * c + lg));
+        else b = qf[rt][c];
+        s[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[c], b, s[rt], 0, 0, 0);
+      }
+  };
+
+  auto softmax_pv = [&](int tt, const char* stage, f32x4* s) {
     const char* Vs = stage + TILEB;
     const int tile_base = key_begin + tt * TK;
     const int kb = kg * 16;
-    const int rk = kb + ln;
-    bf16x8 kf[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) kf[c] = *reinterpret_cast<const bf16x8*>(Ks + sw_off(rk, 4 * c + lg));
     // V^T operand of d-tile t: lane (ln, lg) gets V[kb + 4lg + j][16t + ln], j < 4
     const int rv = kb + 4 * lg + (ln >> 2);
     i16x4 vf[8];
@@ -358,47 +444,38 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       const char* p = Vs + sw_off(rv, 2 * t + ((ln >> 1) & 1)) + ((ln & 1) << 3);
       vf[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
     }
-    // S^T for every row tile of the wave, the accumulation chains interleaved
-    f32x4 s[NTW];
 #pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) s[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < NTW; ++rt)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+      for (int i = 0; i < 4; ++i) s[rt][i] *= scale_log2;
+    if (tile_base + TK > key_end || tile_base + TK - 1 > causal_off) {   // wave-uniform
+      const int key0 = tile_base + kb + 4 * lg;
 #pragma unroll
-      for (int rt = 0; rt < NTW; ++rt) {
-        bf16x8 b;
-        if constexpr (C::kQLds) b = *reinterpret_cast<const bf16x8*>(qs + sw_off((rg * NTW + rt) * 16 + ln, 4 * c + lg));
-        else b = qreg[c];
-        s[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[c], b, s[rt], 0, 0, 0);
-      }
-    }
-    const bool need_mask = (tile_base + TK > key_end) || (tile_base + TK - 1 > causal_off);
-    const int key0 = tile_base + kb + 4 * lg;
-    float mt[NTW];
+      for (int rt = 0; rt < NTW; ++rt)
 #pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[rt][i] *= scale_log2;
-        if (need_mask) {
+        for (int i = 0; i < 4; ++i) {
           const int key = key0 + i;
-          if (key >= key_end || key > lim[rt]) s[rt][i] = -INFINITY;
+          s[rt][i] = (key < key_end && key <= lim[rt]) ? s[rt][i] : -INFINITY;
         }
-      }
-      mt[rt] = xor32_max(xor16_max(fmaxf(fmaxf(s[rt][0], s[rt][1]), fmaxf(s[rt][2], s[rt][3]))));
     }
-    // The running max is raised only when a score exceeds it by more than
-    // kRescaleSlack (log2 units): probabilities stay <= 2^kRescaleSlack and the
-    // accumulators are rescaled rarely (one wave-uniform branch per tile).
+    // Per-lane max against the running max; the running max is raised
+    // (cross-lane reduction + rescale, one wave-uniform branch) only when a
+    // score exceeds it by more than kRescaleSlack, so probabilities stay
+    // <= 2^kRescaleSlack and the common path has no cross-lane traffic.
+    float lm[NTW];
     bool rise = false;
 #pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) rise |= mt[rt] > m_run[rt] + kRescaleSlack;
+    for (int rt = 0; rt < NTW; ++rt) {
+      lm[rt] = fmaxf(fmaxf(s[rt][0], s[rt][1]), fmaxf(s[rt][2], s[rt][3]));
+      rise |= lm[rt] > m_run[rt] + kRescaleSlack;
+    }
     if (__ballot(rise)) {
 #pragma unroll
       for (int rt = 0; rt < NTW; ++rt) {
-        const float m_new = mt[rt] > m_run[rt] + kRescaleSlack ? mt[rt] : m_run[rt];
+        const float mt = xor32_max(xor16_max(lm[rt]));
+        const float m_new = mt > m_run[rt] + kRescaleSlack ? mt : m_run[rt];
         const float alpha = fast_exp2(m_run[rt] - m_new);
-        l_run[rt] *= alpha;
+        lsum[rt] *= alpha;
 #pragma unroll
         for (int d = 0; d < 8; ++d) acc[rt][d] *= alpha;
         m_run[rt] = m_new;
@@ -407,12 +484,13 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     i16x4 pb[NTW];
 #pragma unroll
     for (int rt = 0; rt < NTW; ++rt) {
-      f32x4 p;
+      float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[rt][i] - m_run[rt]);
-      l_run[rt] += (p[0] + p[1]) + (p[2] + p[3]);
-      pb[rt] = __builtin_bit_cast(i16x4, __builtin_convertvector(p, bf16x4));
+      pb[rt] = pack_bf16x4(p[0], p[1], p[2], p[3]);
     }
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt) lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ones, pb[rt], lsum[rt], 0, 0, 0);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -420,33 +498,30 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
         acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[t], pb[rt], acc[rt][t], 0, 0, 0);
   };
 
-  // Tile tt: wait for its DMA, barrier (every wave is also done reading the
-  // stage of tile tt-1), compute, then refill that stage with tile tt+3. The
-  // refill is issued after the compute's LDS reads so that none of them has
-  // to wait for it.
-  auto step = [&](int tt, const char* cur, char* nxt) {
-    if (tt >= ntiles) return;
-    wait_vm_ahead<C::kLoadsPerTile>(min(ntiles - 1 - tt, 2));
-    __builtin_amdgcn_s_barrier();
-    compute(tt, cur);
-    if (tt + 3 < ntiles) issue(tt + 3, nxt);
+  auto step = [&](int u, const char* cur, const char* prev, char* ahead2, f32x4* s_new, f32x4* s_old) {
+    if (u > ntiles) return;
+    if (u < ntiles) wait_vm_ahead<C::kLoadsPerTile>(u + 1 < ntiles ? 1 : 0);
+    wg_barrier();
+    if (u + 2 < ntiles) issue(u + 2, ahead2);
+    if (u < ntiles) qk(cur, s_new);
+    if (u > 0) softmax_pv(u - 1, prev, s_old);
   };
 
   issue(0, st0);
   if (ntiles > 1) issue(1, st1);
-  if (ntiles > 2) issue(2, st2);
-  for (int t = 0; t < ntiles; t += NSTAGE) {
-    step(t, st0, st3);
-    step(t + 1, st1, st0);
-    step(t + 2, st2, st1);
-    step(t + 3, st3, st2);
+  for (int u = 0; u <= ntiles; u += NSTAGE) {
+    step(u, st0, st3, st2, sA, sB);
+    step(u + 1, st1, st0, st3, sB, sA);
+    step(u + 2, st2, st1, st0, sA, sB);
+    step(u + 3, st3, st2, st1, sB, sA);
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
 
   // ---- merge the four key-waves of each row group: row tiles 0-2 in st0, 3-5 in st1 ----
+  float l_run[NTW];
 #pragma unroll
-  for (int rt = 0; rt < NTW; ++rt) l_run[rt] = xor32_sum(xor16_sum(l_run[rt]));
+  for (int rt = 0; rt < NTW; ++rt) l_run[rt] = lsum[rt][0];
   if (lg == 0) {
 #pragma unroll
     for (int rt = 0; rt < NTW; ++rt)
@@ -736,7 +811,8 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   const dim3 grid(p.n_split, n_kv);
   if (dtype == STD_BF16) {
     constexpr int RG = NT >= 3 ? 2 : 1;   // second row group of waves once a wave would carry > 2 row tiles
-    hipLaunchKernelGGL((attn_bf16_kernel<NT, RG>), grid, dim3(Bf16Cfg<NT, RG>::kThreads), 0, st,
+    constexpr bool QL = RG == 2;
+    hipLaunchKernelGGL((attn_bf16_kernel<NT, RG, QL>), grid, dim3(Bf16Cfg<NT, RG, QL>::kThreads), 0, st,
                        static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                        static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
                        p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
