@@ -132,57 +132,98 @@ __device__ void finish_split(OPtr So, const float2* ml_f, T* __restrict__ out, f
   }
 }
 
-// Standalone merge: grid (R, n_kv), block D. Weights of the n_split partials
-// of one row are computed once in LDS, then every head-dim element sums its
-// column in split order.
+// Standalone merge: grid (R, n_kv), block kMergeThreads = 8 split groups x
+// 32 float4 lanes of the head dim. Every load is issued up front (a thread's
+// first kMergePrefetch partials together with the (m, l) statistics), so the
+// kernel costs about one memory round trip. Group sg sums splits sg, sg + 8,
+// ... in order and the eight group sums are added in group order, so the
+// result is deterministic.
+constexpr int kMergeGroups = 8;
+constexpr int kMergeThreads = kMergeGroups * (D / 4);
+constexpr int kMergePrefetch = 8;
+
 template <typename T>
-__global__ void __launch_bounds__(D)
+__global__ void __launch_bounds__(kMergeThreads)
 attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
                   int n_split, int q_len, int group) {
   __shared__ float wts[kMaxSplit];
-  __shared__ float red[D / 64];
+  __shared__ float red[2][kMergeThreads / 64];
+  __shared__ f32x4 part[kMergeGroups][D / 4];
   const int r = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int d4 = tid & (D / 4 - 1), sg = tid / (D / 4);
   const int R = group * q_len;
   const long long base = (long long)g * n_split * R + r;
+  const f32x4* col = reinterpret_cast<const f32x4*>(ws_o + base * D) + d4;
+  const long long step = (long long)R * (D / 4);
+  f32x4 pre[kMergePrefetch];
+#pragma unroll
+  for (int j = 0; j < kMergePrefetch; ++j) {
+    const int sp = sg + j * kMergeGroups;
+    pre[j] = sp < n_split ? col[sp * step] : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  constexpr int kMlPerThread = kMaxSplit / kMergeThreads;
+  float2 mls[kMlPerThread];
   float m = -1e30f;
-  for (int s = tid; s < n_split; s += D) m = fmaxf(m, ws_ml[base + (long long)s * R].x);
+#pragma unroll
+  for (int i = 0; i < kMlPerThread; ++i) {
+    const int sp = tid + i * kMergeThreads;
+    mls[i] = sp < n_split ? ws_ml[base + (long long)sp * R] : make_float2(-1e30f, 0.f);
+    m = fmaxf(m, mls[i].x);
+  }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-  if (lane == 0) red[wv] = m;
+  if (lane == 0) red[0][wv] = m;
   __syncthreads();
-  float M = red[0];
+  float M = red[0][0];
 #pragma unroll
-  for (int i = 1; i < D / 64; ++i) M = fmaxf(M, red[i]);
-  __syncthreads();
+  for (int i = 1; i < kMergeThreads / 64; ++i) M = fmaxf(M, red[0][i]);
   float l = 0.f;
-  for (int s = tid; s < n_split; s += D) {
-    const float2 ml = ws_ml[base + (long long)s * R];
-    const float e = fast_exp2(ml.x - M);
-    wts[s] = e;
-    l += ml.y * e;
+#pragma unroll
+  for (int i = 0; i < kMlPerThread; ++i) {
+    const int sp = tid + i * kMergeThreads;
+    if (sp < n_split) {
+      const float e = fast_exp2(mls[i].x - M);
+      wts[sp] = e;
+      l += mls[i].y * e;
+    }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
-  if (lane == 0) red[wv] = l;
+  if (lane == 0) red[1][wv] = l;
   __syncthreads();
-  float L = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) L += red[i];
-  float o = 0.f;
-  const float* col = ws_o + base * D + tid;
-  const long long step = (long long)R * D;
-  int s = 0;
-  for (; s + 4 <= n_split; s += 4) {
-    const float a0 = col[(s + 0) * step], a1 = col[(s + 1) * step];
-    const float a2 = col[(s + 2) * step], a3 = col[(s + 3) * step];
-    o += a0 * wts[s];
-    o += a1 * wts[s + 1];
-    o += a2 * wts[s + 2];
-    o += a3 * wts[s + 3];
+  for (int j = 0; j < kMergePrefetch; ++j) {
+    const int sp = sg + j * kMergeGroups;
+    if (sp < n_split) o += pre[j] * wts[sp];
   }
-  for (; s < n_split; ++s) o += col[s * step] * wts[s];
-  const int hl = r / q_len, i = r - hl * q_len;
-  out[((long long)(g * group + hl) * q_len + i) * D + tid] = from_f32<T>(o / L);
+  for (int s0 = kMergePrefetch * kMergeGroups; s0 < n_split; s0 += 4 * kMergeGroups) {
+    f32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int sp = s0 + sg + j * kMergeGroups;
+      v[j] = sp < n_split ? col[sp * step] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int sp = s0 + sg + j * kMergeGroups;
+      if (sp < n_split) o += v[j] * wts[sp];
+    }
+  }
+  part[sg][d4] = o;
+  __syncthreads();
+  if (sg == 0) {
+    float L = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMergeThreads / 64; ++i) L += red[1][i];
+    f32x4 t = part[0][d4];
+#pragma unroll
+    for (int k = 1; k < kMergeGroups; ++k) t += part[k][d4];
+    const int hl = r / q_len, i = r - hl * q_len;
+    T* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(t[e] / L);
+  }
 }
 
 // ===========================================================================
@@ -219,9 +260,17 @@ constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) 
 // the M0 write before an LDS DMA and an SGPR operand written by a VALU
 // instruction (v_readfirstlane) shortly before a VMEM instruction reads it.
 __device__ __forceinline__ void lds_dma16_sbase(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  // readfirstlane pins the wave-uniform operands to SGPRs even where the
+  // compiler cannot prove them uniform (it folds away when they already are).
+  const uint64_t b = reinterpret_cast<uint64_t>(sbase);
+  // (readfirstlane returns int: widen through uint32_t, never sign-extend.)
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  const uint64_t base = static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+  const uint32_t lds = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lds_base));
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(voff), "s"(sbase), "s"(lds_base)
+               : "v"(voff), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 
@@ -301,10 +350,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
                  long long n_hs, long long n_rs, int n_new) {
   using C = Bf16Cfg<NT, RG, QL>;
   constexpr int NTW = C::NTW;
-  __shared__ __align__(16) char st0[STAGEB];
-  __shared__ __align__(16) char st1[STAGEB];
-  __shared__ __align__(16) char st2[STAGEB];
-  __shared__ __align__(16) char st3[STAGEB];
+  __shared__ __align__(16) char ring[NSTAGE * STAGEB];
   __shared__ __align__(16) char qs[C::kQBytes];
   __shared__ float2 ml_w[WAVES * C::kRowTiles * 16];
   __shared__ float2 ml_f[C::kRowTiles * 16];
@@ -326,61 +372,6 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     append_rows<bf16_t>(kh, vh, new_k, new_v, n_hs, n_rs, g, n_new, kv_len, key_begin, key_end, C::kThreads);
     __syncthreads();
   }
-
-  int lim[NTW];
-#pragma unroll
-  for (int rt = 0; rt < NTW; ++rt) {
-    const int r = (rg * NTW + rt) * 16 + ln;
-    lim[rt] = r < R ? causal_off + (r % q_len) : INT_MAX;
-  }
-  // Q^T operand of row tile rt, 32-wide chunk c: lane (ln, lg) holds
-  // q[row][32c + 8lg, +8) of row (rg*NTW + rt)*16 + ln; padding rows are 0.
-  bf16x8 qf[C::kQRegTiles][4];
-  if constexpr (QL) {
-    for (int idx = tid; idx < C::kRowTiles * 16 * 16; idx += C::kThreads) {
-      const int r = idx >> 4, ch = idx & 15;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (r < R) {
-        const int hl = r / q_len, i = r - hl * q_len;
-        val = *reinterpret_cast<const uint4*>(q + ((long long)(g * group + hl) * q_len + i) * D + ch * 8);
-      }
-      *reinterpret_cast<uint4*>(qs + sw_off(r, ch)) = val;
-    }
-    __syncthreads();
-  } else {
-#pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) {
-      const int r = (rg * NTW + rt) * 16 + ln;
-      if (r < R) {
-        const int hl = r / q_len, i = r - hl * q_len;
-        const bf16_t* row = q + ((long long)(g * group + hl) * q_len + i) * D;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qf[rt][c] = *reinterpret_cast<const bf16x8*>(row + 32 * c + 8 * lg);
-      } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qf[rt][c] = bf16x8{};
-      }
-    }
-    // Retire the query loads before the DMA ring starts: the compiler counts
-    // only its own loads, and a wait for them placed after ring DMAs would
-    // drain the ring.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  }
-
-  // Running statistics in the log2 domain (scores pre-multiplied by
-  // scale*log2(e)): m_run is the running max, and the row sums are
-  // accumulated by an MFMA against a ones operand (all rows of lsum equal the
-  // row sum of the bf16 probabilities used for PV).
-  float m_run[NTW];
-  f32x4 acc[NTW][8], lsum[NTW];
-#pragma unroll
-  for (int rt = 0; rt < NTW; ++rt) {
-    m_run[rt] = -1e30f;
-    lsum[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  const i16x4 ones = {0x3f80, 0x3f80, 0x3f80, 0x3f80};   // bf16 1.0
 
   // Each wave DMAs kSegsPerWave 1 KiB segments (4 rows) of K and of V per
   // tile. Lane l fills row 4*seg + l/16 at physical chunk l%16, i.e. logical
@@ -406,6 +397,74 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       lds_dma16_sbase(vt, off, dst + TILEB);
     }
   };
+
+  // The first two tiles are in flight while the queries are staged.
+  auto stage = [&](int u) { return ring + (u & (NSTAGE - 1)) * STAGEB; };
+  issue(0, stage(0));
+  if (ntiles > 1) issue(1, stage(1));
+
+  int lim[NTW];
+#pragma unroll
+  for (int rt = 0; rt < NTW; ++rt) {
+    const int r = (rg * NTW + rt) * 16 + ln;
+    lim[rt] = r < R ? causal_off + (r % q_len) : INT_MAX;
+  }
+  // Q^T operand of row tile rt, 32-wide chunk c: lane (ln, lg) holds
+  // q[row][32c + 8lg, +8) of row (rg*NTW + rt)*16 + ln; padding rows are 0.
+  bf16x8 qf[C::kQRegTiles][4];
+  if constexpr (QL) {
+    // kRowTiles * 16 rows of 16 chunks over kThreads threads: exactly NTW
+    // chunks per thread, all loads issued before the first LDS store.
+    uint4 qv[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int idx = tid + j * C::kThreads, r = idx >> 4, ch = idx & 15;
+      qv[j] = make_uint4(0, 0, 0, 0);
+      if (r < R) {
+        const int hl = r / q_len, i = r - hl * q_len;
+        qv[j] = *reinterpret_cast<const uint4*>(q + ((long long)(g * group + hl) * q_len + i) * D + ch * 8);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int idx = tid + j * C::kThreads;
+      *reinterpret_cast<uint4*>(qs + sw_off(idx >> 4, idx & 15)) = qv[j];
+    }
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int rt = 0; rt < NTW; ++rt) {
+      const int r = (rg * NTW + rt) * 16 + ln;
+      if (r < R) {
+        const int hl = r / q_len, i = r - hl * q_len;
+        const bf16_t* row = q + ((long long)(g * group + hl) * q_len + i) * D;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qf[rt][c] = *reinterpret_cast<const bf16x8*>(row + 32 * c + 8 * lg);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qf[rt][c] = bf16x8{};
+      }
+    }
+    // Retire the query loads (and with them the two ring tiles issued
+    // before them) here: the compiler counts only its own loads, and a wait
+    // for them placed inside the loop would drain the ring there.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+
+  // Running statistics in the log2 domain (scores pre-multiplied by
+  // scale*log2(e)): m_run is the running max, and the row sums are
+  // accumulated by an MFMA against a ones operand (all rows of lsum equal the
+  // row sum of the bf16 probabilities used for PV).
+  float m_run[NTW];
+  f32x4 acc[NTW][8], lsum[NTW];
+#pragma unroll
+  for (int rt = 0; rt < NTW; ++rt) {
+    m_run[rt] = -1e30f;
+    lsum[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const i16x4 ones = {0x3f80, 0x3f80, 0x3f80, 0x3f80};   // bf16 1.0
 
   // Software pipeline, one step per tile u (steps 0..ntiles): after the
   // barrier, tile u+2 is prefetched into the stage tile u-2 used (every wave
@@ -507,18 +566,18 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     if (u > 0) softmax_pv(u - 1, prev, s_old);
   };
 
-  issue(0, st0);
-  if (ntiles > 1) issue(1, st1);
-  for (int u = 0; u <= ntiles; u += NSTAGE) {
-    step(u, st0, st3, st2, sA, sB);
-    step(u + 1, st1, st0, st3, sB, sA);
-    step(u + 2, st2, st1, st0, sA, sB);
-    step(u + 3, st3, st2, st1, sB, sA);
+  // Tile u lives in ring stage u % NSTAGE (tiles 0 and 1 were issued before
+  // the query staging). The loop is unrolled by two only for the score
+  // ping-pong; stage addresses are computed at run time, which keeps the loop
+  // body small (it is fetched cold by every CU).
+  for (int u = 0; u <= ntiles; u += 2) {
+    step(u, stage(u), stage(u + 3), stage(u + 2), sA, sB);
+    step(u + 1, stage(u + 1), stage(u), stage(u + 3), sB, sA);
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
 
-  // ---- merge the four key-waves of each row group: row tiles 0-2 in st0, 3-5 in st1 ----
+  // ---- merge the four key-waves of each row group: row tiles 0-2 in stage 0, 3-5 in stage 1 ----
   float l_run[NTW];
 #pragma unroll
   for (int rt = 0; rt < NTW; ++rt) l_run[rt] = lsum[rt][0];
@@ -546,7 +605,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   }
   auto orow = [&](int r) -> float* {
     const int rt = r >> 4;
-    char* base = rt < 3 ? st0 + rt * OTILE_BYTES : st1 + (rt - 3) * OTILE_BYTES;
+    char* base = ring + (rt < 3 ? rt * OTILE_BYTES : STAGEB + (rt - 3) * OTILE_BYTES);
     return reinterpret_cast<float*>(base) + (r & 15) * OROW;
   };
 #pragma unroll
@@ -826,10 +885,10 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   int s = launch_status();
   if (s != 0 || p.n_split == 1) return s;
   if (dtype == STD_BF16)
-    hipLaunchKernelGGL((attn_merge_kernel<bf16_t>), dim3(R, n_kv), dim3(D), 0, st, ws_o, ws_ml,
+    hipLaunchKernelGGL((attn_merge_kernel<bf16_t>), dim3(R, n_kv), dim3(kMergeThreads), 0, st, ws_o, ws_ml,
                        static_cast<bf16_t*>(out), p.n_split, q_len, group);
   else
-    hipLaunchKernelGGL((attn_merge_kernel<float>), dim3(R, n_kv), dim3(D), 0, st, ws_o, ws_ml,
+    hipLaunchKernelGGL((attn_merge_kernel<float>), dim3(R, n_kv), dim3(kMergeThreads), 0, st, ws_o, ws_ml,
                        static_cast<float*>(out), p.n_split, q_len, group);
   return launch_status();
 }
