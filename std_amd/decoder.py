@@ -1,0 +1,224 @@
+"""A random-init Qwen2.5-VL-7B-shaped language decoder for the end-to-end
+self-speculative decode (the model side of std_qwen25vl.py's loop).
+
+Architecture (Qwen2.5-VL-7B language model, modeling_qwen2_5_vl.py):
+RMSNorm -> q/k/v projections with bias -> rotary embedding -> GQA attention
+-> o_proj; RMSNorm -> SwiGLU MLP; final RMSNorm -> untied lm_head. With the
+reference's position ids (three identical rows, modeling_qwen2_5_vl.py:1368-1384)
+the multimodal rotary embedding with mrope_section [16, 24, 24] equals the
+1-D rotary embedding (theta 1e6) used here.
+
+Attention on the decode hot path runs in libstdhip.so:
+  * q_len == 1 (sparse draft over the compact cache, or dense AR decode):
+    ``ops.gqa_decode_append`` writes the new K/V row and attends, one launch;
+  * 1 < q_len <= 96 / group (dense verify of gamma + 1 rows):
+    ``ops.verify_attention_append`` (offset-causal, one launch).
+Longer inputs (the prompt prefill, which is not part of the decode path) use
+chunked fp32 matrix products in torch.
+
+Dense GEMMs/GEMVs, norms and the MLP run in torch (hipBLASLt).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import ops
+from .kv_cache import KVCache
+
+MAX_FUSED_ROWS = 96   # query rows per KV head served by one verify launch
+
+
+@dataclass
+class DecoderConfig:
+    num_hidden_layers: int = 28
+    hidden_size: int = 3584
+    num_attention_heads: int = 28
+    num_key_value_heads: int = 4
+    intermediate_size: int = 18944
+    vocab_size: int = 152064
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1000000.0
+    max_position_embeddings: int = 128000
+    init_std: float = 0.02
+    video_token_id: int = 151656     # benchmark_std.py:44
+    eos_token_id: int = 151645
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+    @classmethod
+    def qwen25vl_7b(cls) -> "DecoderConfig":
+        return cls()
+
+    @classmethod
+    def tiny(cls, layers: int = 2, vocab: int = 2048) -> "DecoderConfig":
+        """7 query heads / 1 KV head of dim 128 (the GQA group of the 7B model)."""
+        return cls(num_hidden_layers=layers, hidden_size=7 * 128, num_attention_heads=7, num_key_value_heads=1,
+                   intermediate_size=1536, vocab_size=vocab, video_token_id=vocab - 2, eos_token_id=vocab - 1,
+                   max_position_embeddings=8192)
+
+
+class RandomDecoder:
+    """Weights ~ N(0, init_std) (norm weights 1), drawn on the target device
+    from one seeded generator in a fixed order."""
+
+    def __init__(self, config: DecoderConfig, device: torch.device, dtype: torch.dtype = torch.bfloat16,
+                 seed: int = 5001):
+        if config.head_dim != ops.HEAD_DIM:
+            raise ValueError(f"head_dim {config.head_dim} unsupported (the HIP path is built for 128)")
+        if config.num_attention_heads % config.num_key_value_heads:
+            raise ValueError("query heads must be a multiple of KV heads")
+        self.config = config
+        self.device = torch.device(device)
+        self.dtype = dtype
+        c = config
+        gen = torch.Generator(device=self.device).manual_seed(seed)
+
+        def w(*shape):
+            return (torch.randn(*shape, generator=gen, device=self.device, dtype=torch.float32)
+                    * c.init_std).to(dtype)
+
+        hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        self.embed_tokens = w(c.vocab_size, c.hidden_size)
+        self.layers = []
+        for _ in range(c.num_hidden_layers):
+            self.layers.append({
+                "qkv_w": w((hq + 2 * hkv) * d, c.hidden_size),     # q_proj | k_proj | v_proj rows
+                "qkv_b": w((hq + 2 * hkv) * d),
+                "o_w": w(c.hidden_size, hq * d),
+                "gate_up_w": w(2 * c.intermediate_size, c.hidden_size),
+                "down_w": w(c.hidden_size, c.intermediate_size),
+                "ln1": torch.ones(c.hidden_size, device=self.device, dtype=dtype),
+                "ln2": torch.ones(c.hidden_size, device=self.device, dtype=dtype),
+            })
+        self.norm = torch.ones(c.hidden_size, device=self.device, dtype=dtype)
+        self.lm_head = w(c.vocab_size, c.hidden_size)
+        inv = 1.0 / (c.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
+        self.inv_freq = inv.to(torch.float32).to(self.device)
+        self.sparse_controller = None     # set by SparseDraftController.install()
+        self.capture_text_queries = False
+        self.captured_queries: List[Optional[torch.Tensor]] = [None] * c.num_hidden_layers
+
+    # -- pieces ---------------------------------------------------------------
+    def _rms_norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.config.rms_norm_eps)
+        return weight * xf.to(x.dtype)
+
+    def _rope(self, position_ids: torch.Tensor):
+        freqs = position_ids.to(torch.float32)[:, None] * self.inv_freq[None, :]
+        emb = torch.cat([freqs, freqs], dim=-1)
+        return emb.cos().to(self.dtype), emb.sin().to(self.dtype)
+
+    @staticmethod
+    def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+        h = x.shape[-1] // 2
+        return torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+
+    def embed(self, input_ids: torch.Tensor, visual_embeds: Optional[torch.Tensor] = None) -> torch.Tensor:
+        x = self.embed_tokens[input_ids]                      # [1, n, hidden]
+        if visual_embeds is not None:
+            vis = input_ids[0] == self.config.video_token_id
+            n_vis = int(vis.sum())
+            if n_vis:
+                if visual_embeds.shape[0] < n_vis:
+                    raise ValueError("fewer visual embeddings than video tokens")
+                x[0, vis] = visual_embeds[:n_vis].to(x.dtype)
+        return x
+
+    def _prefill_attention(self, q, k_new, v_new, kc: KVCache, vc: KVCache, chunk: int = 512) -> torch.Tensor:
+        """Causal attention of n prompt rows over the cache (torch, fp32)."""
+        c = self.config
+        g_size = c.num_attention_heads // c.num_key_value_heads
+        past = kc.length
+        n = q.shape[2]
+        kc.cat(k_new)
+        vc.cat(v_new)
+        out = torch.empty_like(q)
+        scale = 1.0 / math.sqrt(c.head_dim)
+        for g in range(c.num_key_value_heads):
+            for c0 in range(0, n, chunk):
+                c1 = min(n, c0 + chunk)
+                s_len = past + c1                                           # keys visible to the chunk
+                kt = kc.data[0, g, :s_len].float().t().contiguous()          # [D, S]
+                vg = vc.data[0, g, :s_len].float()                            # [S, D]
+                qg = q[0, g * g_size:(g + 1) * g_size, c0:c1].float()        # [G, m, D]
+                s = (qg.reshape(-1, c.head_dim) @ kt).view(g_size, c1 - c0, s_len) * scale
+                qpos = past + torch.arange(c0, c1, device=q.device)
+                kpos = torch.arange(s_len, device=q.device)
+                s.masked_fill_((kpos[None, :] > qpos[:, None])[None], float("-inf"))
+                p = torch.softmax(s, dim=-1)
+                o = p.reshape(-1, s_len) @ vg
+                out[0, g * g_size:(g + 1) * g_size, c0:c1] = o.view(g_size, c1 - c0, c.head_dim).to(q.dtype)
+        return out
+
+    def _attention(self, li: int, h: torch.Tensor, cos, sin, kc: KVCache, vc: KVCache) -> torch.Tensor:
+        c = self.config
+        p = self.layers[li]
+        n = h.shape[1]
+        hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        qkv = F.linear(h, p["qkv_w"], p["qkv_b"])                            # [1, n, (hq + 2hkv) d]
+        q = qkv[..., :hq * d].view(1, n, hq, d).transpose(1, 2)
+        k = qkv[..., hq * d:(hq + hkv) * d].view(1, n, hkv, d).transpose(1, 2)
+        v = qkv[..., (hq + hkv) * d:].view(1, n, hkv, d).transpose(1, 2)
+        q = (q * cos + self._rotate_half(q) * sin).contiguous()
+        k = (k * cos + self._rotate_half(k) * sin).contiguous()
+        v = v.contiguous()
+        if self.capture_text_queries:
+            self.captured_queries[li] = q
+        controller = self.sparse_controller
+        if controller is not None and controller.enabled and n != 1:
+            raise RuntimeError("Sparse draft attention currently expects autoregressive q_len=1 calls.")
+        pos = kc.length
+        if n == 1:
+            out = ops.gqa_decode_append(q, kc.data, vc.data, k, v, kv_len=pos + 1)
+            kc.advance(1)
+            vc.advance(1)
+        elif n * (hq // hkv) <= MAX_FUSED_ROWS:
+            out = ops.verify_attention_append(q, kc.data, vc.data, k, v, kv_len=pos + n)
+            kc.advance(n)
+            vc.advance(n)
+        else:
+            out = self._prefill_attention(q, k, v, kc, vc)
+        out = out.transpose(1, 2).reshape(1, n, hq * d)
+        return F.linear(out, p["o_w"])
+
+    def _mlp(self, li: int, h: torch.Tensor) -> torch.Tensor:
+        p = self.layers[li]
+        gu = F.linear(h, p["gate_up_w"])
+        gate, up = gu.chunk(2, dim=-1)
+        return F.linear(F.silu(gate) * up, p["down_w"])
+
+    # -- forward ----------------------------------------------------------------
+    @torch.inference_mode()
+    def forward(self, input_ids: torch.Tensor, past_key_values: List[List[KVCache]],
+                position_ids: Optional[torch.Tensor] = None, visual_embeds: Optional[torch.Tensor] = None,
+                all_logits: bool = False, start_position: Optional[int] = None) -> torch.Tensor:
+        """input_ids [1, n]; returns logits [1, n, vocab] if all_logits else
+        [1, 1, vocab] for the last position. Positions default to
+        ``past + arange(n)`` with past = the cache length (the reference's
+        cache_position); the sparse draft passes its original positions, as a
+        tensor or (without a host-to-device copy) as ``start_position``."""
+        n = input_ids.shape[1]
+        x = self.embed(input_ids, visual_embeds)
+        if position_ids is not None:
+            position_ids = position_ids.reshape(-1).to(self.device)
+        else:
+            past = past_key_values[0][0].length if start_position is None else int(start_position)
+            position_ids = torch.arange(past, past + n, device=self.device)
+        cos, sin = self._rope(position_ids)
+        for li in range(self.config.num_hidden_layers):
+            kc, vc = past_key_values[li]
+            x = x + self._attention(li, self._rms_norm(x, self.layers[li]["ln1"]), cos, sin, kc, vc)
+            x = x + self._mlp(li, self._rms_norm(x, self.layers[li]["ln2"]))
+        if not all_logits:
+            x = x[:, -1:]
+        return F.linear(self._rms_norm(x, self.norm), self.lm_head)
+
+    __call__ = forward

@@ -1,0 +1,488 @@
+"""Sparse-to-Dense decoding with the HIP hot path, keeping the interface of
+the reference's std_repro/std_qwen25vl.py.
+
+Same flow and names as the reference: sparse visual KV selection after the
+prompt prefill, a gamma-token draft with sparse attention over a compact
+cache, one parallel dense verification, greedy acceptance, rollback and the
+bonus-token append. What changes underneath:
+
+* selection (``build_sparse_selection``) takes each layer's text-suffix
+  queries and the dense key cache instead of materialised attention
+  probabilities, and keeps the selected indices on the device
+  (``SparseSelection.topk_device``; the reference's per-layer CPU lists are a
+  lazily built host mirror);
+* compaction gathers straight from the dense cache into the sparse cache
+  (no full-prompt copy);
+* ``sparse_attn_mode="hip"``: every attention call of the decode loop is a
+  libstdhip.so launch with the KV append fused in;
+* acceptance and rollback are computed on the device, and draft tokens stay
+  on the device, so a round reads back a handful of int32 values once.
+
+Only ``verify_mode="parallel"`` with ``verify_fallback="none"`` (the
+reference defaults) is provided; the reference's optional sequential
+fallbacks and margin re-runs are outside the hot path and raise.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from . import ops
+from .kv_cache import KVCache, fill_cache_length, initialize_past_key_values
+
+SPARSE_ATTN_MODES = {"hip"}
+
+
+@dataclass
+class SparseSelection:
+    """Per-layer sparse visual KV choices (std_qwen25vl.py:41-50).
+
+    ``topk_device``: int32 [L, Hkv, k] on the device, each row ascending.
+    ``topk_positions`` gives the reference's per-layer CPU int64 [Hkv, k]
+    tensors, built on first access."""
+
+    topk_device: torch.Tensor
+    non_visual_positions: torch.Tensor      # CPU int64 [N_nv], ascending
+    prompt_len: int
+    visual_len: int
+    text_len: int
+    k: int
+    _host: Optional[List[torch.Tensor]] = field(default=None, repr=False)
+
+    @property
+    def topk_positions(self) -> List[torch.Tensor]:
+        if self._host is None:
+            host = self.topk_device.to("cpu", torch.int64)
+            self._host = [host[i] for i in range(host.shape[0])]
+        return self._host
+
+    @property
+    def compact_len(self) -> int:
+        return int(self.non_visual_positions.numel()) + self.k
+
+
+@dataclass
+class GenerateResult:
+    """Same fields as the reference's GenerateResult (std_qwen25vl.py:53-89)."""
+
+    output_ids: torch.Tensor
+    decoding_time: float
+    inference_time: float
+    generate_len: int
+    accepted_draft_tokens: int = 0
+    proposed_draft_tokens: int = 0
+    mean_accept_length: float = 0.0
+    decode_rounds: int = 0
+    final_gamma: int = 0
+    fallback_count: int = 0
+    fallback_accepted_extra: int = 0
+    verify_margin_reruns: int = 0
+    min_verify_margin: float = 0.0
+    gamma_history: List[int] = field(default_factory=list)
+    proposed_lengths: List[int] = field(default_factory=list)
+    accept_lengths: List[int] = field(default_factory=list)
+    pending_lengths: List[int] = field(default_factory=list)
+    draft_time: float = 0.0
+    verify_time: float = 0.0
+    bonus_time: float = 0.0
+    cache_adjust_time: float = 0.0
+    cache_init_time: float = 0.0
+    prefill_time: float = 0.0
+    selection_prefill_time: float = 0.0
+    selection_time: float = 0.0
+    dense_prefill_time: float = 0.0
+    sparse_cache_time: float = 0.0
+
+    @property
+    def acceptance_rate(self) -> float:
+        if self.proposed_draft_tokens == 0:
+            return 0.0
+        return self.accepted_draft_tokens / self.proposed_draft_tokens
+
+
+# ---------------------------------------------------------------------------
+# Prompt layout and the selection size rule.
+
+def get_last_video_idx(input_ids, video_token_id: int) -> int:
+    """Last position of video_token_id, or -1 (specvlm/utils/utils.py:8-15)."""
+    ids = torch.as_tensor(input_ids).reshape(-1)
+    hits = torch.nonzero(ids == video_token_id, as_tuple=False)
+    return int(hits[-1]) if hits.numel() else -1
+
+
+def selection_k(prompt_len: int, text_start: int, n_visual: int, target_k_plus_text: int = 1024,
+                explicit_k: Optional[int] = None) -> Tuple[int, int]:
+    """(text_len, k) with text_len = max(1, P - text_start) and
+    k = min(explicit_k or max(1, target - text_len), n_visual)
+    (std_qwen25vl.py:190-195)."""
+    text_len = max(1, int(prompt_len) - int(text_start))
+    k = int(explicit_k) if explicit_k is not None else max(1, int(target_k_plus_text) - text_len)
+    return text_len, min(k, int(n_visual))
+
+
+def split_video_text_inputs(input_ids: torch.Tensor, video_token_id: int) -> Tuple[int, torch.Tensor, torch.Tensor]:
+    """(text_start, video-prefix ids, text-suffix ids) (std_qwen25vl.py:125-147)."""
+    last = get_last_video_idx(input_ids[0], video_token_id)
+    if last < 0:
+        raise ValueError("No video token found in the prompt; STD visual KV selection requires video input.")
+    text_start = last + 1
+    return text_start, input_ids[:, :text_start], input_ids[:, text_start:]
+
+
+def prefill_prompt(model, inputs: Dict[str, torch.Tensor], past_key_values, video_token_id: int,
+                   capture_text_queries: bool = False):
+    """Video-prefix prefill, then the text suffix (std_qwen25vl.py:150-172).
+    Returns (prompt ids, next token [1, 1] on the device, text_start); with
+    capture_text_queries the text suffix's per-layer queries are kept on the
+    model for selection."""
+    input_ids = inputs["input_ids"].to(model.device)
+    visual = inputs.get("visual_embeds")
+    text_start, video_ids, text_ids = split_video_text_inputs(input_ids, video_token_id)
+    model(video_ids, past_key_values, visual_embeds=visual)
+    model.capture_text_queries = capture_text_queries
+    try:
+        logits = model(text_ids, past_key_values)
+    finally:
+        model.capture_text_queries = False
+    next_token = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+    return input_ids, next_token, text_start
+
+
+# ---------------------------------------------------------------------------
+# Selection and compaction.
+
+def build_sparse_selection(text_queries, key_caches, full_input_ids: torch.Tensor, video_token_id: int,
+                           text_start: int, target_k_plus_text: int = 1024, explicit_k: Optional[int] = None,
+                           num_key_value_heads: int = 4) -> SparseSelection:
+    """Top-k visual positions per (layer, KV head) (std_qwen25vl.py:175-231).
+
+    text_queries[l]: [1, Hq, T, D] text-suffix queries of layer l (RoPE
+    applied); key_caches[l]: [1, Hkv, >= P, D] cache view of layer l. The
+    scores are the reference's head-group and text-row sums of the causal
+    softmax probabilities, computed exactly (fp64) on the device; ties go to
+    the lowest position."""
+    prompt_ids = full_input_ids[0]
+    dev = key_caches[0].device
+    visual = torch.nonzero(prompt_ids == video_token_id, as_tuple=False).flatten()
+    if visual.numel() == 0:
+        raise ValueError("Cannot build sparse selection without visual/video token positions.")
+    non_visual = torch.nonzero(prompt_ids != video_token_id, as_tuple=False).flatten()
+    prompt_len = int(prompt_ids.numel())
+    text_len, k = selection_k(prompt_len, text_start, visual.numel(), target_k_plus_text, explicit_k)
+    visual_i32 = visual.to(dev, torch.int32)
+    layers = []
+    for q_text, key in zip(text_queries, key_caches):
+        if q_text.shape[1] % num_key_value_heads or key.shape[1] != num_key_value_heads:
+            raise ValueError(
+                f"Query heads ({q_text.shape[1]}) must be divisible by KV heads ({num_key_value_heads}).")
+        if q_text.shape[2] != text_len:
+            raise ValueError(f"text queries hold {q_text.shape[2]} rows, the prompt has {text_len}")
+        layers.append(ops.select_topk(q_text.contiguous(), key, int(text_start), visual_i32, k))
+    return SparseSelection(topk_device=torch.stack(layers), non_visual_positions=non_visual.to("cpu", torch.int64),
+                           prompt_len=prompt_len, visual_len=int(visual.numel()), text_len=text_len, k=k)
+
+
+def compact_sparse_prompt_cache(past_key_values, current_length_data: torch.Tensor, selection: SparseSelection,
+                                dense_past_key_values) -> int:
+    """Fill the sparse cache with each head's sorted union of non-visual and
+    selected positions (std_qwen25vl.py:265-298), gathered straight from the
+    dense prompt cache (which replaces copy_prompt_cache, :301-320)."""
+    compact_len = selection.compact_len
+    dev = past_key_values[0][0].data.device
+    non_visual = selection.non_visual_positions.to(dev, torch.int32)
+    for layer_idx, (sparse_layer, dense_layer) in enumerate(zip(past_key_values, dense_past_key_values)):
+        index = ops.build_compact_index(non_visual, selection.topk_device[layer_idx])
+        if index.shape[1] != compact_len:
+            raise RuntimeError("Compacted sparse KV produced an unexpected length.")
+        ops.compact_kv(dense_layer[0].data, dense_layer[1].data, sparse_layer[0].data, sparse_layer[1].data, index)
+    fill_cache_length(current_length_data, compact_len)
+    return compact_len
+
+
+class SparseDraftController:
+    """Routes the model's q_len = 1 attention to the sparse cache with the
+    HIP decode kernel while enabled (std_qwen25vl.py:234-262)."""
+
+    def __init__(self, model, selection: SparseSelection, sparse_attn_mode: str = "hip",
+                 use_compile: bool = False):
+        if sparse_attn_mode not in SPARSE_ATTN_MODES:
+            raise ValueError(f"Unsupported sparse_attn_mode={sparse_attn_mode!r}.")
+        if use_compile:
+            raise ValueError("use_compile is not supported: the HIP decode step is captured with HIP graphs instead")
+        self.model = model
+        self.selection = selection
+        self.sparse_attn_mode = sparse_attn_mode
+        self.enabled = False
+        self._installed = False
+        self.compiled_forward = None
+
+    def install(self) -> None:
+        if self._installed:
+            return
+        self.model.sparse_controller = self
+        self._installed = True
+
+    def set_enabled(self, enabled: bool) -> None:
+        self.enabled = enabled
+
+
+def _token_argmax(logits: torch.Tensor) -> torch.Tensor:
+    return torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+
+
+def _profile_mark(enabled: bool) -> float:
+    if enabled:
+        torch.cuda.synchronize()
+    return time.time()
+
+
+def _draft_tokens(model, first_token: torch.Tensor, gamma: int, past_key_values,
+                  sparse_controller: SparseDraftController, start_position: int) -> torch.Tensor:
+    """gamma sequential sparse forwards (std_qwen25vl.py:531-550); token i is
+    fed at position start_position + i. Returns the drafted tokens as a device
+    int64 tensor [gamma] (no per-token host sync)."""
+    token = first_token.reshape(1, 1)
+    drafted = []
+    sparse_controller.set_enabled(True)
+    try:
+        for offset in range(gamma):
+            drafted.append(token.reshape(1))
+            logits = model(token, past_key_values, start_position=start_position + offset)
+            token = _token_argmax(logits)
+    finally:
+        sparse_controller.set_enabled(False)
+    return torch.cat(drafted)
+
+
+def _append_sparse_tokens(model, tokens: torch.Tensor, past_key_values, sparse_controller: SparseDraftController,
+                          start_position: int) -> torch.Tensor:
+    """Cache the bonus token in the sparse cache (std_qwen25vl.py:474-494)."""
+    sparse_controller.set_enabled(True)
+    try:
+        next_token = None
+        for offset in range(tokens.numel()):
+            logits = model(tokens.reshape(-1)[offset:offset + 1].reshape(1, 1), past_key_values,
+                           start_position=start_position + offset)
+            next_token = _token_argmax(logits)
+    finally:
+        sparse_controller.set_enabled(False)
+    if next_token is None:
+        raise ValueError("Cannot append an empty sparse token sequence.")
+    return next_token
+
+
+def _contains_eos(tokens, eos_token_id: int) -> Optional[int]:
+    for idx, token in enumerate(tokens):
+        if int(token) == eos_token_id:
+            return idx
+    return None
+
+
+def _cache_capacity(prompt_len: int, max_new_tokens: int, gamma: int) -> int:
+    return prompt_len + max_new_tokens + gamma + 2
+
+
+# ---------------------------------------------------------------------------
+# Orchestrators.
+
+@torch.inference_mode()
+def ar_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id: int, eos_token_id: int,
+                         max_new_tokens: int = 256, output_attentions: bool = False, profile_prefill: bool = False,
+                         ignore_eos: bool = False) -> GenerateResult:
+    """Greedy dense decoding with the same two-stage prefill
+    (std_qwen25vl.py:553-606); every decode step is one HIP decode launch per
+    layer over the full dense cache."""
+    del output_attentions
+    torch.cuda.synchronize()
+    start = time.time()
+    prompt_len = int(inputs["input_ids"].shape[1])
+    stage = _profile_mark(profile_prefill)
+    pkv, _, lengths = initialize_past_key_values(model.config, model.device, model.dtype,
+                                                 _cache_capacity(prompt_len, max_new_tokens, 0))
+    cache_init_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
+    stage = _profile_mark(profile_prefill)
+    prompt_ids, next_token, _ = prefill_prompt(model, inputs, pkv, video_token_id)
+    prefill_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
+
+    generated: List[torch.Tensor] = []
+    torch.cuda.synchronize()
+    decode_start = time.time()
+    while len(generated) < max_new_tokens:
+        generated.append(next_token.reshape(1))
+        if not ignore_eos and int(next_token) == eos_token_id:
+            break
+        if len(generated) == max_new_tokens:
+            break
+        next_token = _token_argmax(model(next_token, pkv))
+    torch.cuda.synchronize()
+    end = time.time()
+    gen = torch.cat(generated) if generated else torch.empty(0, dtype=torch.long, device=model.device)
+    out = torch.cat([prompt_ids, gen.reshape(1, -1)], dim=1)
+    return GenerateResult(out, end - decode_start, end - start, int(gen.numel()), cache_init_time=cache_init_time,
+                          prefill_time=prefill_time)
+
+
+@torch.inference_mode()
+def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id: int, eos_token_id: int,
+                          max_new_tokens: int = 256, gamma: int = 9, target_k_plus_text: int = 1024,
+                          explicit_k: Optional[int] = None, verify_mode: str = "parallel",
+                          verify_fallback: str = "none", sequential_fallback_max_accept: int = 1,
+                          profile_decode: bool = False, sparse_attn_mode: str = "hip",
+                          adaptive_gamma_min: Optional[int] = None, adaptive_gamma_mode: str = "accept_len",
+                          copy_sparse_prefill: bool = True, profile_prefill: bool = False,
+                          verify_attn_backend: str = "math", verify_margin_threshold: Optional[float] = None,
+                          use_compile: bool = False, ignore_eos: bool = False
+                          ) -> Tuple[GenerateResult, SparseSelection]:
+    """Sparse-to-Dense greedy decoding (std_qwen25vl.py:609-978)."""
+    if verify_mode != "parallel":
+        raise ValueError(f"Unsupported verify_mode={verify_mode!r}; the HIP path implements 'parallel'.")
+    if verify_fallback != "none" or verify_margin_threshold is not None:
+        raise ValueError("verify fallbacks and margin re-runs are not part of the HIP decode path")
+    if verify_attn_backend not in {"default", "math"}:
+        raise ValueError("verify_attn_backend must be 'default' or 'math' (both run the exact HIP verify).")
+    if adaptive_gamma_min is not None and not (1 <= adaptive_gamma_min <= gamma):
+        raise ValueError("adaptive_gamma_min must be between 1 and gamma.")
+    if adaptive_gamma_mode not in {"accept_len", "conservative"}:
+        raise ValueError("adaptive_gamma_mode must be 'accept_len' or 'conservative'.")
+    if not copy_sparse_prefill:
+        raise ValueError("the sparse cache is always gathered from the dense prefill")
+    del sequential_fallback_max_accept
+    dev = model.device
+
+    torch.cuda.synchronize()
+    start = time.time()
+    prompt_len = int(inputs["input_ids"].shape[1])
+    stage = _profile_mark(profile_prefill)
+    dense_pkv, _, dense_lengths = initialize_past_key_values(model.config, dev, model.dtype,
+                                                             _cache_capacity(prompt_len, max_new_tokens, gamma))
+    cache_init_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
+
+    stage = _profile_mark(profile_prefill)
+    prompt_ids, dense_next, text_start = prefill_prompt(model, inputs, dense_pkv, video_token_id,
+                                                        capture_text_queries=True)
+    selection_prefill_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
+
+    stage = _profile_mark(profile_prefill)
+    queries = model.captured_queries
+    model.captured_queries = [None] * model.config.num_hidden_layers
+    selection = build_sparse_selection(queries, [layer[0].data for layer in dense_pkv], prompt_ids, video_token_id,
+                                       text_start, target_k_plus_text=target_k_plus_text, explicit_k=explicit_k,
+                                       num_key_value_heads=model.config.num_key_value_heads)
+    del queries
+    selection_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
+    controller = SparseDraftController(model, selection, sparse_attn_mode=sparse_attn_mode, use_compile=use_compile)
+    controller.install()
+
+    stage = _profile_mark(profile_prefill)
+    sparse_pkv, _, sparse_lengths = initialize_past_key_values(
+        model.config, dev, model.dtype, _cache_capacity(selection.compact_len, max_new_tokens, gamma))
+    sparse_prompt_len = compact_sparse_prompt_cache(sparse_pkv, sparse_lengths, selection, dense_pkv)
+    sparse_next = dense_next.clone()
+    sparse_cache_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
+
+    generated: List[int] = []
+    accept_lengths: List[int] = []
+    proposed_lengths: List[int] = []
+    pending_lengths: List[int] = []
+    gamma_history: List[int] = []
+    dense_pending: List[int] = []
+    accepted_total = proposed_total = decode_rounds = 0
+    draft_time = verify_time = bonus_time = cache_adjust_time = 0.0
+    current_gamma = gamma
+    dense_next_i32 = dense_next.reshape(1).to(torch.int32)
+
+    torch.cuda.synchronize()
+    decode_start = time.time()
+    while len(generated) < max_new_tokens:
+        decode_rounds += 1
+        remaining = max_new_tokens - len(generated)
+        gamma_history.append(current_gamma)
+        propose_len = min(current_gamma, remaining)
+        context_len = prompt_len + len(generated)
+        dense_cached_len = context_len - len(dense_pending)
+        sparse_prev_len = sparse_prompt_len + len(generated)
+
+        stage = _profile_mark(profile_decode)
+        draft_dev = _draft_tokens(model, sparse_next, propose_len, sparse_pkv, controller, start_position=context_len)
+        draft_time += _profile_mark(profile_decode) - stage
+        proposed_total += propose_len
+        proposed_lengths.append(propose_len)
+        pending_lengths.append(len(dense_pending))
+
+        stage = _profile_mark(profile_decode)
+        if dense_pending:
+            pend = torch.tensor(dense_pending, dtype=torch.long).to(dev, non_blocking=True)
+            verify_ids = torch.cat([pend, draft_dev]).reshape(1, -1)
+        else:
+            verify_ids = draft_dev.reshape(1, -1)
+        logits = model(verify_ids, dense_pkv, all_logits=True)
+        res = ops.greedy_accept(logits[0], draft_dev.to(torch.int32), has_pending=bool(dense_pending),
+                                dense_next=None if dense_pending else dense_next_i32)
+        host = torch.cat([res[:2], draft_dev.to(torch.int32)]).tolist()     # the round's one readback
+        accept_len, bonus_token, draft = host[0], host[1], host[2:]
+        verify_time += _profile_mark(profile_decode) - stage
+        accept_lengths.append(accept_len)
+        accepted_total += accept_len
+        if adaptive_gamma_min is not None:
+            if accept_len < propose_len:
+                if adaptive_gamma_mode == "accept_len":
+                    current_gamma = max(adaptive_gamma_min, accept_len if accept_len > 0 else adaptive_gamma_min)
+                else:
+                    ratio = accept_len / propose_len if propose_len else 0.0
+                    if accept_len == 0:
+                        current_gamma = max(adaptive_gamma_min, current_gamma - 2)
+                    elif ratio < 0.5:
+                        current_gamma = max(adaptive_gamma_min, current_gamma - 1)
+            elif current_gamma < gamma:
+                current_gamma = min(gamma, current_gamma + 1)
+
+        full_append = draft[:accept_len] + [bonus_token]
+        eos_index = None if ignore_eos else _contains_eos(full_append, eos_token_id)
+        if eos_index is not None:
+            full_append = full_append[:eos_index + 1]
+        to_append = full_append[:remaining]
+        generated.extend(int(x) for x in to_append)
+        if len(generated) >= max_new_tokens or (not ignore_eos and to_append and to_append[-1] == eos_token_id):
+            break
+
+        stage = _profile_mark(profile_decode)
+        # Keep the previous pending token and the accepted draft prefix; the
+        # new bonus stays pending until the next verification caches it.
+        fill_cache_length(dense_lengths, dense_cached_len + len(dense_pending) + accept_len)
+        fill_cache_length(sparse_lengths, sparse_prev_len + accept_len)
+        cache_adjust_time += _profile_mark(profile_decode) - stage
+
+        dense_pending = [bonus_token]
+        stage = _profile_mark(profile_decode)
+        bonus_dev = torch.tensor([bonus_token], dtype=torch.long).to(dev, non_blocking=True)
+        sparse_next = _append_sparse_tokens(model, bonus_dev, sparse_pkv, controller,
+                                            start_position=context_len + accept_len)
+        bonus_time += _profile_mark(profile_decode) - stage
+
+    torch.cuda.synchronize()
+    end = time.time()
+    out = torch.cat([prompt_ids, torch.tensor([generated], dtype=torch.long, device=dev)], dim=1)
+    result = GenerateResult(
+        output_ids=out, decoding_time=end - decode_start, inference_time=end - start, generate_len=len(generated),
+        accepted_draft_tokens=accepted_total, proposed_draft_tokens=proposed_total,
+        mean_accept_length=sum(accept_lengths) / len(accept_lengths) if accept_lengths else 0.0,
+        decode_rounds=decode_rounds, final_gamma=current_gamma, gamma_history=gamma_history,
+        proposed_lengths=proposed_lengths, accept_lengths=accept_lengths, pending_lengths=pending_lengths,
+        draft_time=draft_time, verify_time=verify_time, bonus_time=bonus_time, cache_adjust_time=cache_adjust_time,
+        cache_init_time=cache_init_time, prefill_time=selection_prefill_time,
+        selection_prefill_time=selection_prefill_time, selection_time=selection_time, dense_prefill_time=0.0,
+        sparse_cache_time=sparse_cache_time)
+    return result, selection
+
+
+def first_divergence(a: torch.Tensor, b: torch.Tensor) -> Optional[int]:
+    """Index of the first differing generated token, or None (the diagnostic of
+    benchmark_std.py:327-356)."""
+    a, b = a.reshape(-1).tolist(), b.reshape(-1).tolist()
+    for i, (x, y) in enumerate(zip(a, b)):
+        if x != y:
+            return i
+    return None if len(a) == len(b) else min(len(a), len(b))

@@ -1,0 +1,99 @@
+"""End-to-end self-speculative decode on a tiny random decoder with the HIP
+hot path (selection, compaction, sparse draft, parallel verify, greedy
+acceptance, rollback): the std_qwen25vl.py loop through libstdhip.so."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import selection as ref_sel
+from std_amd.decoder import DecoderConfig, RandomDecoder
+from std_amd.kv_cache import initialize_past_key_values
+from std_amd.std_qwen25vl import (ar_generate_qwen25vl, build_sparse_selection, compact_sparse_prompt_cache,
+                                  first_divergence, prefill_prompt, std_generate_qwen25vl)
+from tests.gpu_helpers import announce, dev
+
+pytestmark = pytest.mark.gpu
+
+N_VISUAL, N_TEXT, TARGET = 1000, 24, 256
+
+
+def _inputs(cfg, seed, n_visual=N_VISUAL, n_text=N_TEXT, dtype=torch.float32):
+    gen = torch.Generator().manual_seed(seed)
+    text = torch.randint(0, cfg.vocab_size - 2, (n_text,), generator=gen)
+    ids = torch.cat([torch.full((n_visual,), cfg.video_token_id), text]).view(1, -1)
+    vis = torch.randn(n_visual, cfg.hidden_size, generator=gen)
+    return {"input_ids": ids.to(dev()), "visual_embeds": vis.to(dev(), dtype)}
+
+
+@pytest.fixture(scope="module")
+def tiny32():
+    cfg = DecoderConfig.tiny(layers=2)
+    return cfg, RandomDecoder(cfg, dev(), torch.float32, seed=5001)
+
+
+def test_selection_and_compaction_from_prefill(tiny32):
+    """Selection on the captured text queries equals the oracle bit-exactly;
+    the compact cache rows are bit copies of the dense rows."""
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 11)
+    P = inputs["input_ids"].shape[1]
+    announce(f"e2e selection tiny fp32 P={P}")
+    pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.float32, P + 8)
+    prompt_ids, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
+    queries = list(model.captured_queries)
+    assert text_start == N_VISUAL and queries[0].shape == (1, 7, N_TEXT, 128)
+    sel = build_sparse_selection(queries, [layer[0].data for layer in pkv], prompt_ids, cfg.video_token_id,
+                                 text_start, target_k_plus_text=TARGET, num_key_value_heads=1)
+    want = ref_sel.build_sparse_selection([q.cpu() for q in queries], [layer[0].data[:, :, :P].cpu() for layer in pkv],
+                                          prompt_ids[0].cpu().tolist(), cfg.video_token_id, target_k_plus_text=TARGET)
+    assert (sel.k, sel.text_len, sel.visual_len, sel.prompt_len) == (want["k"], want["text_len"],
+                                                                      want["visual_len"], want["prompt_len"])
+    for layer in range(cfg.num_hidden_layers):
+        np.testing.assert_array_equal(sel.topk_positions[layer].numpy(), want["topk_positions"][layer])
+    sparse, _, sparse_len = initialize_past_key_values(cfg, dev(), torch.float32, sel.compact_len + 4)
+    n = compact_sparse_prompt_cache(sparse, sparse_len, sel, pkv)
+    torch.cuda.synchronize()
+    assert n == N_TEXT + sel.k and all(int(x) == n for x in sparse_len)
+    for layer in range(cfg.num_hidden_layers):
+        idx = ref_sel.compact_index(want["non_visual_positions"], want["topk_positions"][layer][0])
+        for kind in range(2):
+            got = sparse[layer][kind].data[0, 0, :n].cpu()
+            assert torch.equal(got, pkv[layer][kind].data[0, 0, torch.as_tensor(idx)].cpu())
+
+
+def test_std_tokens_equal_dense_ar_fp32(tiny32):
+    """Greedy STD with exact dense verification reproduces dense AR decoding."""
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 5)
+    announce("e2e STD vs AR tiny fp32, 40 tokens, gamma 9")
+    ar = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=40, ignore_eos=True)
+    std, sel = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=40, gamma=9,
+                                     target_k_plus_text=TARGET, ignore_eos=True)
+    assert ar.generate_len == std.generate_len == 40
+    assert first_divergence(std.output_ids, ar.output_ids) is None
+    assert std.decode_rounds == len(std.accept_lengths) == len(std.proposed_lengths)
+    assert std.accepted_draft_tokens == sum(std.accept_lengths)
+    assert std.proposed_draft_tokens == sum(std.proposed_lengths)
+    assert all(0 <= a <= p for a, p in zip(std.accept_lengths, std.proposed_lengths))
+    # every round but the last appends accept + 1 tokens
+    assert sum(a + 1 for a in std.accept_lengths[:-1]) < 40 <= sum(a + 1 for a in std.accept_lengths)
+    assert std.pending_lengths[0] == 0 and all(x == 1 for x in std.pending_lengths[1:])
+    assert sel.k == TARGET - N_TEXT
+
+
+def test_std_runs_bf16_with_eos_stop():
+    """bf16 tiny decoder: the loop's invariants hold and generation stops at
+    the first EOS when ignore_eos is False."""
+    cfg = DecoderConfig.tiny(layers=2)
+    model = RandomDecoder(cfg, dev(), torch.bfloat16, seed=7)
+    inputs = _inputs(cfg, 9, dtype=torch.bfloat16)
+    announce("e2e STD tiny bf16, 32 tokens")
+    std, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=32, gamma=9,
+                                   target_k_plus_text=TARGET, ignore_eos=True)
+    gen = std.output_ids[0, -std.generate_len:].tolist()
+    assert std.generate_len == 32 and std.accepted_draft_tokens == sum(std.accept_lengths)
+    eos = gen[5]                       # pretend the sixth generated token is EOS
+    stop, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, eos, max_new_tokens=32, gamma=9,
+                                    target_k_plus_text=TARGET, ignore_eos=False)
+    got = stop.output_ids[0, -stop.generate_len:].tolist()
+    assert got == gen[:gen.index(eos) + 1]

@@ -1,0 +1,128 @@
+"""Host-side logic of the std_qwen25vl / kv_cache mirror (CPU only: no
+kernel is launched)."""
+import pytest
+import torch
+
+from std_amd import kv_cache
+from std_amd.decoder import DecoderConfig
+from std_amd.std_qwen25vl import (GenerateResult, SparseDraftController, SparseSelection, first_divergence,
+                                  get_last_video_idx, selection_k, split_video_text_inputs, std_generate_qwen25vl)
+
+
+def test_last_video_idx_matches_reverse_scan():
+    """utils.py:8-15: last occurrence, -1 when absent."""
+    assert get_last_video_idx([5, 9, 9, 3, 9, 1], 9) == 4
+    assert get_last_video_idx([1, 2, 3], 9) == -1
+    assert get_last_video_idx(torch.tensor([9]), 9) == 0
+
+
+@pytest.mark.parametrize("prompt_len,text_start,n_visual,target,explicit,expect", [
+    (4096, 3968, 3968, 1024, None, (128, 896)),        # C1/C2/C4 layout
+    (65536, 65408, 65408, 4096, None, (128, 3968)),    # C3
+    (200, 190, 190, 1024, None, (10, 190)),            # k capped by the visual count
+    (100, 100, 100, 1024, None, (1, 100)),             # text_len floors at 1
+    (4096, 3968, 3968, 1024, 7, (128, 7)),             # explicit k wins
+    (4096, 3968, 3968, 100, None, (128, 1)),           # k floors at 1
+])
+def test_selection_k_rule(prompt_len, text_start, n_visual, target, explicit, expect):
+    """std_qwen25vl.py:190-195."""
+    assert selection_k(prompt_len, text_start, n_visual, target, explicit) == expect
+
+
+def test_split_video_text_inputs():
+    ids = torch.tensor([[7, 7, 1, 7, 2, 3]])
+    text_start, video, text = split_video_text_inputs(ids, 7)
+    assert text_start == 4
+    assert video.tolist() == [[7, 7, 1, 7]] and text.tolist() == [[2, 3]]
+    with pytest.raises(ValueError, match="No video token"):
+        split_video_text_inputs(torch.tensor([[1, 2]]), 7)
+
+
+def test_kv_cache_cat_copy_and_overflow():
+    """kv_cache.py:42-69 semantics on CPU tensors."""
+    cfg = DecoderConfig.tiny(layers=2)
+    pkv, data, lengths = kv_cache.initialize_past_key_values(cfg, torch.device("cpu"), torch.float32, 8)
+    assert data.shape == (4, 1, 1, 8, 128) and lengths.shape == (4,) and lengths.dtype == torch.long
+    assert pkv[1][0].data.data_ptr() == data[2].data_ptr() and pkv[1][1].current_length is not None
+    kc = pkv[0][0]
+    rows = torch.arange(3 * 128, dtype=torch.float32).view(1, 1, 3, 128)
+    view = kc.cat(rows)
+    assert kc.length == 3 and view.shape == (1, 1, 3, 128) and torch.equal(view, rows)
+    assert int(lengths[0]) == 3 and int(lengths[1]) == 0          # K and V lengths are independent
+    assert kc.shape == (1, 1, 3, 128)
+    kc.copy(torch.tensor([2, 0]), prev_length=1)
+    assert kc.length == 3
+    assert torch.equal(kc.data[0, 0, 1], rows[0, 0, 2]) and torch.equal(kc.data[0, 0, 2], rows[0, 0, 0])
+    with pytest.raises(RuntimeError, match="overflow"):
+        kc.cat(torch.zeros(1, 1, 6, 128))
+    with pytest.raises(RuntimeError, match="overflow"):
+        kc.advance(6)
+    kv_cache.fill_cache_length(lengths, 5)
+    assert all(int(x) == 5 for x in lengths) and kc.length == 5
+
+
+def test_default_max_cache_len(monkeypatch):
+    monkeypatch.delenv("SPECVLM_MAX_CACHE_LEN", raising=False)
+    assert kv_cache.default_max_cache_len(128000) == 16384
+    assert kv_cache.default_max_cache_len(4096) == 8192
+    monkeypatch.setenv("SPECVLM_MAX_CACHE_LEN", "1000")
+    assert kv_cache.default_max_cache_len(128000) == 1000
+
+
+def test_sparse_selection_host_mirror():
+    topk = torch.tensor([[[3, 5], [1, 4]], [[0, 2], [6, 7]]], dtype=torch.int32)
+    sel = SparseSelection(topk_device=topk, non_visual_positions=torch.tensor([8, 9]), prompt_len=10,
+                          visual_len=8, text_len=2, k=2)
+    host = sel.topk_positions
+    assert len(host) == 2 and host[1].dtype == torch.int64 and host[1].tolist() == [[0, 2], [6, 7]]
+    assert sel.topk_positions is host and sel.compact_len == 4
+
+
+def test_controller_validates_mode():
+    """std_qwen25vl.py:239-240 raises ValueError on an unknown mode."""
+    class Model:
+        sparse_controller = None
+    sel = SparseSelection(torch.zeros(1, 1, 1, dtype=torch.int32), torch.tensor([0]), 2, 1, 1, 1)
+    with pytest.raises(ValueError, match="sparse_attn_mode"):
+        SparseDraftController(Model(), sel, sparse_attn_mode="triton_gqa")
+    m = Model()
+    c = SparseDraftController(m, sel, sparse_attn_mode="hip")
+    c.install()
+    assert m.sparse_controller is c and not c.enabled
+    c.set_enabled(True)
+    assert c.enabled
+
+
+@pytest.mark.parametrize("kwargs", [dict(verify_mode="sequential"), dict(verify_fallback="sequential_on_reject"),
+                                    dict(adaptive_gamma_min=0), dict(verify_attn_backend="flash"),
+                                    dict(copy_sparse_prefill=False)])
+def test_std_generate_rejects_unsupported_options(kwargs):
+    with pytest.raises(ValueError):
+        std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
+
+
+def test_generate_result_fields_and_rate():
+    r = GenerateResult(torch.zeros(1, 3), 1.0, 2.0, 3, accepted_draft_tokens=6, proposed_draft_tokens=8)
+    assert r.acceptance_rate == 0.75
+    assert GenerateResult(torch.zeros(1), 0.0, 0.0, 0).acceptance_rate == 0.0
+    for name in ("accept_lengths", "proposed_lengths", "pending_lengths", "gamma_history", "draft_time",
+                 "verify_time", "bonus_time", "selection_time", "sparse_cache_time"):
+        assert hasattr(r, name)
+
+
+def test_first_divergence():
+    assert first_divergence(torch.tensor([1, 2, 3]), torch.tensor([1, 2, 3])) is None
+    assert first_divergence(torch.tensor([1, 2, 3]), torch.tensor([1, 5, 3])) == 1
+    assert first_divergence(torch.tensor([1, 2]), torch.tensor([1, 2, 3])) == 2
+
+
+def test_7b_config_shapes():
+    """Qwen2.5-VL-7B language model: 6.53 B layer + 0.545 B lm_head parameters."""
+    c = DecoderConfig.qwen25vl_7b()
+    d = c.head_dim
+    per_layer = ((c.num_attention_heads + 2 * c.num_key_value_heads) * d * (c.hidden_size + 1)
+                 + c.hidden_size * c.num_attention_heads * d + 3 * c.hidden_size * c.intermediate_size
+                 + 2 * c.hidden_size)
+    assert d == 128 and c.num_attention_heads // c.num_key_value_heads == 7
+    assert abs(per_layer * c.num_hidden_layers / 1e9 - 6.53) < 0.01
+    assert abs(c.vocab_size * c.hidden_size / 1e9 - 0.545) < 0.001
