@@ -65,6 +65,12 @@ def _attn_workspace(nbytes: int, dev: torch.device) -> int:
     return buf.data_ptr()
 
 
+def same_layout(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Same shape and the same stride in every dimension of size > 1 (the
+    stride of a size-1 dimension is never used to address an element)."""
+    return a.shape == b.shape and all(a.stride(i) == b.stride(i) for i in range(a.dim()) if a.shape[i] > 1)
+
+
 def _check_cache_view(name: str, t: torch.Tensor) -> None:
     """[1, Hkv, S, D] with contiguous rows; any head stride (cache view)."""
     if t.dim() != 4 or t.shape[0] != 1:
@@ -151,7 +157,7 @@ def _attention(fn: str, query, key, value, scale, out, new_key=None, new_value=N
                 raise ValueError(f"{name} must be [1, n_kv, {q_len}, {HEAD_DIM}] with contiguous rows")
             if t.dtype != query.dtype or t.device != query.device:
                 raise TypeError(f"{name} must match the query dtype and device")
-        if new_value.stride() != new_key.stride():
+        if not same_layout(new_key, new_value):
             raise ValueError("new_key and new_value must share strides")
         if value.stride(1) != key.stride(1):
             raise ValueError("key and value caches must share a head stride")
@@ -303,7 +309,7 @@ def kv_append(cache_k: torch.Tensor, cache_v: torch.Tensor, new_k: torch.Tensor,
             raise ValueError(f"{name} must be [1, n_kv, rows, D], got {tuple(t.shape)}")
         if t.stride(3) != 1 or t.dtype != cache_k.dtype:
             raise ValueError(f"{name} must have contiguous head_dim and the cache dtype")
-    if new_v.stride() != new_k.stride() or new_v.shape != new_k.shape:
+    if new_v.shape != new_k.shape or not same_layout(new_k, new_v):
         raise ValueError("new_k and new_v must share shape and strides")
     if length.dtype != torch.int32:
         raise TypeError("length must be a device int32 tensor")

@@ -97,3 +97,20 @@ def test_std_runs_bf16_with_eos_stop():
                                     target_k_plus_text=TARGET, ignore_eos=False)
     got = stop.output_ids[0, -stop.generate_len:].tolist()
     assert got == gen[:gen.index(eos) + 1]
+
+
+def test_full_selection_draft_equals_dense(tiny32):
+    """With k = every visual position the compact cache equals the dense
+    prompt cache, so the sparse draft (original positions, fused append,
+    rollback, bonus append) must reproduce the dense model: every drafted
+    token is accepted."""
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 21, n_visual=300, n_text=20)
+    announce("e2e STD tiny fp32, k = all visual positions")
+    std, sel = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=36, gamma=5,
+                                     explicit_k=300, ignore_eos=True)
+    assert sel.k == 300 and sel.compact_len == 320
+    assert std.accept_lengths == std.proposed_lengths, (std.accept_lengths, std.proposed_lengths)
+    assert std.acceptance_rate == 1.0
+    ar = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=36, ignore_eos=True)
+    assert first_divergence(std.output_ids, ar.output_ids) is None

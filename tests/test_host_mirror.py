@@ -126,3 +126,17 @@ def test_7b_config_shapes():
     assert d == 128 and c.num_attention_heads // c.num_key_value_heads == 7
     assert abs(per_layer * c.num_hidden_layers / 1e9 - 6.53) < 0.01
     assert abs(c.vocab_size * c.hidden_size / 1e9 - 0.545) < 0.001
+
+
+def test_same_layout_ignores_size_one_strides():
+    """A projection's K (made contiguous after RoPE) and V (a transposed view)
+    of one decode token differ only in the unused stride of the size-1 row dim."""
+    from std_amd.ops import same_layout
+    k = torch.randn(1, 4, 1, 128)
+    v = torch.randn(1, 1, 4, 128).transpose(1, 2)
+    assert k.stride() != v.stride() and v.is_contiguous()
+    assert same_layout(k, v)
+    kk = torch.randn(1, 4, 3, 128)
+    vv = torch.randn(1, 3, 4, 128).transpose(1, 2)
+    assert not same_layout(kk, vv)
+    assert not same_layout(k, kk)
