@@ -252,6 +252,10 @@ def main():
         for l in range(L):
             ops.gqa_decode(q_draft[l], sparse_k[l][:, :, :S0], sparse_v[l][:, :, :S0], out=draft_out[l])
 
+    def draft_all_layers():
+        # the all-layer roofline unit of one draft step: the L layers' decodes as one batched launch
+        ops.gqa_decode_batched(q_draft, sparse_k[:, :, :, :S0], sparse_v[:, :, :, :S0], out=draft_out)
+
     def time_graph(graph, iters, flush=None):
         stream = torch.cuda.current_stream()
         times = []
@@ -268,10 +272,13 @@ def main():
 
     verify_graph, _ = capture(verify_only)
     draft_graph, _ = capture(draft_only)
+    draft_all_graph, _ = capture(draft_all_layers)
     verify_call_us = time_graph(verify_graph, 10) / L
     draft_call_us = time_graph(draft_graph, 50) / L
+    draft_all_warm_us = time_graph(draft_all_graph, 50)
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     draft_step_cold_us = time_graph(draft_graph, args.cold_iters, flush)      # 1 GiB written before each
+    draft_all_cold_us = time_graph(draft_all_graph, args.cold_iters, flush)
     del flush
     d_bytes = draft_bytes(Hq, Hkv, S0, D, es)
     v_bytes = verify_bytes(Hq, Hkv, Q, P + Q, D, es)
@@ -311,6 +318,11 @@ def main():
         "draft_attn_us_per_step_cold": round(draft_step_cold_us, 2),
         "draft_hbm_gbps_cold_step": round(draft_step_cold_gbps, 1),
         "draft_pct_peak_cold_step": round(100 * draft_step_cold_gbps / HBM_PEAK_GBPS, 2),
+        "draft_attn_us_per_step_one_launch_cold": round(draft_all_cold_us, 2),
+        "draft_attn_us_per_step_one_launch_warm": round(draft_all_warm_us, 2),
+        "draft_one_launch_hbm_gbps_cold": round(L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9, 1),
+        "draft_one_launch_pct_peak_cold": round(100 * L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+                                                2),
         "verify_attn_us_per_step": round(verify_call_us * L, 2),
         "verify_attn_us_per_layer": round(verify_call_us, 3),
         "verify_hbm_gbps": round(verify_gbps, 1),

@@ -73,6 +73,25 @@ int std_gqa_decode(const void* q, const void* k, const void* v, void* out,
                    float scale, int dtype,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Batched decode: n_batch independent single-query problems of the same
+ * shape in one launch (plus one merge launch). Problem b reads
+ * q + b*q_batch_stride, k + b*k_batch_stride, v + b*v_batch_stride and
+ * writes out + b*out_batch_stride (strides in elements; q/out strides
+ * >= n_q*d, 16-byte multiples). Each problem is exactly std_gqa_decode.
+ * Serves several sequences' draft steps at once (the reference decodes one
+ * sequence per call, triton_attention.py:83-112); the same call over the
+ * 28 layers of one draft step is the all-layer roofline unit of the draft
+ * attention. n_batch <= 65535. */
+size_t std_gqa_decode_batched_workspace_bytes(int n_batch, int n_q, int n_kv, int kv_len, int d);
+
+int std_gqa_decode_batched(const void* q, const void* k, const void* v, void* out,
+                           int n_batch, int n_q, int n_kv, int kv_len, int d,
+                           long long q_batch_stride, long long k_batch_stride,
+                           long long v_batch_stride, long long out_batch_stride,
+                           long long k_head_stride, long long v_head_stride,
+                           float scale, int dtype,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 /* Append + decode in one launch: the single new K/V row (new_k/new_v
  * [n_kv][1][d], head stride new_head_stride) is written to cache row
  * kv_len - 1, then the call attends over kv_len keys exactly as

@@ -66,6 +66,12 @@ SplitPlan plan_splits(int n_kv, int rows, int kv_len, int dtype) {
   return p;
 }
 
+// Element strides between the independent problems of a batched launch
+// (blockIdx.z); all zero for a single problem.
+struct BatchStrides {
+  long long q, k, v, o;
+};
+
 struct WsLayout {
   size_t o_off, ml_off, total;
 };
@@ -145,14 +151,15 @@ constexpr int kMergePrefetch = 8;
 template <typename T>
 __global__ void __launch_bounds__(kMergeThreads)
 attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
-                  int n_split, int q_len, int group) {
+                  int n_split, int q_len, int group, long long out_bs) {
   __shared__ float wts[kMaxSplit];
   __shared__ float red[2][kMergeThreads / 64];
   __shared__ f32x4 part[kMergeGroups][D / 4];
   const int r = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int d4 = tid & (D / 4 - 1), sg = tid / (D / 4);
   const int R = group * q_len;
-  const long long base = (long long)g * n_split * R + r;
+  out += blockIdx.z * out_bs;
+  const long long base = ((long long)blockIdx.z * gridDim.y + g) * n_split * R + r;
   const f32x4* col = reinterpret_cast<const f32x4*>(ws_o + base * D) + d4;
   const long long step = (long long)R * (D / 4);
   f32x4 pre[kMergePrefetch];
@@ -347,7 +354,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
                  bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                  int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
-                 long long n_hs, long long n_rs, int n_new) {
+                 long long n_hs, long long n_rs, int n_new, BatchStrides bs) {
   using C = Bf16Cfg<NT, RG, QL>;
   constexpr int NTW = C::NTW;
   __shared__ __align__(16) char ring[NSTAGE * STAGEB];
@@ -362,6 +369,17 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   const int rg = w >> 2;         // row group: row tiles [rg*NTW, rg*NTW + NTW)
   const int ln = lane & 15, lg = lane >> 4;
   const int R = group * q_len;
+  {
+    const long long b = blockIdx.z;
+    q += b * bs.q;
+    kc += b * bs.k;
+    vc += b * bs.v;
+    out += b * bs.o;
+    if (n_split > 1) {
+      ws_o += b * gridDim.y * n_split * R * D;
+      ws_ml += b * gridDim.y * n_split * R;
+    }
+  }
   const int t_begin = split_tile(split, ntiles_total, n_split);
   const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
   const int key_begin = t_begin * TK;
@@ -683,7 +701,7 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
                 float* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                 int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                 int n_split, int causal_off, const float* __restrict__ new_k, const float* __restrict__ new_v,
-                long long n_hs, long long n_rs, int n_new) {
+                long long n_hs, long long n_rs, int n_new, BatchStrides bs) {
   using F = F32Frag;
   using S = F32Smem<NT>;
   constexpr int CPR = D / 4;                    // 16-byte chunks per fp32 row
@@ -696,6 +714,17 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
   const int R = group * q_len;
+  {
+    const long long b = blockIdx.z;
+    q += b * bs.q;
+    kc += b * bs.k;
+    vc += b * bs.v;
+    out += b * bs.o;
+    if (n_split > 1) {
+      ws_o += b * gridDim.y * n_split * R * D;
+      ws_ml += b * gridDim.y * n_split * R;
+    }
+  }
   const int t_begin = split_tile(split, ntiles_total, n_split);
   const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
   const int key_begin = t_begin * TK;
@@ -859,15 +888,15 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
 template <int NT>
 int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
               long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
-              long long n_hs, long long n_rs, int n_new, hipStream_t st) {
+              long long n_hs, long long n_rs, int n_new, int n_batch, BatchStrides bs, hipStream_t st) {
   const int R = group * q_len;
-  const SplitPlan p = plan_splits(n_kv, R, kv_len, dtype);
-  const WsLayout wl = ws_layout(n_kv, R, p);
+  const SplitPlan p = plan_splits(n_kv * n_batch, R, kv_len, dtype);
+  const WsLayout wl = ws_layout(n_kv * n_batch, R, p);
   char* base = static_cast<char*>(ws);
   float* ws_o = p.n_split > 1 ? reinterpret_cast<float*>(base + wl.o_off) : nullptr;
   float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
   const float scale_log2 = scale * 1.4426950408889634f;
-  const dim3 grid(p.n_split, n_kv);
+  const dim3 grid(p.n_split, n_kv, n_batch);
   if (dtype == STD_BF16) {
     constexpr int RG = NT >= 3 ? 2 : 1;   // second row group of waves once a wave would carry > 2 row tiles
     constexpr bool QL = RG == 2;
@@ -875,29 +904,30 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
                        static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                        static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
                        p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
-                       static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new);
+                       static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs);
   } else {
     hipLaunchKernelGGL((attn_f32_kernel<NT>), grid, dim3(NTHREADS), 0, st, static_cast<const float*>(q),
                        static_cast<float*>(k), static_cast<float*>(v), static_cast<float*>(out), ws_o, ws_ml, q_len,
                        kv_len, group, k_hs, v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len,
-                       static_cast<const float*>(nk), static_cast<const float*>(nv), n_hs, n_rs, n_new);
+                       static_cast<const float*>(nk), static_cast<const float*>(nv), n_hs, n_rs, n_new, bs);
   }
   int s = launch_status();
   if (s != 0 || p.n_split == 1) return s;
   if (dtype == STD_BF16)
-    hipLaunchKernelGGL((attn_merge_kernel<bf16_t>), dim3(R, n_kv), dim3(kMergeThreads), 0, st, ws_o, ws_ml,
-                       static_cast<bf16_t*>(out), p.n_split, q_len, group);
+    hipLaunchKernelGGL((attn_merge_kernel<bf16_t>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st, ws_o,
+                       ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len, group, bs.o);
   else
-    hipLaunchKernelGGL((attn_merge_kernel<float>), dim3(R, n_kv), dim3(kMergeThreads), 0, st, ws_o, ws_ml,
-                       static_cast<float*>(out), p.n_split, q_len, group);
+    hipLaunchKernelGGL((attn_merge_kernel<float>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st, ws_o,
+                       ws_ml, static_cast<float*>(out), p.n_split, q_len, group, bs.o);
   return launch_status();
 }
 
 int launch_attn(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
                 long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
-                long long n_hs, long long n_rs, int n_new, hipStream_t st) {
-#define STD_LAUNCH_NT(N) \
-  launch_nt<N>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs, n_new, st)
+                long long n_hs, long long n_rs, int n_new, int n_batch, BatchStrides bs, hipStream_t st) {
+#define STD_LAUNCH_NT(N)                                                                                       \
+  launch_nt<N>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs, n_new, \
+               n_batch, bs, st)
   switch ((group * q_len + 15) / 16) {
     case 1: return STD_LAUNCH_NT(1);
     case 2: return STD_LAUNCH_NT(2);
@@ -916,8 +946,19 @@ size_t attn_workspace_bytes(int n_kv, int rows, int kv_len, int dtype) {
 
 int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, int q_len, int kv_len, int d,
                long long k_hs, long long v_hs, float scale, int dtype, void* ws, size_t ws_bytes, const void* nk,
-               const void* nv, long long n_hs, long long n_rs, int n_new, void* stream) {
+               const void* nv, long long n_hs, long long n_rs, int n_new, void* stream, int n_batch = 1,
+               BatchStrides bs = BatchStrides{0, 0, 0, 0}) {
   if (!q || !k || !v || !out) return STD_E_NULL;
+  if (n_batch < 1 || n_batch > 65535) return STD_E_SHAPE;
+  if (n_batch == 1) {
+    bs = BatchStrides{0, 0, 0, 0};
+  } else {
+    const long long rows = (long long)n_q * q_len * D;
+    if (n_new > 0) return STD_E_SHAPE;                       // the fused append serves one problem
+    if (bs.q < rows || bs.o < rows || bs.k < 0 || bs.v < 0) return STD_E_SHAPE;
+    const int es = dtype_size(dtype);
+    if ((bs.q * es) % 16 || (bs.o * es) % 16 || (bs.k * es) % 16 || (bs.v * es) % 16) return STD_E_ALIGN;
+  }
   if (n_new > 0 && (!nk || !nv)) return STD_E_NULL;
   if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
   if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len) return STD_E_SHAPE;
@@ -929,11 +970,11 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
   if ((k_hs * es) % 16 != 0 || (v_hs * es) % 16 != 0) return STD_E_ALIGN;
   if (n_new > 0 && (!aligned16(nk) || !aligned16(nv) || (n_hs * es) % 16 != 0 || (n_rs * es) % 16 != 0))
     return STD_E_ALIGN;
-  const size_t need = attn_workspace_bytes(n_kv, group * q_len, kv_len, dtype);
+  const size_t need = attn_workspace_bytes(n_kv * n_batch, group * q_len, kv_len, dtype);
   if (need > 0 && (ws == nullptr || ws_bytes < need)) return STD_E_WORKSPACE;
   if (need > 0 && !aligned16(ws)) return STD_E_ALIGN;
   return launch_attn(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs,
-                     n_new, static_cast<hipStream_t>(stream));
+                     n_new, n_batch, bs, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -954,6 +995,23 @@ extern "C" int std_gqa_decode(const void* q, const void* k, const void* v, void*
                               int dtype, void* workspace, size_t workspace_bytes, void* stream) {
   return attn_entry(q, const_cast<void*>(k), const_cast<void*>(v), out, n_q, n_kv, 1, kv_len, d, k_head_stride,
                     v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0, 0, stream);
+}
+
+extern "C" size_t std_gqa_decode_batched_workspace_bytes(int n_batch, int n_q, int n_kv, int kv_len, int d) {
+  if (n_batch < 1 || n_batch > 65535 || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || kv_len < 1 || d != D) return 0;
+  const size_t a = attn_workspace_bytes(n_kv * n_batch, n_q / n_kv, kv_len, STD_BF16);
+  const size_t b = attn_workspace_bytes(n_kv * n_batch, n_q / n_kv, kv_len, STD_F32);
+  return a > b ? a : b;
+}
+
+extern "C" int std_gqa_decode_batched(const void* q, const void* k, const void* v, void* out, int n_batch, int n_q,
+                                      int n_kv, int kv_len, int d, long long q_batch_stride, long long k_batch_stride,
+                                      long long v_batch_stride, long long out_batch_stride, long long k_head_stride,
+                                      long long v_head_stride, float scale, int dtype, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  return attn_entry(q, const_cast<void*>(k), const_cast<void*>(v), out, n_q, n_kv, 1, kv_len, d, k_head_stride,
+                    v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0, 0, stream, n_batch,
+                    BatchStrides{q_batch_stride, k_batch_stride, v_batch_stride, out_batch_stride});
 }
 
 extern "C" int std_gqa_decode_append(const void* q, void* k_cache, void* v_cache, const void* new_k, const void* new_v,

@@ -101,6 +101,47 @@ def gqa_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     return _attention("std_gqa_decode", query, key, value, scale, out)
 
 
+def gqa_decode_batched(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                       scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """n_batch independent single-query GQA decodes in one launch.
+
+    query [B, 1, n_q, 1, D] (or [B, n_q, 1, D]); key, value [B, 1, n_kv, S, D]
+    with any batch and head strides (e.g. one draft step's 28 layer caches).
+    Each problem b is exactly gqa_decode(query[b], key[b], value[b])."""
+    squeeze = query.dim() == 4
+    if squeeze:
+        query = query.unsqueeze(1)
+    if query.dim() != 5 or query.shape[1] != 1 or query.shape[3] != 1:
+        raise ValueError(f"Expected query [B, 1, n_q, 1, D], got {tuple(query.shape)}")
+    if key.dim() != 5 or key.shape[0] != query.shape[0] or value.shape != key.shape:
+        raise ValueError("key/value must be [B, 1, n_kv, S, D] matching the query batch")
+    dev = _check_device(query, key, value)
+    code = _dtype_code(query)
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise TypeError("query, key and value must share a dtype")
+    _check_cache_view("key", key[0])
+    _check_cache_view("value", value[0])
+    if not query[0].is_contiguous():
+        raise ValueError("each query problem must be contiguous")
+    n_batch, _, n_q, _, d = query.shape
+    n_kv, kv_len = key.shape[2], key.shape[3]
+    if d != HEAD_DIM or n_q % n_kv:
+        raise ValueError("unsupported head_dim or head counts")
+    if out is None:
+        out = torch.empty_like(query, memory_format=torch.contiguous_format)
+    elif out.shape != query.shape or out.dtype != query.dtype or not out[0].is_contiguous():
+        raise ValueError("out must be shaped like query with contiguous problems")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    lib = _lib.load_library()
+    ws_bytes = lib.std_gqa_decode_batched_workspace_bytes(n_batch, n_q, n_kv, kv_len, d)
+    ws_ptr = _attn_workspace(ws_bytes, dev)
+    _lib.call("std_gqa_decode_batched", query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), n_batch,
+              n_q, n_kv, kv_len, d, query.stride(0), key.stride(0), value.stride(0), out.stride(0), key.stride(2),
+              value.stride(2), float(scale), code, ws_ptr, ws_bytes, _stream(dev))
+    return out.squeeze(1) if squeeze else out
+
+
 def verify_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                      scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Dense verify attention for q_len appended rows with the offset-causal mask.

@@ -69,6 +69,25 @@ def test_decode_validation(args, expected):
     assert _lib.load_library().std_gqa_decode(*args) == expected
 
 
+def test_batched_decode_validation():
+    """Every call here fails validation before any launch."""
+    lib = _lib.load_library()
+    hs = 1024 * 128
+    assert lib.std_gqa_decode_batched_workspace_bytes(28, 28, 4, 1034, 128) > 0
+    assert lib.std_gqa_decode_batched_workspace_bytes(0, 28, 4, 1034, 128) == 0
+    args = [16, 16, 16, 16, 28, 28, 4, 1024, 128, 28 * 128, 4 * hs, 4 * hs, 28 * 128, hs, hs, 1.0, 1, NULL, 0, NULL]
+    bad_batch = list(args)
+    bad_batch[4] = 0
+    assert lib.std_gqa_decode_batched(*bad_batch) == -3
+    overlap = list(args)
+    overlap[12] = 100                                      # out batch stride < n_q * d: problems overlap
+    assert lib.std_gqa_decode_batched(*overlap) == -3
+    misaligned = list(args)
+    misaligned[10] = 4 * hs + 3                            # k batch stride not a 16-byte multiple
+    assert lib.std_gqa_decode_batched(*misaligned) == -5
+    assert lib.std_gqa_decode_batched(*args) == -4         # no workspace
+
+
 def test_verify_validation():
     lib = _lib.load_library()
     hs = 4106 * 128

@@ -190,3 +190,27 @@ def test_verify_append_matches_oracle(dtype, kv_len):
     assert torch.equal(vb[:, :, kv_len - Q:kv_len].cpu(), v[:, :, kv_len - Q:])
     assert torch.isnan(vb[:, :, kv_len:].float()).all()
     assert_close(out, ref.verify_attention(q, k, v), dtype)
+
+
+@pytest.mark.parametrize("dtype,S,B", [(torch.bfloat16, 1034, 28), (torch.float32, 1024, 3), (torch.bfloat16, 16384, 4),
+                                       (torch.bfloat16, 64, 5)])
+def test_decode_batched_matches_oracle(dtype, S, B):
+    """B independent decodes in one launch (e.g. one draft step's 28 layers);
+    each equals the oracle, and a batch of one equals gqa_decode exactly."""
+    gen = torch.Generator().manual_seed(S + B)
+    k = torch.randn(B, 1, 4, S, 128, generator=gen).to(dtype)
+    v = torch.randn(B, 1, 4, S, 128, generator=gen).to(dtype)
+    q = torch.randn(B, 1, 28, 1, 128, generator=gen).to(dtype)
+    announce(f"decode_batched {dtype} S={S} B={B}")
+    kb = torch.full((B, 1, 4, S + 9, 128), float("nan"), dtype=dtype, device=dev())
+    vb = torch.full_like(kb, float("nan"))
+    kb[:, :, :, :S] = k.to(dev())
+    vb[:, :, :, :S] = v.to(dev())
+    out = ops.gqa_decode_batched(q.to(dev()), kb[:, :, :, :S], vb[:, :, :, :S])
+    one = ops.gqa_decode_batched(q[:1].to(dev()), kb[:1, :, :, :S], vb[:1, :, :, :S])
+    single = ops.gqa_decode(q[0].to(dev()), kb[0, :, :, :S], vb[0, :, :, :S])
+    torch.cuda.synchronize()
+    assert out.shape == q.shape
+    for b in range(B):
+        assert_close(out[b], ref.gqa_sdpa(q[b], k[b], v[b]), dtype)
+    assert torch.equal(one[0], single)
