@@ -55,21 +55,32 @@ argmax_partial_kernel(const T* __restrict__ logits, long long row_stride, int vo
   }
 }
 
-// One block: final argmax per row, greedy prefix, bonus, rollback.
-__global__ void __launch_bounds__(64)
+// One block of kFinalThreads: wave w reduces rows w, w + kFinalWaves, ... (each
+// lane takes every 64th block partial, then a shuffle reduction with the same
+// ordering), then thread 0 forms the greedy prefix, the bonus and the rollback.
+constexpr int kFinalThreads = 256;
+constexpr int kFinalWaves = kFinalThreads / 64;
+
+__global__ void __launch_bounds__(kFinalThreads)
 accept_final_kernel(const uint2* __restrict__ part, int n_blocks, int q_rows, const int32_t* __restrict__ draft,
                     int n_draft, int has_pending, const int32_t* __restrict__ dense_next, int32_t* __restrict__ out,
                     int32_t* __restrict__ lens, int n_lens) {
   __shared__ int pred[kMaxRows + 1];
-  const int tid = threadIdx.x;
-  if (tid < q_rows) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int row = w; row < q_rows; row += kFinalWaves) {
     uint32_t bk = 0;
     int bi = INT_MAX;
-    for (int b = 0; b < n_blocks; ++b) {
-      const uint2 v = part[(long long)tid * n_blocks + b];
+    for (int b = lane; b < n_blocks; b += 64) {
+      const uint2 v = part[(long long)row * n_blocks + b];
       if (better(v.x, (int)v.y, bk, bi)) { bk = v.x; bi = (int)v.y; }
     }
-    pred[tid + (has_pending ? 0 : 1)] = bi;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const uint32_t ok = __shfl_xor(bk, off);
+      const int oi = __shfl_xor(bi, off);
+      if (better(ok, oi, bk, bi)) { bk = ok; bi = oi; }
+    }
+    if (lane == 0) pred[row + (has_pending ? 0 : 1)] = bi;
   }
   if (tid == 0 && !has_pending) pred[0] = *dense_next;
   __syncthreads();
@@ -156,7 +167,7 @@ extern "C" int std_greedy_accept(const void* logits, long long logits_row_stride
                        static_cast<const float*>(logits), logits_row_stride, vocab, nb, part);
   int s = launch_status();
   if (s) return s;
-  hipLaunchKernelGGL(accept_final_kernel, dim3(1), dim3(64), 0, st, part, nb, q_rows, draft, n_draft,
+  hipLaunchKernelGGL(accept_final_kernel, dim3(1), dim3(kFinalThreads), 0, st, part, nb, q_rows, draft, n_draft,
                      has_pending ? 1 : 0, dense_next, out, rollback_lens, n_lens);
   return launch_status();
 }

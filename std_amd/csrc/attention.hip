@@ -114,8 +114,8 @@ __device__ void append_rows(T* __restrict__ kh, T* __restrict__ vh, const T* __r
 // ---------------------------------------------------------------------------
 // Epilogue shared by both kernels: the key-waves' merged rows are in LDS
 // (So(r) -> row r of O, unnormalised; ml_f[r] = (m, l), log2 domain).
-template <typename T, typename OPtr>
-__device__ void finish_split(OPtr So, const float2* ml_f, T* __restrict__ out, float* __restrict__ ws_o,
+template <typename T, typename OLoad>
+__device__ void finish_split(OLoad load_o, const float2* ml_f, T* __restrict__ out, float* __restrict__ ws_o,
                              float2* __restrict__ ws_ml, int g, int split, int n_split, int q_len, int group,
                              int nthreads) {
   const int tid = threadIdx.x;
@@ -123,7 +123,7 @@ __device__ void finish_split(OPtr So, const float2* ml_f, T* __restrict__ out, f
   const long long head_row0 = (long long)g * n_split * R;
   for (int idx = tid; idx < R * (D / 4); idx += nthreads) {
     const int r = idx / (D / 4), d4 = idx - r * (D / 4);
-    const f32x4 o = *reinterpret_cast<const f32x4*>(So(r) + 4 * d4);
+    const f32x4 o = load_o(r, d4);
     if (n_split == 1) {
       const float L = ml_f[r].y;
       const int hl = r / q_len, i = r - hl * q_len;
@@ -595,7 +595,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
 
-  // ---- merge the four key-waves of each row group: row tiles 0-2 in stage 0, 3-5 in stage 1 ----
+  // ---- merge the four key-waves of each row group ----
   float l_run[NTW];
 #pragma unroll
   for (int rt = 0; rt < NTW; ++rt) l_run[rt] = lsum[rt][0];
@@ -621,28 +621,37 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     scl[rt] = fast_exp2(m_run[rt] - M);
     if (kg == 0 && lg == 0) ml_f[r] = make_float2(M, L);
   }
-  auto orow = [&](int r) -> float* {
+  // Two rounds over two row buffers (stages 0-1 and 2-3 of the ring): key-waves
+  // 0 and 2 store, key-waves 1 and 3 accumulate, and the write-out adds the
+  // buffers: (kg0 + kg1) + (kg2 + kg3) in a fixed order.
+  auto orow = [&](int buf, int r) -> float* {
     const int rt = r >> 4;
-    char* base = ring + (rt < 3 ? rt * OTILE_BYTES : STAGEB + (rt - 3) * OTILE_BYTES);
+    char* base = ring + 2 * buf * STAGEB + (rt < 3 ? rt * OTILE_BYTES : STAGEB + (rt - 3) * OTILE_BYTES);
     return reinterpret_cast<float*>(base) + (r & 15) * OROW;
   };
 #pragma unroll
-  for (int kk = 0; kk < WAVES; ++kk) {
-    if (kg == kk) {
+  for (int round = 0; round < 2; ++round) {
+    if ((kg & 1) == round) {
 #pragma unroll
       for (int rt = 0; rt < NTW; ++rt) {
-        float* rowp = orow((rg * NTW + rt) * 16 + ln);
+        const int row = (rg * NTW + rt) * 16 + ln;
+        if ((rg * NTW + rt) * 16 >= R) break;                 // padding row tile (wave-uniform)
+        if (row >= R) continue;                               // padding rows of the last tile
+        float* rowp = orow(kg >> 1, row);
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
           f32x4* dst = reinterpret_cast<f32x4*>(rowp + 16 * d + 4 * lg);
           const f32x4 o = acc[rt][d] * scl[rt];
-          if (kk == 0) *dst = o; else *dst += o;
+          if (round == 0) *dst = o; else *dst += o;
         }
       }
     }
     __syncthreads();
   }
-  finish_split<bf16_t>(orow, ml_f, out, ws_o, ws_ml, g, split, n_split, q_len, group, C::kThreads);
+  auto load_o = [&](int r, int d4) -> f32x4 {
+    return *reinterpret_cast<const f32x4*>(orow(0, r) + 4 * d4) + *reinterpret_cast<const f32x4*>(orow(1, r) + 4 * d4);
+  };
+  finish_split<bf16_t>(load_o, ml_f, out, ws_o, ws_ml, g, split, n_split, q_len, group, C::kThreads);
 }
 
 // ===========================================================================
@@ -880,8 +889,8 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
     }
     __syncthreads();
   }
-  auto orow = [&](int r) -> float* { return So + r * OROW; };
-  finish_split<float>(orow, ml_f, out, ws_o, ws_ml, g, split, n_split, q_len, group, NTHREADS);
+  auto load_o = [&](int r, int d4) -> f32x4 { return *reinterpret_cast<const f32x4*>(So + r * OROW + 4 * d4); };
+  finish_split<float>(load_o, ml_f, out, ws_o, ws_ml, g, split, n_split, q_len, group, NTHREADS);
 }
 
 // ===========================================================================
