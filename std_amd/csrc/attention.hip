@@ -243,6 +243,7 @@ constexpr int STAGEB = 2 * TILEB;         // K then V
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef short i16x8 __attribute__((ext_vector_type(8)));
 
 // 16-byte chunk c of row r lives at chunk c ^ swz(r): sixteen consecutive
 // rows map one logical chunk to sixteen distinct positions (K reads), and
@@ -331,42 +332,34 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(a[0]) + __uint_as_float(a[1]);
 }
 
-// NT row tiles of 16 query rows, RG row groups of four key-waves each; a wave
-// carries NTW = ceil(NT / RG) row tiles (padding tiles have zero queries and
-// are never written out). QL: the Q^T operand is re-read from LDS every tile
-// instead of being held in registers (needed when two waves share a SIMD
-// and each may hold only 256 registers).
-template <int NT, int RG, bool QL>
+// Row-owner layout: compute wave w < NT owns query rows [16w, 16w + 16) of the
+// launch's R rows and processes all 64 keys of every tile, so at the end of
+// its key range a wave holds complete row statistics and output rows and
+// writes them straight from registers (no cross-wave merge, no LDS epilogue).
+// Waves w >= NT only help issue the DMA ring. Decode (NT == 1) runs four
+// waves, verify eight.
+template <int NT>
 struct Bf16Cfg {
-  static constexpr int kWaves = 4 * RG;
+  static constexpr int kWaves = NT == 1 ? 4 : 8;
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int NTW = (NT + RG - 1) / RG;
-  static constexpr int kRowTiles = NTW * RG;            // including padding tiles
   static constexpr int kSegsPerWave = 16 / kWaves;       // 1 KiB K segments (and V) per wave per tile
   static constexpr int kLoadsPerTile = 2 * kSegsPerWave;
-  static constexpr int kQBytes = QL ? kRowTiles * 16 * ROWB : 16;
-  static constexpr int kQRegTiles = QL ? 1 : NTW;
 };
 
-template <int NT, int RG, bool QL>
-__global__ void __launch_bounds__(256 * RG)
+template <int NT>
+__global__ void __launch_bounds__(NT == 1 ? 256 : 512)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
                  bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                  int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
                  long long n_hs, long long n_rs, int n_new, BatchStrides bs) {
-  using C = Bf16Cfg<NT, RG, QL>;
-  constexpr int NTW = C::NTW;
+  using C = Bf16Cfg<NT>;
   __shared__ __align__(16) char ring[NSTAGE * STAGEB];
-  __shared__ __align__(16) char qs[C::kQBytes];
-  __shared__ float2 ml_w[WAVES * C::kRowTiles * 16];
-  __shared__ float2 ml_f[C::kRowTiles * 16];
 
   const int g = blockIdx.y, split = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kg = w & 3;          // key group: keys [16kg, 16kg + 16) of each tile
-  const int rg = w >> 2;         // row group: row tiles [rg*NTW, rg*NTW + NTW)
+  const bool computes = w < NT;                 // wave-uniform
   const int ln = lane & 15, lg = lane >> 4;
   const int R = group * q_len;
   {
@@ -416,73 +409,126 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     }
   };
 
-  // The first two tiles are in flight while the queries are staged.
+  // The first two tiles are in flight while the query row is loaded.
   auto stage = [&](int u) { return ring + (u & (NSTAGE - 1)) * STAGEB; };
   issue(0, stage(0));
   if (ntiles > 1) issue(1, stage(1));
 
-  int lim[NTW];
+  // This wave's query row is the lane's column ln of the S^T tiles; padding
+  // rows (and the helper waves) carry zero queries and are never written.
+  const int row = w * 16 + ln;
+  const bool row_ok = computes && row < R;
+  const int lim = row_ok ? causal_off + (row % q_len) : INT_MAX;
+  // Q^T operand, 32-wide chunk c: lane (ln, lg) holds q[row][32c + 8lg, +8).
+  bf16x8 qf[4];
+  if (row_ok) {
+    const int hl = row / q_len, i = row - hl * q_len;
+    const bf16_t* qrow = q + ((long long)(g * group + hl) * q_len + i) * D;
 #pragma unroll
-  for (int rt = 0; rt < NTW; ++rt) {
-    const int r = (rg * NTW + rt) * 16 + ln;
-    lim[rt] = r < R ? causal_off + (r % q_len) : INT_MAX;
-  }
-  // Q^T operand of row tile rt, 32-wide chunk c: lane (ln, lg) holds
-  // q[row][32c + 8lg, +8) of row (rg*NTW + rt)*16 + ln; padding rows are 0.
-  bf16x8 qf[C::kQRegTiles][4];
-  if constexpr (QL) {
-    // kRowTiles * 16 rows of 16 chunks over kThreads threads: exactly NTW
-    // chunks per thread, all loads issued before the first LDS store.
-    uint4 qv[NTW];
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-      const int idx = tid + j * C::kThreads, r = idx >> 4, ch = idx & 15;
-      qv[j] = make_uint4(0, 0, 0, 0);
-      if (r < R) {
-        const int hl = r / q_len, i = r - hl * q_len;
-        qv[j] = *reinterpret_cast<const uint4*>(q + ((long long)(g * group + hl) * q_len + i) * D + ch * 8);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-      const int idx = tid + j * C::kThreads;
-      *reinterpret_cast<uint4*>(qs + sw_off(idx >> 4, idx & 15)) = qv[j];
-    }
-    __syncthreads();
+    for (int c = 0; c < 4; ++c) qf[c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c + 8 * lg);
   } else {
 #pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) {
-      const int r = (rg * NTW + rt) * 16 + ln;
-      if (r < R) {
-        const int hl = r / q_len, i = r - hl * q_len;
-        const bf16_t* row = q + ((long long)(g * group + hl) * q_len + i) * D;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qf[rt][c] = *reinterpret_cast<const bf16x8*>(row + 32 * c + 8 * lg);
-      } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qf[rt][c] = bf16x8{};
-      }
-    }
-    // Retire the query loads (and with them the two ring tiles issued
-    // before them) here: the compiler counts only its own loads, and a wait
-    // for them placed inside the loop would drain the ring there.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    for (int c = 0; c < 4; ++c) qf[c] = bf16x8{};
   }
+  // Retire the query loads (and with them the two ring tiles issued before
+  // them) here: the compiler counts only its own loads, and a wait for them
+  // placed inside the loop would drain the ring there.
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 
   // Running statistics in the log2 domain (scores pre-multiplied by
-  // scale*log2(e)): m_run is the running max, and the row sums are
-  // accumulated by an MFMA against a ones operand (all rows of lsum equal the
-  // row sum of the bf16 probabilities used for PV).
-  float m_run[NTW];
-  f32x4 acc[NTW][8], lsum[NTW];
+  // scale*log2(e)): m_run is the row's running max; the row sum is
+  // accumulated by an MFMA against a ones operand (every element of lsum
+  // equals the row sum of the bf16 probabilities used for PV).
+  float m_run = -1e30f;
+  f32x4 acc[8], lsum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int rt = 0; rt < NTW; ++rt) {
-    m_run[rt] = -1e30f;
-    lsum[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, i16x8{0x3f80, 0x3f80, 0x3f80, 0x3f80, 0x3f80, 0x3f80, 0x3f80,
+                                                       0x3f80});
+
+  // S^T sub-tile j (keys 16j..16j+15 of the tile): lane (ln, lg) element i is
+  // key 16j + 4lg + i of query row ln.
+  auto qk = [&](const char* st, f32x4* s) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  const i16x4 ones = {0x3f80, 0x3f80, 0x3f80, 0x3f80};   // bf16 1.0
+    for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      bf16x8 kf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kf[j] = *reinterpret_cast<const bf16x8*>(st + sw_off(16 * j + ln, 4 * c + lg));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j], qf[c], s[j], 0, 0, 0);
+    }
+  };
+
+  // P V over key pairs (sub-tiles 2p, 2p+1) with 16x16x32 MFMA: contraction
+  // slots 8lg..8lg+3 are keys 32p + 4lg + {0..3}, slots 8lg+4..8lg+7 keys
+  // 32p + 16 + 4lg + {0..3}, for both the V^T operand (two transposed LDS
+  // reads) and the P^T operand (the lane's own scores).
+  auto softmax_pv = [&](int tt, const char* st, f32x4* s) {
+    const char* Vs = st + TILEB;
+    const int tile_base = key_begin + tt * TK;
+    bf16x8 vf[2][8];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int rv = 32 * p + 4 * lg + (ln >> 2);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int chunk = 2 * t + ((ln >> 1) & 1), half = (ln & 1) << 3;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Vs + sw_off(rv, chunk) + half));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Vs + sw_off(rv + 16, chunk) + half));
+        vf[p][t] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[j][i] *= scale_log2;
+    if (tile_base + TK > key_end || tile_base + TK - 1 > causal_off) {   // wave-uniform
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = tile_base + 16 * j + 4 * lg + i;
+          s[j][i] = (key < key_end && key <= lim) ? s[j][i] : -INFINITY;
+        }
+    }
+    // Per-lane max against the running max; the running max is raised
+    // (cross-lane reduction + rescale, one wave-uniform branch) only when a
+    // score exceeds it by more than kRescaleSlack, so probabilities stay
+    // <= 2^kRescaleSlack and the common path has no cross-lane traffic.
+    float lm = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+    for (int j = 1; j < 4; ++j) lm = fmaxf(lm, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
+    if (__ballot(lm > m_run + kRescaleSlack)) {
+      const float mt = xor32_max(xor16_max(lm));
+      const float m_new = mt > m_run + kRescaleSlack ? mt : m_run;
+      const float alpha = fast_exp2(m_run - m_new);
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] *= alpha;
+      m_run = m_new;
+    }
+    bf16x8 pb[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = fast_exp2(s[2 * p][i] - m_run);
+        x[4 + i] = fast_exp2(s[2 * p + 1][i] - m_run);
+      }
+      const i16x4 lo = pack_bf16x4(x[0], x[1], x[2], x[3]);
+      const i16x4 hi = pack_bf16x4(x[4], x[5], x[6], x[7]);
+      pb[p] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[p], lsum, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[p][t], pb[p], acc[t], 0, 0, 0);
+  };
 
   // Software pipeline, one step per tile u (steps 0..ntiles): after the
   // barrier, tile u+2 is prefetched into the stage tile u-2 used (every wave
@@ -490,168 +536,43 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   // issued into one score buffer, then the softmax and PV of tile u-1 run on
   // the other, so matrix and vector work of neighbouring tiles overlap inside
   // a wave and two tiles stay in flight during the step.
-  f32x4 sA[NTW], sB[NTW];
-  auto qk = [&](const char* stage, f32x4* s) {
-    const int rk = kg * 16 + ln;
-    bf16x8 kf[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) kf[c] = *reinterpret_cast<const bf16x8*>(stage + sw_off(rk, 4 * c + lg));
-#pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) s[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int rt = 0; rt < NTW; ++rt) {
-        bf16x8 b;
-        if constexpr (QL) b = *reinterpret_cast<const bf16x8*>(qs + sw_off((rg * NTW + rt) * 16 + ln, 4 * c + lg));
-        else b = qf[rt][c];
-        s[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[c], b, s[rt], 0, 0, 0);
-      }
-  };
-
-  auto softmax_pv = [&](int tt, const char* stage, f32x4* s) {
-    const char* Vs = stage + TILEB;
-    const int tile_base = key_begin + tt * TK;
-    const int kb = kg * 16;
-    // V^T operand of d-tile t: lane (ln, lg) gets V[kb + 4lg + j][16t + ln], j < 4
-    const int rv = kb + 4 * lg + (ln >> 2);
-    i16x4 vf[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const char* p = Vs + sw_off(rv, 2 * t + ((ln >> 1) & 1)) + ((ln & 1) << 3);
-      vf[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-    }
-#pragma unroll
-    for (int rt = 0; rt < NTW; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[rt][i] *= scale_log2;
-    if (tile_base + TK > key_end || tile_base + TK - 1 > causal_off) {   // wave-uniform
-      const int key0 = tile_base + kb + 4 * lg;
-#pragma unroll
-      for (int rt = 0; rt < NTW; ++rt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = key0 + i;
-          s[rt][i] = (key < key_end && key <= lim[rt]) ? s[rt][i] : -INFINITY;
-        }
-    }
-    // Per-lane max against the running max; the running max is raised
-    // (cross-lane reduction + rescale, one wave-uniform branch) only when a
-    // score exceeds it by more than kRescaleSlack, so probabilities stay
-    // <= 2^kRescaleSlack and the common path has no cross-lane traffic.
-    float lm[NTW];
-    bool rise = false;
-#pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) {
-      lm[rt] = fmaxf(fmaxf(s[rt][0], s[rt][1]), fmaxf(s[rt][2], s[rt][3]));
-      rise |= lm[rt] > m_run[rt] + kRescaleSlack;
-    }
-    if (__ballot(rise)) {
-#pragma unroll
-      for (int rt = 0; rt < NTW; ++rt) {
-        const float mt = xor32_max(xor16_max(lm[rt]));
-        const float m_new = mt > m_run[rt] + kRescaleSlack ? mt : m_run[rt];
-        const float alpha = fast_exp2(m_run[rt] - m_new);
-        lsum[rt] *= alpha;
-#pragma unroll
-        for (int d = 0; d < 8; ++d) acc[rt][d] *= alpha;
-        m_run[rt] = m_new;
-      }
-    }
-    i16x4 pb[NTW];
-#pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) {
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[rt][i] - m_run[rt]);
-      pb[rt] = pack_bf16x4(p[0], p[1], p[2], p[3]);
-    }
-#pragma unroll
-    for (int rt = 0; rt < NTW; ++rt) lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ones, pb[rt], lsum[rt], 0, 0, 0);
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int rt = 0; rt < NTW; ++rt)
-        acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[t], pb[rt], acc[rt][t], 0, 0, 0);
-  };
-
+  f32x4 sA[4], sB[4];
   auto step = [&](int u, const char* cur, const char* prev, char* ahead2, f32x4* s_new, f32x4* s_old) {
     if (u > ntiles) return;
     if (u < ntiles) wait_vm_ahead<C::kLoadsPerTile>(u + 1 < ntiles ? 1 : 0);
     wg_barrier();
     if (u + 2 < ntiles) issue(u + 2, ahead2);
-    if (u < ntiles) qk(cur, s_new);
-    if (u > 0) softmax_pv(u - 1, prev, s_old);
+    if (computes) {
+      if (u < ntiles) qk(cur, s_new);
+      if (u > 0) softmax_pv(u - 1, prev, s_old);
+    }
   };
-
-  // Tile u lives in ring stage u % NSTAGE (tiles 0 and 1 were issued before
-  // the query staging). The loop is unrolled by two only for the score
-  // ping-pong; stage addresses are computed at run time, which keeps the loop
-  // body small (it is fetched cold by every CU).
+  // Tile u lives in ring stage u % NSTAGE. The loop is unrolled by two only
+  // for the score ping-pong; stage addresses are computed at run time, which
+  // keeps the loop body small (it is fetched cold by every CU).
   for (int u = 0; u <= ntiles; u += 2) {
     step(u, stage(u), stage(u + 3), stage(u + 2), sA, sB);
     step(u + 1, stage(u + 1), stage(u), stage(u + 3), sB, sA);
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  __syncthreads();
+  if (!row_ok) return;
 
-  // ---- merge the four key-waves of each row group ----
-  float l_run[NTW];
+  // Complete rows: normalised output (one split) or the (m, l, O) partial.
+  const float l_row = lsum[0];
+  const int hl = row / q_len, i = row - hl * q_len;
+  if (n_split == 1) {
+    bf16_t* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * lg;
 #pragma unroll
-  for (int rt = 0; rt < NTW; ++rt) l_run[rt] = lsum[rt][0];
-  if (lg == 0) {
-#pragma unroll
-    for (int rt = 0; rt < NTW; ++rt)
-      ml_w[kg * C::kRowTiles * 16 + (rg * NTW + rt) * 16 + ln] = make_float2(m_run[rt], l_run[rt]);
-  }
-  __syncthreads();
-  float scl[NTW];
-#pragma unroll
-  for (int rt = 0; rt < NTW; ++rt) {
-    const int r = (rg * NTW + rt) * 16 + ln;
-    float M = ml_w[r].x;
-#pragma unroll
-    for (int kk = 1; kk < WAVES; ++kk) M = fmaxf(M, ml_w[kk * C::kRowTiles * 16 + r].x);
-    float L = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < WAVES; ++kk) {
-      const float2 ml = ml_w[kk * C::kRowTiles * 16 + r];
-      L += ml.y * fast_exp2(ml.x - M);
+    for (int t = 0; t < 8; ++t) {
+      const f32x4 o = acc[t] / l_row;
+      *reinterpret_cast<i16x4*>(dst + 16 * t) = pack_bf16x4(o[0], o[1], o[2], o[3]);
     }
-    scl[rt] = fast_exp2(m_run[rt] - M);
-    if (kg == 0 && lg == 0) ml_f[r] = make_float2(M, L);
+  } else {
+    const long long prow = (long long)g * n_split * R + (long long)split * R + row;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) *reinterpret_cast<f32x4*>(ws_o + prow * D + 16 * t + 4 * lg) = acc[t];
+    if (lg == 0) ws_ml[prow] = make_float2(m_run, l_row);
   }
-  // Two rounds over two row buffers (stages 0-1 and 2-3 of the ring): key-waves
-  // 0 and 2 store, key-waves 1 and 3 accumulate, and the write-out adds the
-  // buffers: (kg0 + kg1) + (kg2 + kg3) in a fixed order.
-  auto orow = [&](int buf, int r) -> float* {
-    const int rt = r >> 4;
-    char* base = ring + 2 * buf * STAGEB + (rt < 3 ? rt * OTILE_BYTES : STAGEB + (rt - 3) * OTILE_BYTES);
-    return reinterpret_cast<float*>(base) + (r & 15) * OROW;
-  };
-#pragma unroll
-  for (int round = 0; round < 2; ++round) {
-    if ((kg & 1) == round) {
-#pragma unroll
-      for (int rt = 0; rt < NTW; ++rt) {
-        const int row = (rg * NTW + rt) * 16 + ln;
-        if ((rg * NTW + rt) * 16 >= R) break;                 // padding row tile (wave-uniform)
-        if (row >= R) continue;                               // padding rows of the last tile
-        float* rowp = orow(kg >> 1, row);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-          f32x4* dst = reinterpret_cast<f32x4*>(rowp + 16 * d + 4 * lg);
-          const f32x4 o = acc[rt][d] * scl[rt];
-          if (round == 0) *dst = o; else *dst += o;
-        }
-      }
-    }
-    __syncthreads();
-  }
-  auto load_o = [&](int r, int d4) -> f32x4 {
-    return *reinterpret_cast<const f32x4*>(orow(0, r) + 4 * d4) + *reinterpret_cast<const f32x4*>(orow(1, r) + 4 * d4);
-  };
-  finish_split<bf16_t>(load_o, ml_f, out, ws_o, ws_ml, g, split, n_split, q_len, group, C::kThreads);
 }
 
 // ===========================================================================
@@ -907,9 +828,7 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   const float scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(p.n_split, n_kv, n_batch);
   if (dtype == STD_BF16) {
-    constexpr int RG = NT >= 3 ? 2 : 1;   // second row group of waves once a wave would carry > 2 row tiles
-    constexpr bool QL = RG == 2;
-    hipLaunchKernelGGL((attn_bf16_kernel<NT, RG, QL>), grid, dim3(Bf16Cfg<NT, RG, QL>::kThreads), 0, st,
+    hipLaunchKernelGGL((attn_bf16_kernel<NT>), grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
                        static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                        static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
                        p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
