@@ -40,21 +40,32 @@ __device__ __forceinline__ f64x4 mfma_f64(double a, double b, f64x4 c) {
 // interleaved by 4, unlike the fp32-accumulator 16x16 forms whose element i is
 // row 4*lg + i).
 //
-// Pass 1. grid (n_kb, n_kv, n_rg1), block 256 (4 waves x 4 row tiles of 16).
+// Pass 1. grid (n_kb, n_kv, n_rg1), block 256 (4 waves x 2 row tiles of 16:
+// 128 rows, so the 7 x 128 text rows of a GQA group need no padding).
 // S^T tile = K Q^T: A[m = ln][k = lg] = K[key][4c + lg] from LDS (fp64),
 // B[k = lg][n = ln] = Q[row][4c + lg] from registers; lane holds row ln and
-// keys lg + 4i of the 16-key subtile.
-constexpr int P1_RTW = 4;
+// keys lg + 4i of the 16-key subtile. The next 64-key tile of K is loaded
+// into registers (16-byte loads) while the current one is consumed.
+constexpr int P1_RTW = 2;
 constexpr int P1_WAVES = 4;
-constexpr int P1_ROWS = P1_WAVES * P1_RTW * 16;  // 256 rows per workgroup
+constexpr int P1_THREADS = 64 * P1_WAVES;
+constexpr int P1_ROWS = P1_WAVES * P1_RTW * 16;  // 128 rows per workgroup
 constexpr int P1_TK = 64;
 constexpr int KROW64 = D + 1;                    // LDS pitch in doubles
 
 template <typename T>
-__global__ void __launch_bounds__(256)
+struct KTile {
+  static constexpr int kPerChunk = 16 / (int)sizeof(T);           // elements per 16-byte load
+  static constexpr int kChunksPerRow = D / kPerChunk;
+  static constexpr int kPerThread = P1_TK * kChunksPerRow / P1_THREADS;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(P1_THREADS)
 sel_rowstats_kernel(const T* __restrict__ q, const T* __restrict__ k, double2* __restrict__ part,
                     int group, int text_len, int prompt_len, int text_start, long long k_hs,
                     double scale, int keys_per_block, int n_kb) {
+  using KT = KTile<T>;
   __shared__ double Ks[P1_TK * KROW64];
   const int kbk = blockIdx.x, g = blockIdx.y, rg = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ln = lane & 15, lg = lane >> 4;
@@ -84,13 +95,37 @@ sel_rowstats_kernel(const T* __restrict__ q, const T* __restrict__ k, double2* _
   const T* kh = k + (long long)g * k_hs;
   const int kbeg = kbk * keys_per_block;
   const int kend = min(prompt_len, kbeg + keys_per_block);
+  // K tile staging: thread chunk e = tid + P1_THREADS * i is row e / kChunksPerRow,
+  // 16 bytes at element (e % kChunksPerRow) * kPerChunk; rows past the block's
+  // last key re-read that key and are stored as zeros.
+  uint4 kpre[KT::kPerThread];
+  auto load_tile = [&](int key0) {
+#pragma unroll
+    for (int i = 0; i < KT::kPerThread; ++i) {
+      const int e = tid + P1_THREADS * i, kr = e / KT::kChunksPerRow;
+      const int c0 = (e - kr * KT::kChunksPerRow) * KT::kPerChunk;
+      const int key = min(key0 + kr, kend - 1);
+      kpre[i] = *reinterpret_cast<const uint4*>(kh + (long long)key * D + c0);
+    }
+  };
+  auto store_tile = [&](int key0) {
+#pragma unroll
+    for (int i = 0; i < KT::kPerThread; ++i) {
+      const int e = tid + P1_THREADS * i, kr = e / KT::kChunksPerRow;
+      const int c0 = (e - kr * KT::kChunksPerRow) * KT::kPerChunk;
+      const bool ok = key0 + kr < kend;
+      const T* v = reinterpret_cast<const T*>(&kpre[i]);
+      double* dst = Ks + kr * KROW64 + c0;
+#pragma unroll
+      for (int j = 0; j < KT::kPerChunk; ++j) dst[j] = ok ? to_f64<T>(v[j]) : 0.0;
+    }
+  };
+  load_tile(kbeg);
   for (int key0 = kbeg; key0 < kend; key0 += P1_TK) {
     __syncthreads();
-    for (int e = tid; e < P1_TK * D; e += 256) {
-      const int kr = e / D, d = e - kr * D, key = key0 + kr;
-      Ks[kr * KROW64 + d] = key < kend ? to_f64<T>(kh[(long long)key * D + d]) : 0.0;
-    }
+    store_tile(key0);
     __syncthreads();
+    if (key0 + P1_TK < kend) load_tile(key0 + P1_TK);
 #pragma unroll 1
     for (int ks = 0; ks < P1_TK / 16; ++ks) {
       f64x4 acc[P1_RTW];
@@ -160,16 +195,19 @@ sel_lse_kernel(const double2* __restrict__ part, double* __restrict__ lse, int R
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2. grid (n_kb2, n_kv, n_rg2), block 256. A row group of 128 rows is
-// staged in LDS; each wave takes 16-key column tiles, holds K^T in registers
-// and walks the 8 row tiles: S tile = Q K^T, A[m = ln][k = lg] = Q[row][4c+lg],
-// B[k = lg][n = ln] = K[key][4c + lg]; lane holds key ln and rows lg + 4i.
+// Pass 2. grid (n_kb2, n_kv, n_rg2), block 512. A row group of 128 rows is
+// staged in LDS; each of the 8 waves takes 16-key column tiles, holds K^T in
+// registers and walks the 8 row tiles: S tile = Q K^T, A[m = ln][k = lg] =
+// Q[row][4c+lg], B[k = lg][n = ln] = K[key][4c + lg]; lane holds key ln and
+// rows lg + 4i.
 constexpr int P2_RT = 8;
 constexpr int P2_ROWS = P2_RT * 16;
+constexpr int P2_WAVES = 8;
+constexpr int P2_THREADS = 64 * P2_WAVES;
 constexpr int QROW = D + 4;
 
 template <typename T>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(P2_THREADS)
 sel_colsum_kernel(const T* __restrict__ q, const T* __restrict__ k, const double* __restrict__ lse,
                   double* __restrict__ colpart, int group, int text_len, int prompt_len, int text_start,
                   long long k_hs, double scale, int keys_per_block, int n_kv) {
@@ -179,7 +217,7 @@ sel_colsum_kernel(const T* __restrict__ q, const T* __restrict__ k, const double
   const int kbk = blockIdx.x, g = blockIdx.y, rg = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ln = lane & 15, lg = lane >> 4;
   const int R = group * text_len;
-  for (int e = tid; e < P2_ROWS * D; e += 256) {
+  for (int e = tid; e < P2_ROWS * D; e += P2_THREADS) {
     const int rr = e / D, d = e - rr * D, r = rg * P2_ROWS + rr;
     float v = 0.f;
     if (r < R) {
@@ -188,7 +226,7 @@ sel_colsum_kernel(const T* __restrict__ q, const T* __restrict__ k, const double
     }
     Qs[rr * QROW + d] = v;
   }
-  for (int e = tid; e < P2_ROWS; e += 256) {
+  for (int e = tid; e < P2_ROWS; e += P2_THREADS) {
     const int r = rg * P2_ROWS + e;
     Ls[e] = r < R ? lse[(long long)g * R + r] : 0.0;
     Lim[e] = r < R ? text_start + (r % text_len) : -1;
@@ -198,11 +236,16 @@ sel_colsum_kernel(const T* __restrict__ q, const T* __restrict__ k, const double
   const T* kh = k + (long long)g * k_hs;
   const int kbeg = kbk * keys_per_block;
   const int kend = min(prompt_len, kbeg + keys_per_block);
-  for (int kt0 = kbeg + w * 16; kt0 < kend; kt0 += 4 * 16) {
+  for (int kt0 = kbeg + w * 16; kt0 < kend; kt0 += P2_WAVES * 16) {
     const int key = kt0 + ln;
+    // every lane loads (a key past the block's end re-reads the last key), so
+    // the 32 loads are in flight together; such columns are zeroed
+    const T* krow = kh + (long long)min(key, kend - 1) * D + lg;
     double bk[32];
 #pragma unroll
-    for (int c = 0; c < 32; ++c) bk[c] = key < kend ? to_f64<T>(kh[(long long)key * D + 4 * c + lg]) : 0.0;
+    for (int c = 0; c < 32; ++c) bk[c] = to_f64<T>(krow[4 * c]);
+#pragma unroll
+    for (int c = 0; c < 32; ++c) bk[c] = key < kend ? bk[c] : 0.0;
     double colsum = 0.0;
 #pragma unroll 1
     for (int rt = 0; rt < P2_RT; ++rt) {
@@ -393,13 +436,13 @@ SelectPlan plan_select(int n_q, int n_kv, int text_len, int prompt_len, int n_vi
   p.R = (n_q / n_kv) * text_len;
   p.n_rg1 = (p.R + P1_ROWS - 1) / P1_ROWS;
   int per_kb = n_kv * p.n_rg1;
-  p.n_kb = (512 + per_kb - 1) / per_kb;
+  p.n_kb = 512 / per_kb > 0 ? 512 / per_kb : 1;       // at most 2 workgroups per CU, one round
   p.kpb1 = (int)round_up((size_t)((prompt_len + p.n_kb - 1) / p.n_kb), P1_TK);
   p.n_kb = (prompt_len + p.kpb1 - 1) / p.kpb1;
   p.n_rg2 = (p.R + P2_ROWS - 1) / P2_ROWS;
   per_kb = n_kv * p.n_rg2;
-  p.n_kb2 = (1024 + per_kb - 1) / per_kb;
-  p.kpb2 = (int)round_up((size_t)((prompt_len + p.n_kb2 - 1) / p.n_kb2), 64);
+  p.n_kb2 = 1024 / per_kb > 0 ? 1024 / per_kb : 1;    // at most two rounds of 2 workgroups per CU
+  p.kpb2 = (int)round_up((size_t)((prompt_len + p.n_kb2 - 1) / p.n_kb2), P2_WAVES * 16);
   p.n_kb2 = (prompt_len + p.kpb2 - 1) / p.kpb2;
   p.off_part = 0;
   p.off_lse = round_up(p.off_part + (size_t)n_kv * p.n_kb * p.R * sizeof(double2), 256);
@@ -430,13 +473,13 @@ int launch_select(const void* q_text, const void* k, int n_q, int n_kv, int text
   const double scale = 1.0 / sqrt((double)D);
   const T* qt = static_cast<const T*>(q_text);
   const T* kk = static_cast<const T*>(k);
-  hipLaunchKernelGGL((sel_rowstats_kernel<T>), dim3(p.n_kb, n_kv, p.n_rg1), dim3(256), 0, st, qt, kk, part, group,
+  hipLaunchKernelGGL((sel_rowstats_kernel<T>), dim3(p.n_kb, n_kv, p.n_rg1), dim3(P1_THREADS), 0, st, qt, kk, part, group,
                      text_len, prompt_len, text_start, k_hs, scale, p.kpb1, p.n_kb);
   int s = launch_status();
   if (s) return s;
   hipLaunchKernelGGL(sel_lse_kernel, dim3((n_kv * p.R + 255) / 256), dim3(256), 0, st, part, lse, p.R, p.n_kb, n_kv);
   if ((s = launch_status())) return s;
-  hipLaunchKernelGGL((sel_colsum_kernel<T>), dim3(p.n_kb2, n_kv, p.n_rg2), dim3(256), 0, st, qt, kk, lse, colpart,
+  hipLaunchKernelGGL((sel_colsum_kernel<T>), dim3(p.n_kb2, n_kv, p.n_rg2), dim3(P2_THREADS), 0, st, qt, kk, lse, colpart,
                      group, text_len, prompt_len, text_start, k_hs, scale, p.kpb2, n_kv);
   if ((s = launch_status())) return s;
   const int n_cols = n_vis > prompt_len ? n_vis : prompt_len;
@@ -468,7 +511,8 @@ extern "C" int std_select_topk(const void* q_text, const void* k, int n_q, int n
   if (!select_shape_ok(n_q, n_kv, text_len, prompt_len, text_start, d, n_visual, k_select)) return STD_E_SHAPE;
   if (n_kv > 1 && k_head_stride < (long long)prompt_len * D) return STD_E_SHAPE;
   if (workspace_bytes < plan_select(n_q, n_kv, text_len, prompt_len, n_visual).total) return STD_E_WORKSPACE;
-  if (!aligned16(workspace)) return STD_E_ALIGN;
+  if (!aligned16(workspace) || !aligned16(k)) return STD_E_ALIGN;
+  if ((k_head_stride * dtype_size(dtype)) % 16) return STD_E_ALIGN;   // 16-byte K row loads
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == STD_BF16)
     return launch_select<bf16_t>(q_text, k, n_q, n_kv, text_len, prompt_len, text_start, k_head_stride, visual_pos,

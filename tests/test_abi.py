@@ -105,6 +105,11 @@ def test_select_validation():
                                NULL) == -3
     assert lib.std_select_topk(16, 16, 28, 4, 128, 4096, 3968, 128, hs, 1, 16, 3968, 896, 16, NULL, 16, 10,
                                NULL) == -4
+    # K is read in 16-byte chunks: a misaligned base or head stride is rejected
+    assert lib.std_select_topk(16, 8, 28, 4, 128, 4096, 3968, 128, hs, 1, 16, 3968, 896, 16, NULL, 16, 1 << 30,
+                               NULL) == -5
+    assert lib.std_select_topk(16, 16, 28, 4, 128, 4096, 3968, 128, hs + 4, 1, 16, 3968, 896, 16, NULL, 16, 1 << 30,
+                               NULL) == -5
 
 
 def test_accept_and_append_validation():
