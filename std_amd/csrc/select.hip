@@ -17,8 +17,9 @@
 //   merge   sel_lse:      lse per row, blocks in fixed order
 //   pass 2  sel_colsum:   per (row group, key) partial column sums       MFMA f64
 //   keys    sel_keys:     column score of every visual position, row groups in order
-//   select  sel_topk:     radix select of the k-th largest (score, -position),
-//                         then an ordered scan that emits positions ascending
+//   select  sel_topk_*:   multi-block radix select of the k-th largest score
+//                         (8 histogram passes), then per-block counts and an
+//                         ordered emission of positions ascending (ties: lowest)
 #include <cfloat>
 
 #include "common.h"
@@ -267,13 +268,16 @@ sel_colsum_kernel(const T* __restrict__ q, const T* __restrict__ k, const double
 
 // Column score of each visual position as an order-preserving u64 key
 // (scores are >= 0, so the IEEE bit pattern orders like the value), and the
-// optional full score row. grid (ceil(max(n_vis, P) / 256), n_kv).
+// optional full score row; the first block of each head also clears that
+// head's radix histograms. grid (ceil(max(n_vis, P) / 256), n_kv), block 256.
 __global__ void __launch_bounds__(256)
 sel_keys_kernel(const double* __restrict__ colpart, int n_rg2, int n_kv, int prompt_len,
                 const int32_t* __restrict__ vis, int n_vis, unsigned long long* __restrict__ keys,
-                double* __restrict__ scores_out) {
+                double* __restrict__ scores_out, unsigned* __restrict__ hist) {
   const int g = blockIdx.y;
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (blockIdx.x == 0)
+    for (int p = 0; p < 8; ++p) hist[((long long)p * n_kv + g) * 256 + threadIdx.x] = 0u;
   if (t < n_vis) {
     const int j = vis[t];
     double s = 0.0;
@@ -288,9 +292,25 @@ sel_keys_kernel(const double* __restrict__ colpart, int n_rg2, int n_kv, int pro
   }
 }
 
-constexpr int TOPK_THREADS = 1024;
+// ---------------------------------------------------------------------------
+// Top-k by a multi-block radix select over the u64 keys, 8 bits per pass from
+// the top. Pass p histograms digit p of the keys whose higher digits equal
+// those of the k-th largest key (found from passes < p): every block adds its
+// slice's histogram into hist[p][g][256] (zeroed by sel_keys_kernel) and
+// re-derives the earlier digits from those histograms, so no state but the
+// histograms passes between launches. sel_topk_count then counts, per block,
+// the keys above the k-th largest key T and the keys equal to it, and
+// sel_topk_emit writes every key above T and the kk lowest-position keys equal
+// to T (kk = k minus the count above T), positions ascending.
+constexpr int TOPK_THREADS = 256;
+constexpr int TOPK_PER_THREAD = 16;
+constexpr int TOPK_SLICE = TOPK_THREADS * TOPK_PER_THREAD;   // keys per block
+constexpr int TOPK_PASSES = 8;
 
-// Exclusive prefix sum over the block (1024 threads) in thread order.
+int topk_blocks(int n_vis) { return (n_vis + TOPK_SLICE - 1) / TOPK_SLICE; }
+
+// Exclusive prefix sum over the block (TOPK_THREADS threads) in thread order;
+// *total receives the block sum.
 __device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int x = v;
@@ -316,64 +336,152 @@ __device__ int block_exclusive_scan(int v, int* wave_tot, int* total) {
   return res;
 }
 
-// grid (n_kv), block 1024.
-__global__ void __launch_bounds__(TOPK_THREADS)
-sel_topk_kernel(const unsigned long long* __restrict__ keys_all, const int32_t* __restrict__ vis, int n_vis,
-                int k_sel, int32_t* __restrict__ topk_out) {
-  __shared__ unsigned int hist[256];
-  __shared__ int wave_tot[TOPK_THREADS / 64];
-  __shared__ int s_total, s_digit, s_kk;
-  const int g = blockIdx.x, tid = threadIdx.x;
-  const unsigned long long* keys = keys_all + (long long)g * n_vis;
+struct RadixState {
+  unsigned long long prefix, mask;
+  int kk;   // rank (from the top) of the k-th largest key among keys matching prefix
+};
 
-  unsigned long long prefix = 0, mask = 0;
-  int kk = k_sel;  // rank (from the top) still to be located inside the current prefix
-  for (int shift = 56; shift >= 0; shift -= 8) {
-    for (int b = tid; b < 256; b += TOPK_THREADS) hist[b] = 0;
-    __syncthreads();
-    for (int t = tid; t < n_vis; t += TOPK_THREADS) {
-      const unsigned long long u = keys[t];
-      if ((u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+// The k-th largest key's digits of passes [0, n_pass) from the histograms;
+// thread t examines digit 255 - t, so the exclusive scan counts larger digits.
+__device__ RadixState radix_state(const unsigned* __restrict__ hist, int g, int n_kv, int n_pass, int k_sel,
+                                  int* wave_tot, int* sh) {
+  RadixState st{0ull, 0ull, k_sel};
+  const int tid = threadIdx.x;
+  for (int p = 0; p < n_pass; ++p) {
+    const int digit = 255 - tid;
+    const int c = (int)hist[((long long)p * n_kv + g) * 256 + digit];
+    const int above = block_exclusive_scan(c, wave_tot, sh + 2);
+    if (above < st.kk && st.kk <= above + c) {
+      sh[0] = digit;
+      sh[1] = st.kk - above;
     }
     __syncthreads();
-    if (tid == 0) {
-      int cum = 0, b = 255;
-      for (; b > 0; --b) {
-        if (cum + (int)hist[b] >= kk) break;
-        cum += (int)hist[b];
-      }
-      s_digit = b;
-      s_kk = kk - cum;
-    }
-    __syncthreads();
-    prefix |= (unsigned long long)s_digit << shift;
-    mask |= 255ull << shift;
-    kk = s_kk;
+    const int shift = 56 - 8 * p;
+    st.prefix |= (unsigned long long)sh[0] << shift;
+    st.mask |= 255ull << shift;
+    st.kk = sh[1];
     __syncthreads();
   }
-  // prefix is the k-th largest key; take every key above it and the kk
-  // lowest-position keys equal to it, emitting positions in ascending order.
-  const int chunk = (n_vis + TOPK_THREADS - 1) / TOPK_THREADS;
-  const int t0 = min(n_vis, tid * chunk), t1 = min(n_vis, t0 + chunk);
-  int n_eq = 0;
-  for (int t = t0; t < t1; ++t) n_eq += keys[t] == prefix;
-  int eq_rank = block_exclusive_scan(n_eq, wave_tot, &s_total);
+  return st;
+}
+
+// LDS histogram add with one atomic per wave when all active lanes share a bin
+// (the common case in the first passes, where most keys share a digit).
+__device__ __forceinline__ void wave_hist_add(unsigned* h, unsigned bin, bool act, int lane) {
+  const unsigned long long a = __ballot(act);
+  if (a == 0) return;
+  const int leader = __ffsll((long long)a) - 1;
+  const unsigned b0 = __shfl(bin, leader);
+  if (__ballot(act && bin == b0) == a) {
+    if (lane == leader) atomicAdd(&h[b0], (unsigned)__popcll(a));
+  } else if (act) {
+    atomicAdd(&h[bin], 1u);
+  }
+}
+
+// grid (topk_blocks(n_vis), n_kv), block TOPK_THREADS.
+__global__ void __launch_bounds__(TOPK_THREADS)
+sel_topk_hist_kernel(const unsigned long long* __restrict__ keys_all, int n_vis, int k_sel, int n_kv,
+                     unsigned* __restrict__ hist, int pass) {
+  __shared__ unsigned h[256];
+  __shared__ int wave_tot[TOPK_THREADS / 64];
+  __shared__ int sh[3];
+  const int g = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const RadixState st = radix_state(hist, g, n_kv, pass, k_sel, wave_tot, sh);
+  h[tid] = 0;
+  __syncthreads();
+  const unsigned long long* keys = keys_all + (long long)g * n_vis;
+  const int shift = 56 - 8 * pass, base = blockIdx.x * TOPK_SLICE;
+#pragma unroll 4
+  for (int i = 0; i < TOPK_PER_THREAD; ++i) {
+    const int t = base + i * TOPK_THREADS + tid;
+    bool act = false;
+    unsigned bin = 0;
+    if (t < n_vis) {
+      const unsigned long long u = keys[t];
+      act = (u & st.mask) == st.prefix;
+      bin = (unsigned)(u >> shift) & 255u;
+    }
+    wave_hist_add(h, bin, act, lane);
+  }
+  __syncthreads();
+  if (h[tid]) atomicAdd(&hist[((long long)pass * n_kv + g) * 256 + tid], h[tid]);
+}
+
+// Thread tid owns keys [base + tid * TOPK_PER_THREAD, +TOPK_PER_THREAD) of the
+// block's slice (contiguous, so thread order is position order).
+__device__ __forceinline__ void slice_range(int n_vis, int& t0, int& t1) {
+  t0 = min(n_vis, blockIdx.x * TOPK_SLICE + (int)threadIdx.x * TOPK_PER_THREAD);
+  t1 = min(n_vis, t0 + TOPK_PER_THREAD);
+}
+
+// grid (topk_blocks(n_vis), n_kv): counts[g][blk] = (keys > T, keys == T).
+__global__ void __launch_bounds__(TOPK_THREADS)
+sel_topk_count_kernel(const unsigned long long* __restrict__ keys_all, int n_vis, int k_sel, int n_kv,
+                      const unsigned* __restrict__ hist, int2* __restrict__ counts) {
+  __shared__ int wave_tot[TOPK_THREADS / 64];
+  __shared__ int sh[3];
+  __shared__ int s_gt;
+  const int g = blockIdx.y;
+  const RadixState st = radix_state(hist, g, n_kv, TOPK_PASSES, k_sel, wave_tot, sh);
+  const unsigned long long* keys = keys_all + (long long)g * n_vis;
+  int t0, t1, gt = 0, eq = 0;
+  slice_range(n_vis, t0, t1);
+  for (int t = t0; t < t1; ++t) {
+    const unsigned long long u = keys[t];
+    gt += u > st.prefix;
+    eq += u == st.prefix;
+  }
+  block_exclusive_scan(gt, wave_tot, &s_gt);
+  block_exclusive_scan(eq, wave_tot, sh + 2);
+  if (threadIdx.x == 0) counts[(long long)g * gridDim.x + blockIdx.x] = make_int2(s_gt, sh[2]);
+}
+
+// grid (topk_blocks(n_vis), n_kv): emit the block's selected positions at
+// their global ranks.
+__global__ void __launch_bounds__(TOPK_THREADS)
+sel_topk_emit_kernel(const unsigned long long* __restrict__ keys_all, const int32_t* __restrict__ vis, int n_vis,
+                     int k_sel, int n_kv, const unsigned* __restrict__ hist, const int2* __restrict__ counts,
+                     int32_t* __restrict__ topk_out) {
+  __shared__ int wave_tot[TOPK_THREADS / 64];
+  __shared__ int sh[3];
+  __shared__ int s_before[2];
+  const int g = blockIdx.y, tid = threadIdx.x;
+  const RadixState st = radix_state(hist, g, n_kv, TOPK_PASSES, k_sel, wave_tot, sh);
+  const unsigned long long T = st.prefix;
+  const int kk = st.kk;
+  if (tid == 0) {
+    int eq_before = 0, sel_before = 0;
+    for (int b = 0; b < (int)blockIdx.x; ++b) {
+      const int2 c = counts[(long long)g * gridDim.x + b];
+      sel_before += c.x + min(max(kk - eq_before, 0), c.y);
+      eq_before += c.y;
+    }
+    s_before[0] = eq_before;
+    s_before[1] = sel_before;
+  }
+  __syncthreads();
+  const unsigned long long* keys = keys_all + (long long)g * n_vis;
+  int t0, t1, n_eq = 0;
+  slice_range(n_vis, t0, t1);
+  for (int t = t0; t < t1; ++t) n_eq += keys[t] == T;
+  int eq_rank = s_before[0] + block_exclusive_scan(n_eq, wave_tot, sh + 2);
   int n_sel = 0;
   {
     int r = eq_rank;
     for (int t = t0; t < t1; ++t) {
       const unsigned long long u = keys[t];
-      if (u > prefix) ++n_sel;
-      else if (u == prefix) { if (r < kk) ++n_sel; ++r; }
+      if (u > T) ++n_sel;
+      else if (u == T) { if (r < kk) ++n_sel; ++r; }
     }
   }
-  int off = block_exclusive_scan(n_sel, wave_tot, &s_total);
+  int off = s_before[1] + block_exclusive_scan(n_sel, wave_tot, sh + 2);
   int32_t* out = topk_out + (long long)g * k_sel;
   for (int t = t0; t < t1; ++t) {
     const unsigned long long u = keys[t];
     bool take = false;
-    if (u > prefix) take = true;
-    else if (u == prefix) { take = eq_rank < kk; ++eq_rank; }
+    if (u > T) take = true;
+    else if (u == T) { take = eq_rank < kk; ++eq_rank; }
     if (take && off < k_sel) out[off++] = vis[t];
   }
 }
@@ -427,8 +535,8 @@ compact_kv_kernel(const char* __restrict__ dk, const char* __restrict__ dv, char
 
 // ---------------------------------------------------------------------------
 struct SelectPlan {
-  int R, n_rg1, n_kb, kpb1, n_rg2, n_kb2, kpb2;
-  size_t off_part, off_lse, off_col, off_keys, total;
+  int R, n_rg1, n_kb, kpb1, n_rg2, n_kb2, kpb2, n_tb;
+  size_t off_part, off_lse, off_col, off_keys, off_hist, off_cnt, total;
 };
 
 SelectPlan plan_select(int n_q, int n_kv, int text_len, int prompt_len, int n_vis) {
@@ -448,7 +556,10 @@ SelectPlan plan_select(int n_q, int n_kv, int text_len, int prompt_len, int n_vi
   p.off_lse = round_up(p.off_part + (size_t)n_kv * p.n_kb * p.R * sizeof(double2), 256);
   p.off_col = round_up(p.off_lse + (size_t)n_kv * p.R * sizeof(double), 256);
   p.off_keys = round_up(p.off_col + (size_t)p.n_rg2 * n_kv * prompt_len * sizeof(double), 256);
-  p.total = round_up(p.off_keys + (size_t)n_kv * n_vis * sizeof(unsigned long long), 256);
+  p.n_tb = topk_blocks(n_vis);
+  p.off_hist = round_up(p.off_keys + (size_t)n_kv * n_vis * sizeof(unsigned long long), 256);
+  p.off_cnt = round_up(p.off_hist + (size_t)TOPK_PASSES * n_kv * 256 * sizeof(unsigned), 256);
+  p.total = round_up(p.off_cnt + (size_t)n_kv * p.n_tb * sizeof(int2), 256);
   return p;
 }
 
@@ -469,6 +580,8 @@ int launch_select(const void* q_text, const void* k, int n_q, int n_kv, int text
   double* lse = reinterpret_cast<double*>(base + p.off_lse);
   double* colpart = reinterpret_cast<double*>(base + p.off_col);
   unsigned long long* keys = reinterpret_cast<unsigned long long*>(base + p.off_keys);
+  unsigned* hist = reinterpret_cast<unsigned*>(base + p.off_hist);
+  int2* counts = reinterpret_cast<int2*>(base + p.off_cnt);
   const int group = n_q / n_kv;
   const double scale = 1.0 / sqrt((double)D);
   const T* qt = static_cast<const T*>(q_text);
@@ -484,9 +597,17 @@ int launch_select(const void* q_text, const void* k, int n_q, int n_kv, int text
   if ((s = launch_status())) return s;
   const int n_cols = n_vis > prompt_len ? n_vis : prompt_len;
   hipLaunchKernelGGL(sel_keys_kernel, dim3((n_cols + 255) / 256, n_kv), dim3(256), 0, st, colpart, p.n_rg2, n_kv,
-                     prompt_len, vis, n_vis, keys, scores_out);
+                     prompt_len, vis, n_vis, keys, scores_out, hist);
   if ((s = launch_status())) return s;
-  hipLaunchKernelGGL(sel_topk_kernel, dim3(n_kv), dim3(TOPK_THREADS), 0, st, keys, vis, n_vis, k_sel, topk_out);
+  const dim3 tgrid(p.n_tb, n_kv);
+  for (int pass = 0; pass < TOPK_PASSES; ++pass) {
+    hipLaunchKernelGGL(sel_topk_hist_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, pass);
+    if ((s = launch_status())) return s;
+  }
+  hipLaunchKernelGGL(sel_topk_count_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, counts);
+  if ((s = launch_status())) return s;
+  hipLaunchKernelGGL(sel_topk_emit_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, vis, n_vis, k_sel, n_kv, hist,
+                     counts, topk_out);
   return launch_status();
 }
 
