@@ -453,7 +453,7 @@ def cpu_baseline(w, L):
         threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
     except Exception:  # pragma: no cover
         threads = os.cpu_count() or 1
-    sample_layers, reps = L, 2
+    sample_layers, reps = L, 3
     t_verify = t_draft = 0.0
     for l in range(sample_layers):
         x = make_layer(w, l)
