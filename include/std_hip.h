@@ -214,6 +214,48 @@ int std_kv_append(void* cache_k, void* cache_v, const void* new_k, const void* n
 int std_len_add(int32_t* len_dev, int n, int delta, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Rotary embedding fused with the K/V cache append, at a device length and a
+ * device position (the decode-step glue that keeps lengths and positions on
+ * the GPU, so a whole decode step can be captured in a HIP graph).
+ *
+ * Replaces, for the decode and verify rows, apply_multimodal_rotary_pos_emb
+ *   (modeling_qwen2_5_vl.py:690-732; with three identical position rows the
+ *   multimodal embedding is the 1-D rotate-half embedding), the q/k/v
+ *   transposes and KVCache.cat (src/specvlm/kv_cache/kv_cache.py:54-69).
+ * qkv is the fused projection output [n_rows][(n_q + 2 n_kv) d] (row stride
+ * qkv_row_stride elements): query heads, then key heads, then value heads.
+ * Row r has position *pos_dev + pos_offset + r; angle = float(pos) *
+ * inv_freq[j] (fp32 table of d/2 entries), cos/sin rounded to the dtype, and
+ * x * cos + rotate_half(x) * sin evaluated op by op with dtype rounding (as
+ * torch evaluates it). Rotated queries go to q_out [n_q][n_rows][d]; rotated
+ * keys and the values go to cache row *len_dev + r (head stride
+ * cache_head_stride); rows at or past `capacity` are not written. The length
+ * is not advanced (std_len_add does that once per step).
+ * ------------------------------------------------------------------------ */
+int std_rope_append(const void* qkv, long long qkv_row_stride, void* q_out, void* cache_k, void* cache_v,
+                    int n_rows, int n_q, int n_kv, int d, long long cache_head_stride, int capacity,
+                    const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
+                    const float* inv_freq, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Offset-causal GQA attention at a device length (decode when q_len == 1).
+ *
+ * Replaces, for graph-captured decode steps, the dense verify attention
+ *   (modeling_qwen2_5_vl.py:1007-1140, mask :65-126) and the sparse draft
+ *   attention (std_qwen25vl.py:399-431) with the cache length read on the
+ *   device: the cache holds *len_dev + q_len valid rows (the last q_len written
+ *   for this step, e.g. by std_rope_append) and query row i sees keys
+ *   [0, *len_dev + i]. The split plan and workspace are those of
+ *   std_verify_attn at kv_len = max_kv_len (size the workspace with
+ *   std_verify_attn_workspace_bytes(n_q, n_kv, q_len, max_kv_len, d)); a device
+ *   length outside [0, max_kv_len - q_len] reads nothing and yields NaN outputs.
+ * ------------------------------------------------------------------------ */
+int std_attn_devlen(const void* q, const void* k_cache, const void* v_cache, void* out,
+                    int n_q, int n_kv, int q_len, const int32_t* len_dev, int max_kv_len, int d,
+                    long long k_head_stride, long long v_head_stride, float scale, int dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Greedy acceptance plus cache rollback on the device.
  *
  * Replaces the verify tail of std_generate_qwen25vl

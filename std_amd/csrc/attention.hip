@@ -90,6 +90,18 @@ __device__ __forceinline__ int split_tile(int split, int ntiles, int n_split) {
   return (int)((long long)split * ntiles / n_split);
 }
 
+// Device-length launch: the cache holds *len_dev rows plus this step's q_len
+// new rows, and the grid was planned for kv_len (the launch's maximum). A
+// length outside [0, kv_len - q_len] empties every split: nothing is read and
+// the outputs become 0/0 = NaN.
+__device__ __forceinline__ void device_length(const int32_t* len_dev, int q_len, int& kv_len, int& ntiles_total,
+                                              int& causal_off) {
+  const int len = *len_dev;
+  kv_len = (len >= 0 && len <= kv_len - q_len) ? len + q_len : 0;
+  ntiles_total = (kv_len + TK - 1) / TK;
+  causal_off = kv_len - q_len;
+}
+
 // Fused append: cache rows [kv_len - n_new, kv_len) receive the n_new new
 // rows (new_*[g][r], strides in elements). Each workgroup writes the rows that
 // fall inside its own key range, before it reads that range (the caller puts a
@@ -352,7 +364,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
                  bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                  int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
-                 long long n_hs, long long n_rs, int n_new, BatchStrides bs) {
+                 long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev) {
   using C = Bf16Cfg<NT>;
   __shared__ __align__(16) char ring[NSTAGE * STAGEB];
 
@@ -373,6 +385,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       ws_ml += b * gridDim.y * n_split * R;
     }
   }
+  if (len_dev != nullptr) device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
   const int t_begin = split_tile(split, ntiles_total, n_split);
   const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
   const int key_begin = t_begin * TK;
@@ -411,7 +424,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
 
   // The first two tiles are in flight while the query row is loaded.
   auto stage = [&](int u) { return ring + (u & (NSTAGE - 1)) * STAGEB; };
-  issue(0, stage(0));
+  if (ntiles > 0) issue(0, stage(0));
   if (ntiles > 1) issue(1, stage(1));
 
   // This wave's query row is the lane's column ln of the S^T tiles; padding
@@ -631,7 +644,7 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
                 float* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                 int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                 int n_split, int causal_off, const float* __restrict__ new_k, const float* __restrict__ new_v,
-                long long n_hs, long long n_rs, int n_new, BatchStrides bs) {
+                long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev) {
   using F = F32Frag;
   using S = F32Smem<NT>;
   constexpr int CPR = D / 4;                    // 16-byte chunks per fp32 row
@@ -655,6 +668,7 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
       ws_ml += b * gridDim.y * n_split * R;
     }
   }
+  if (len_dev != nullptr) device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
   const int t_begin = split_tile(split, ntiles_total, n_split);
   const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
   const int key_begin = t_begin * TK;
@@ -818,7 +832,8 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
 template <int NT>
 int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
               long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
-              long long n_hs, long long n_rs, int n_new, int n_batch, BatchStrides bs, hipStream_t st) {
+              long long n_hs, long long n_rs, int n_new, int n_batch, BatchStrides bs, const int32_t* len_dev,
+              hipStream_t st) {
   const int R = group * q_len;
   const SplitPlan p = plan_splits(n_kv * n_batch, R, kv_len, dtype);
   const WsLayout wl = ws_layout(n_kv * n_batch, R, p);
@@ -832,12 +847,12 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
                        static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                        static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
                        p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
-                       static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs);
+                       static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev);
   } else {
     hipLaunchKernelGGL((attn_f32_kernel<NT>), grid, dim3(NTHREADS), 0, st, static_cast<const float*>(q),
                        static_cast<float*>(k), static_cast<float*>(v), static_cast<float*>(out), ws_o, ws_ml, q_len,
                        kv_len, group, k_hs, v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len,
-                       static_cast<const float*>(nk), static_cast<const float*>(nv), n_hs, n_rs, n_new, bs);
+                       static_cast<const float*>(nk), static_cast<const float*>(nv), n_hs, n_rs, n_new, bs, len_dev);
   }
   int s = launch_status();
   if (s != 0 || p.n_split == 1) return s;
@@ -852,10 +867,11 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
 
 int launch_attn(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
                 long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
-                long long n_hs, long long n_rs, int n_new, int n_batch, BatchStrides bs, hipStream_t st) {
+                long long n_hs, long long n_rs, int n_new, int n_batch, BatchStrides bs, const int32_t* len_dev,
+                hipStream_t st) {
 #define STD_LAUNCH_NT(N)                                                                                       \
   launch_nt<N>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs, n_new, \
-               n_batch, bs, st)
+               n_batch, bs, len_dev, st)
   switch ((group * q_len + 15) / 16) {
     case 1: return STD_LAUNCH_NT(1);
     case 2: return STD_LAUNCH_NT(2);
@@ -875,7 +891,7 @@ size_t attn_workspace_bytes(int n_kv, int rows, int kv_len, int dtype) {
 int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, int q_len, int kv_len, int d,
                long long k_hs, long long v_hs, float scale, int dtype, void* ws, size_t ws_bytes, const void* nk,
                const void* nv, long long n_hs, long long n_rs, int n_new, void* stream, int n_batch = 1,
-               BatchStrides bs = BatchStrides{0, 0, 0, 0}) {
+               BatchStrides bs = BatchStrides{0, 0, 0, 0}, const int32_t* len_dev = nullptr) {
   if (!q || !k || !v || !out) return STD_E_NULL;
   if (n_batch < 1 || n_batch > 65535) return STD_E_SHAPE;
   if (n_batch == 1) {
@@ -902,7 +918,7 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
   if (need > 0 && (ws == nullptr || ws_bytes < need)) return STD_E_WORKSPACE;
   if (need > 0 && !aligned16(ws)) return STD_E_ALIGN;
   return launch_attn(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs,
-                     n_new, n_batch, bs, static_cast<hipStream_t>(stream));
+                     n_new, n_batch, bs, len_dev, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -971,4 +987,14 @@ extern "C" int std_verify_attn_append(const void* q, void* k_cache, void* v_cach
                                       size_t workspace_bytes, void* stream) {
   return attn_entry(q, k_cache, v_cache, out, n_q, n_kv, q_len, kv_len, d, k_head_stride, v_head_stride, scale, dtype,
                     workspace, workspace_bytes, new_k, new_v, new_head_stride, new_row_stride, q_len, stream);
+}
+
+extern "C" int std_attn_devlen(const void* q, const void* k_cache, const void* v_cache, void* out, int n_q, int n_kv,
+                               int q_len, const int32_t* len_dev, int max_kv_len, int d, long long k_head_stride,
+                               long long v_head_stride, float scale, int dtype, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (!len_dev) return STD_E_NULL;
+  return attn_entry(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), out, n_q, n_kv, q_len, max_kv_len, d,
+                    k_head_stride, v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0, 0,
+                    stream, 1, BatchStrides{0, 0, 0, 0}, len_dev);
 }

@@ -49,17 +49,21 @@ def _workspace(nbytes: int, dev: torch.device) -> Tuple[int, torch.Tensor]:
 
 
 _ATTN_WS = {}
+_ATTN_WS_RETIRED = []
 
 
 def _attn_workspace(nbytes: int, dev: torch.device) -> int:
     """Persistent attention workspace per (device, stream): calls on one stream
     are ordered and may share it (no per-call allocation on the decode path);
-    another stream gets its own."""
+    another stream gets its own. A workspace outgrown by a larger call is kept
+    alive (never freed), since a captured HIP graph may still address it."""
     if nbytes == 0:
         return 0
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
     buf = _ATTN_WS.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _ATTN_WS_RETIRED.append(buf)
         buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _ATTN_WS[key] = buf
     return buf.data_ptr()
@@ -358,6 +362,93 @@ def kv_append(cache_k: torch.Tensor, cache_v: torch.Tensor, new_k: torch.Tensor,
     _lib.call("std_kv_append", cache_k.data_ptr(), cache_v.data_ptr(), new_k.data_ptr(), new_v.data_ptr(),
               cache_k.shape[1], rows, HEAD_DIM, cache_k.stride(1), new_k.stride(1), new_k.stride(2),
               cache_k.shape[2], length.data_ptr(), code, _stream(dev))
+
+
+def _check_dev_scalar(name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.int32 or t.numel() < 1 or not t.is_contiguous():
+        raise TypeError(f"{name} must be a contiguous device int32 tensor")
+
+
+def rope_append(qkv: torch.Tensor, n_q: int, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                length: torch.Tensor, position: torch.Tensor, inv_freq: torch.Tensor, pos_offset: int = 0,
+                q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rotary embedding of this step's rows plus the K/V cache append, with
+    the length and the position read on the device (one launch).
+
+    qkv [1, n, (n_q + 2 n_kv) D]: the fused q|k|v projection output (rows
+    contiguous in the head dim). Row r has position position[0] + pos_offset
+    + r; its rotated keys and its values go to cache row length[0] + r.
+    Returns the rotated queries [1, n_q, n, D] (q_out if given). Restates
+    apply_multimodal_rotary_pos_emb (modeling_qwen2_5_vl.py:690-732) for text
+    positions and KVCache.cat (kv_cache.py:54-69); the length is not advanced."""
+    dev = _check_device(qkv, key_cache, value_cache, length, position, inv_freq)
+    code = _dtype_code(qkv)
+    if qkv.dim() != 3 or qkv.shape[0] != 1 or qkv.stride(2) != 1:
+        raise ValueError(f"qkv must be [1, n, width] with a contiguous last dim, got {tuple(qkv.shape)}")
+    _check_cache_view("key_cache", key_cache)
+    _check_cache_view("value_cache", value_cache)
+    if value_cache.shape != key_cache.shape or value_cache.stride(1) != key_cache.stride(1):
+        raise ValueError("key and value caches must share shape and head stride")
+    if key_cache.dtype != qkv.dtype or value_cache.dtype != qkv.dtype:
+        raise TypeError("caches must have the qkv dtype")
+    n_kv = key_cache.shape[1]
+    n = qkv.shape[1]
+    if n_q % n_kv or qkv.shape[2] < (n_q + 2 * n_kv) * HEAD_DIM:
+        raise ValueError(f"qkv width {qkv.shape[2]} too small for {n_q} + 2 x {n_kv} heads")
+    _check_dev_scalar("length", length)
+    _check_dev_scalar("position", position)
+    if inv_freq.dtype != torch.float32 or inv_freq.numel() != HEAD_DIM // 2 or not inv_freq.is_contiguous():
+        raise TypeError("inv_freq must be a contiguous float32 tensor of head_dim / 2 entries")
+    if q_out is None:
+        q_out = torch.empty(1, n_q, n, HEAD_DIM, dtype=qkv.dtype, device=dev)
+    elif tuple(q_out.shape) != (1, n_q, n, HEAD_DIM) or q_out.dtype != qkv.dtype or not q_out.is_contiguous():
+        raise ValueError("q_out must be a contiguous [1, n_q, n, D] tensor of the qkv dtype")
+    _lib.call("std_rope_append", qkv.data_ptr(), qkv.stride(1), q_out.data_ptr(), key_cache.data_ptr(),
+              value_cache.data_ptr(), n, n_q, n_kv, HEAD_DIM, key_cache.stride(1), key_cache.shape[2],
+              length.data_ptr(), position.data_ptr(), int(pos_offset), inv_freq.data_ptr(), code, _stream(dev))
+    return q_out
+
+
+def attention_devlen(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                     length: torch.Tensor, max_kv_len: int, scale: Optional[float] = None,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Offset-causal GQA attention with the cache length read on the device:
+    keys [0, length[0] + q_len) are valid (this step's q_len rows last) and
+    query row i sees keys [0, length[0] + i]; q_len == 1 is the decode. The
+    launch is planned for max_kv_len (<= the cache capacity), so one captured
+    graph serves every length up to it; a device length past
+    max_kv_len - q_len yields NaN outputs. query [1, n_q, q_len, D]."""
+    dev = _check_device(query, key_cache, value_cache, length)
+    code = _dtype_code(query)
+    if query.dim() != 4 or query.shape[0] != 1:
+        raise ValueError(f"Expected query [1, n_q, q_len, D], got {tuple(query.shape)}")
+    if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
+        raise TypeError("query and caches must share a dtype")
+    _check_cache_view("key_cache", key_cache)
+    _check_cache_view("value_cache", value_cache)
+    _check_rows_contiguous("query", query)
+    _check_dev_scalar("length", length)
+    if value_cache.shape != key_cache.shape:
+        raise ValueError("key and value caches differ in shape")
+    _, n_q, q_len, d = query.shape
+    n_kv = key_cache.shape[1]
+    if not (q_len <= max_kv_len <= key_cache.shape[2]):
+        raise ValueError(f"max_kv_len={max_kv_len} must be in [q_len, cache capacity {key_cache.shape[2]}]")
+    if d != HEAD_DIM or n_q % n_kv:
+        raise ValueError("unsupported head_dim or head counts")
+    if out is None:
+        out = torch.empty_like(query)
+    elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like query")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    lib = _lib.load_library()
+    ws_bytes = lib.std_verify_attn_workspace_bytes(n_q, n_kv, q_len, max_kv_len, d)
+    ws_ptr = _attn_workspace(ws_bytes, dev)
+    _lib.call("std_attn_devlen", query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), out.data_ptr(), n_q,
+              n_kv, q_len, length.data_ptr(), int(max_kv_len), d, key_cache.stride(1), value_cache.stride(1),
+              float(scale), code, ws_ptr, ws_bytes, _stream(dev))
+    return out
 
 
 def len_add(length: torch.Tensor, delta: int) -> None:

@@ -1,0 +1,123 @@
+"""Device-length decode-step glue on the GPU: the fused rotary embedding +
+K/V append (std_rope_append) against the rope oracle and torch's own
+evaluation, and the device-length attention (std_attn_devlen) against the
+host-length kernels and the attention oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as ref_attn
+from oracle import rope as ref_rope
+from std_amd import ops
+from tests.gpu_helpers import announce, assert_close, dev
+
+pytestmark = pytest.mark.gpu
+
+D, NQ, NKV = 128, 28, 4
+
+
+def _qkv(n, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(1, n, (NQ + 2 * NKV) * D, generator=g).to(dtype)
+
+
+def _scalar(v):
+    return torch.tensor([v], dtype=torch.int32, device=dev())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rope_append_matches_oracle(dtype):
+    n, cap, length, pos, off = 10, 300, 137, 131000, 3
+    announce(f"rope_append {dtype} n={n} len={length} pos={pos}+{off}")
+    qkv = _qkv(n, dtype, 11)
+    kc = torch.full((1, NKV, cap, D), float("nan"), dtype=dtype, device=dev())
+    vc = torch.full_like(kc, float("nan"))
+    inv = ref_rope.inv_freq(1e6, D)
+    q = ops.rope_append(qkv.to(dev()), NQ, kc, vc, _scalar(length), _scalar(pos), torch.from_numpy(inv).to(dev()),
+                        pos_offset=off)
+    torch.cuda.synchronize()
+    name = "bf16" if dtype == torch.bfloat16 else "fp32"
+    x = qkv[0].float().numpy().reshape(n, NQ + 2 * NKV, D)
+    cos, sin = ref_rope.cos_sin(pos + off + np.arange(n), inv, name)
+    want_q = ref_rope.apply_rope(x[:, :NQ].transpose(1, 0, 2), cos, sin, name)          # [NQ, n, D]
+    want_k = ref_rope.apply_rope(x[:, NQ:NQ + NKV].transpose(1, 0, 2), cos, sin, name)  # [NKV, n, D]
+    got_q = q[0].float().cpu().numpy()
+    got_k = kc[0, :, length:length + n].float().cpu().numpy()
+    for got, want in ((got_q, want_q), (got_k, want_k)):
+        diff = np.abs(got - want)
+        if dtype == torch.bfloat16:   # one bf16 ulp at most, where the two cos/sin round differently
+            assert (diff <= np.spacing(np.abs(want)) * 65536).all() and (diff == 0).mean() > 0.995
+        else:   # fp32 cos/sin of angles up to 1.3e5 rad: the device's and the oracle's differ by an ulp often
+            assert diff.max() <= 1e-6
+    np.testing.assert_array_equal(vc[0, :, length:length + n].float().cpu().numpy(),
+                                  x[:, NQ + NKV:].transpose(1, 0, 2))
+    untouched = torch.cat([kc[0, :, :length], kc[0, :, length + n:], vc[0, :, :length], vc[0, :, length + n:]], 1)
+    assert torch.isnan(untouched).all()
+
+
+def test_rope_append_matches_torch_on_device_and_skips_rows_past_capacity():
+    n, cap = 6, 64
+    announce("rope_append vs torch formula on the device; capacity edge")
+    dtype = torch.bfloat16
+    qkv = _qkv(n, dtype, 12).to(dev())
+    kc = torch.zeros(1, NKV, cap, D, dtype=dtype, device=dev())
+    vc = torch.zeros_like(kc)
+    inv = torch.from_numpy(ref_rope.inv_freq(1e6, D)).to(dev())
+    length, pos = cap - 4, 77777
+    q = ops.rope_append(qkv, NQ, kc, vc, _scalar(length), _scalar(pos), inv)
+    freqs = (pos + torch.arange(n, device=dev())).float()[:, None] * inv[None, :]
+    emb = torch.cat([freqs, freqs], -1)
+    c, s = emb.cos().to(dtype), emb.sin().to(dtype)
+    x = qkv[0].view(n, NQ + 2 * NKV, D).transpose(0, 1)
+    rot = torch.cat([-x[..., 64:], x[..., :64]], -1)
+    want = (x * c) + (rot * s)
+    diff = (q[0].float() - want[:NQ].float()).abs()
+    assert (diff == 0).float().mean() > 0.995
+    assert (diff <= want[:NQ].float().abs() * 2 ** -7 + 1e-30).all()
+    torch.testing.assert_close(kc[0, :, length:], want[NQ:NQ + NKV, :4], rtol=2 ** -7, atol=0)
+    assert (kc[0, :, :length] == 0).all()           # rows 4, 5 fall past the capacity: not written
+
+
+@pytest.mark.parametrize("dtype,q_len,kv,cap", [(torch.bfloat16, 10, 4106, 4500), (torch.float32, 10, 8202, 8400),
+                                                 (torch.bfloat16, 1, 131072, 131200)])
+def test_attention_devlen_equals_host_length_kernel(dtype, q_len, kv, cap):
+    """With >= 64 tiles the split plan is the same at kv and at cap, so the
+    device-length launch reproduces the host-length launch bit for bit."""
+    announce(f"attention_devlen {dtype} q_len={q_len} kv={kv} cap={cap}")
+    g = torch.Generator(device=dev()).manual_seed(21)
+    k = torch.randn(1, NKV, cap, D, generator=g, device=dev()).to(dtype)
+    v = torch.randn(1, NKV, cap, D, generator=g, device=dev()).to(dtype)
+    q = torch.randn(1, NQ, q_len, D, generator=g, device=dev()).to(dtype)
+    got = ops.attention_devlen(q, k, v, _scalar(kv - q_len), max_kv_len=cap)
+    want = ops.verify_attention(q, k[:, :, :kv], v[:, :, :kv])
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attention_devlen_small_cache_matches_oracle(dtype):
+    cap, kv = 1163, 1034
+    announce(f"attention_devlen decode {dtype} kv={kv} planned for {cap}")
+    g = torch.Generator().manual_seed(22)
+    k = torch.randn(1, NKV, cap, D, generator=g).to(dtype)
+    v = torch.randn(1, NKV, cap, D, generator=g).to(dtype)
+    q = torch.randn(1, NQ, 1, D, generator=g).to(dtype)
+    kd, vd = k.to(dev()), v.to(dev())
+    kd[:, :, kv:] = float("nan")                    # rows past the device length must never be read
+    vd[:, :, kv:] = float("nan")
+    got = ops.attention_devlen(q.to(dev()), kd, vd, _scalar(kv - 1), max_kv_len=cap)
+    assert_close(got, ref_attn.gqa_sdpa(q, k[:, :, :kv], v[:, :, :kv]), dtype)
+    for q_len in (3, 10):
+        qv = torch.randn(1, NQ, q_len, D, generator=g).to(dtype)
+        got = ops.attention_devlen(qv.to(dev()), kd, vd, _scalar(kv - q_len), max_kv_len=cap)
+        assert_close(got, ref_attn.verify_attention(qv, k[:, :, :kv], v[:, :, :kv]), dtype)
+
+
+def test_attention_devlen_rejects_length_past_plan_with_nan():
+    announce("attention_devlen with a device length past max_kv_len - q_len")
+    k = torch.randn(1, NKV, 512, D, device=dev()).to(torch.bfloat16)
+    q = torch.randn(1, NQ, 4, D, device=dev()).to(torch.bfloat16)
+    for bad in (300, -1):
+        out = ops.attention_devlen(q, k, k, _scalar(bad), max_kv_len=300)
+        torch.cuda.synchronize()
+        assert torch.isnan(out.float()).all()
