@@ -8,13 +8,19 @@ reference's position ids (three identical rows, modeling_qwen2_5_vl.py:1368-1384
 the multimodal rotary embedding with mrope_section [16, 24, 24] equals the
 1-D rotary embedding (theta 1e6) used here.
 
-Attention on the decode hot path runs in libstdhip.so:
-  * q_len == 1 (sparse draft over the compact cache, or dense AR decode):
-    ``ops.gqa_decode_append`` writes the new K/V row and attends, one launch;
-  * 1 < q_len <= 96 / group (dense verify of gamma + 1 rows):
-    ``ops.verify_attention_append`` (offset-causal, one launch).
-Longer inputs (the prompt prefill, which is not part of the decode path) use
-chunked fp32 matrix products in torch.
+Attention on the decode hot path runs in libstdhip.so. For q_len <= 96 / group
+(the sparse draft and the dense AR decode at q_len == 1, the dense verify of
+gamma + 1 rows) a layer is two launches after the q|k|v projection:
+``ops.rope_append`` (rotary embedding of the rows, K/V written into the cache)
+and ``ops.attention_devlen`` (offset-causal attention), both reading the cache
+length and the position from a device int32 pair (length, position). Eager
+calls upload that pair from the host lengths; graph-captured steps pass
+``step_state`` and the pair then lives on the device only (advanced by the
+step's row count, rolled back by the acceptance kernel), so one captured
+graph replays every round. The launches are planned for the cache capacity,
+so eager and captured steps run identical kernels. Longer inputs (the prompt
+prefill, which is not part of the decode path) use torch's rotary embedding
+and chunked fp32 matrix products.
 
 Dense GEMMs/GEMVs, norms and the MLP run in torch (hipBLASLt).
 """
@@ -158,12 +164,30 @@ class RandomDecoder:
                 out[0, g * g_size:(g + 1) * g_size, c0:c1] = o.view(g_size, c1 - c0, c.head_dim).to(q.dtype)
         return out
 
-    def _attention(self, li: int, h: torch.Tensor, cos, sin, kc: KVCache, vc: KVCache) -> torch.Tensor:
+    def fused_rows(self, n: int) -> bool:
+        """Whether n rows per step take the HIP rope/append + attention path."""
+        c = self.config
+        return n * (c.num_attention_heads // c.num_key_value_heads) <= MAX_FUSED_ROWS
+
+    def _attention(self, li: int, h: torch.Tensor, cos, sin, kc: KVCache, vc: KVCache,
+                   state: Optional[torch.Tensor], host_lengths: bool) -> torch.Tensor:
         c = self.config
         p = self.layers[li]
         n = h.shape[1]
         hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         qkv = F.linear(h, p["qkv_w"], p["qkv_b"])                            # [1, n, (hq + 2hkv) d]
+        controller = self.sparse_controller
+        if controller is not None and controller.enabled and n != 1:
+            raise RuntimeError("Sparse draft attention currently expects autoregressive q_len=1 calls.")
+        if self.fused_rows(n):
+            q = ops.rope_append(qkv, hq, kc.data, vc.data, state[0:1], state[1:2], self.inv_freq)
+            if self.capture_text_queries:
+                self.captured_queries[li] = q
+            out = ops.attention_devlen(q, kc.data, vc.data, state[0:1], max_kv_len=kc.capacity)
+            if host_lengths:
+                kc.advance(n)
+                vc.advance(n)
+            return F.linear(out.transpose(1, 2).reshape(1, n, hq * d), p["o_w"])
         q = qkv[..., :hq * d].view(1, n, hq, d).transpose(1, 2)
         k = qkv[..., hq * d:(hq + hkv) * d].view(1, n, hkv, d).transpose(1, 2)
         v = qkv[..., (hq + hkv) * d:].view(1, n, hkv, d).transpose(1, 2)
@@ -172,20 +196,9 @@ class RandomDecoder:
         v = v.contiguous()
         if self.capture_text_queries:
             self.captured_queries[li] = q
-        controller = self.sparse_controller
-        if controller is not None and controller.enabled and n != 1:
-            raise RuntimeError("Sparse draft attention currently expects autoregressive q_len=1 calls.")
-        pos = kc.length
-        if n == 1:
-            out = ops.gqa_decode_append(q, kc.data, vc.data, k, v, kv_len=pos + 1)
-            kc.advance(1)
-            vc.advance(1)
-        elif n * (hq // hkv) <= MAX_FUSED_ROWS:
-            out = ops.verify_attention_append(q, kc.data, vc.data, k, v, kv_len=pos + n)
-            kc.advance(n)
-            vc.advance(n)
-        else:
-            out = self._prefill_attention(q, k, v, kc, vc)
+        if not host_lengths:
+            raise ValueError("a device-state step must have at most 96 query rows per KV head")
+        out = self._prefill_attention(q, k, v, kc, vc)
         out = out.transpose(1, 2).reshape(1, n, hq * d)
         return F.linear(out, p["o_w"])
 
@@ -199,24 +212,48 @@ class RandomDecoder:
     @torch.inference_mode()
     def forward(self, input_ids: torch.Tensor, past_key_values: List[List[KVCache]],
                 position_ids: Optional[torch.Tensor] = None, visual_embeds: Optional[torch.Tensor] = None,
-                all_logits: bool = False, start_position: Optional[int] = None) -> torch.Tensor:
+                all_logits: bool = False, start_position: Optional[int] = None,
+                step_state: Optional[torch.Tensor] = None) -> torch.Tensor:
         """input_ids [1, n]; returns logits [1, n, vocab] if all_logits else
         [1, 1, vocab] for the last position. Positions default to
         ``past + arange(n)`` with past = the cache length (the reference's
         cache_position); the sparse draft passes its original positions, as a
-        tensor or (without a host-to-device copy) as ``start_position``."""
+        tensor or (without a host-to-device copy) as ``start_position``.
+
+        step_state: a device int32 [2] = (cache length, position of row 0). The
+        step then reads both on the device, advances both by n at its end and
+        leaves the host lengths alone (graph capture); without it they come
+        from the host lengths and start_position, and the host lengths advance."""
         n = input_ids.shape[1]
         x = self.embed(input_ids, visual_embeds)
-        if position_ids is not None:
-            position_ids = position_ids.reshape(-1).to(self.device)
+        host_lengths = step_state is None
+        cos = sin = None
+        if self.fused_rows(n):
+            if host_lengths:
+                past = past_key_values[0][0].length
+                if start_position is not None:
+                    pos0 = int(start_position)
+                elif position_ids is not None:
+                    pos0 = int(position_ids.reshape(-1)[0])
+                else:
+                    pos0 = past
+                step_state = torch.tensor([past, pos0], dtype=torch.int32).to(self.device)
         else:
-            past = past_key_values[0][0].length if start_position is None else int(start_position)
-            position_ids = torch.arange(past, past + n, device=self.device)
-        cos, sin = self._rope(position_ids)
+            if not host_lengths:
+                raise ValueError("a device-state step must have at most 96 query rows per KV head")
+            if position_ids is not None:
+                position_ids = position_ids.reshape(-1).to(self.device)
+            else:
+                past = past_key_values[0][0].length if start_position is None else int(start_position)
+                position_ids = torch.arange(past, past + n, device=self.device)
+            cos, sin = self._rope(position_ids)
         for li in range(self.config.num_hidden_layers):
             kc, vc = past_key_values[li]
-            x = x + self._attention(li, self._rms_norm(x, self.layers[li]["ln1"]), cos, sin, kc, vc)
+            x = x + self._attention(li, self._rms_norm(x, self.layers[li]["ln1"]), cos, sin, kc, vc, step_state,
+                                    host_lengths)
             x = x + self._mlp(li, self._rms_norm(x, self.layers[li]["ln2"]))
+        if not host_lengths:
+            ops.len_add(step_state, n)
         if not all_logits:
             x = x[:, -1:]
         return F.linear(self._rms_norm(x, self.norm), self.lm_head)

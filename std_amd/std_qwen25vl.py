@@ -286,15 +286,42 @@ def _cache_capacity(prompt_len: int, max_new_tokens: int, gamma: int) -> int:
 
 
 # ---------------------------------------------------------------------------
+# HIP-graph capture of device-state decode steps.
+
+def _warm_and_capture(run_all, restore, phases):
+    """Run `run_all` once on a side stream (lazy library set-up stays out of
+    the capture), undo its effect on the decode state with `restore`, then
+    capture each phase (fn, args) in order into its own HIP graph. Returns
+    [(graph, outputs)]; capturing executes nothing, so every phase reads the
+    static outputs of the phases before it only when replayed in order."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run_all()
+    torch.cuda.current_stream().wait_stream(side)
+    restore()
+    torch.cuda.synchronize()
+    captured = []
+    for fn, args in phases:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = fn(*[a() if callable(a) else a for a in args])
+        captured.append((graph, out))
+    return captured
+
+
+# ---------------------------------------------------------------------------
 # Orchestrators.
 
 @torch.inference_mode()
 def ar_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id: int, eos_token_id: int,
                          max_new_tokens: int = 256, output_attentions: bool = False, profile_prefill: bool = False,
-                         ignore_eos: bool = False) -> GenerateResult:
+                         ignore_eos: bool = False, use_graphs: bool = False) -> GenerateResult:
     """Greedy dense decoding with the same two-stage prefill
-    (std_qwen25vl.py:553-606); every decode step is one HIP decode launch per
-    layer over the full dense cache."""
+    (std_qwen25vl.py:553-606); every decode step runs the HIP rope/append and
+    attention launches of each layer over the full dense cache. With
+    use_graphs the step (cache length and position on the device) is captured
+    once in a HIP graph and replayed per token."""
     del output_attentions
     torch.cuda.synchronize()
     start = time.time()
@@ -308,15 +335,38 @@ def ar_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id:
     prefill_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
 
     generated: List[torch.Tensor] = []
+    step = None
+    if use_graphs and max_new_tokens > 1:
+        state = torch.tensor([prompt_len, prompt_len], dtype=torch.int32).to(model.device)   # (length, position)
+        token = next_token.reshape(1, 1).clone()
+
+        def ar_step():
+            token.copy_(_token_argmax(model(token, pkv, step_state=state)))
+            return token
+
+        snap = (state.clone(), token.clone())
+
+        def restore():
+            state.copy_(snap[0])
+            token.copy_(snap[1])
+
+        (graph, _), = _warm_and_capture(ar_step, restore, [(ar_step, ())])
+        next_token = token
+        step = graph.replay
     torch.cuda.synchronize()
     decode_start = time.time()
     while len(generated) < max_new_tokens:
-        generated.append(next_token.reshape(1))
+        generated.append(next_token.reshape(1).clone() if step is not None else next_token.reshape(1))
         if not ignore_eos and int(next_token) == eos_token_id:
             break
         if len(generated) == max_new_tokens:
             break
-        next_token = _token_argmax(model(next_token, pkv))
+        if step is not None:
+            step()
+        else:
+            next_token = _token_argmax(model(next_token, pkv))
+    if step is not None:
+        fill_cache_length(lengths, prompt_len + len(generated) - 1)
     torch.cuda.synchronize()
     end = time.time()
     gen = torch.cat(generated) if generated else torch.empty(0, dtype=torch.long, device=model.device)
@@ -334,9 +384,16 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
                           adaptive_gamma_min: Optional[int] = None, adaptive_gamma_mode: str = "accept_len",
                           copy_sparse_prefill: bool = True, profile_prefill: bool = False,
                           verify_attn_backend: str = "math", verify_margin_threshold: Optional[float] = None,
-                          use_compile: bool = False, ignore_eos: bool = False
+                          use_compile: bool = False, ignore_eos: bool = False, use_graphs: bool = False
                           ) -> Tuple[GenerateResult, SparseSelection]:
-    """Sparse-to-Dense greedy decoding (std_qwen25vl.py:609-978)."""
+    """Sparse-to-Dense greedy decoding (std_qwen25vl.py:609-978).
+
+    use_graphs: keep both caches' lengths and positions on the device (the
+    acceptance kernel rolls them back) and replay each full-gamma round with a
+    pending token as three captured HIP graphs (gamma sparse draft steps; the
+    dense verify forward with greedy acceptance; the sparse bonus step), with
+    one readback per round; the first round and any shorter round run the same
+    device-state steps eagerly."""
     if verify_mode != "parallel":
         raise ValueError(f"Unsupported verify_mode={verify_mode!r}; the HIP path implements 'parallel'.")
     if verify_fallback != "none" or verify_margin_threshold is not None:
@@ -394,6 +451,69 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     current_gamma = gamma
     dense_next_i32 = dense_next.reshape(1).to(torch.int32)
 
+    # Device decode state for use_graphs: (dense length, dense position,
+    # sparse length, sparse position). The dense position is the dense length
+    # (cache_position); the sparse position is the original position of the
+    # next drafted token. Both caches' pairs advance with their steps and are
+    # rolled back together by the acceptance kernel.
+    st4 = tok_s = pending = None
+    graphs = None
+    if use_graphs:
+        st4 = torch.tensor([prompt_len, prompt_len, sparse_prompt_len, prompt_len], dtype=torch.int32).to(dev)
+        tok_s = sparse_next.reshape(1, 1).clone()
+        pending = torch.zeros(1, dtype=torch.long, device=dev)
+
+    def draft_phase(n_steps: int) -> torch.Tensor:
+        drafted = []
+        controller.set_enabled(True)
+        try:
+            for _ in range(n_steps):
+                drafted.append(tok_s.reshape(1).clone())
+                tok_s.copy_(_token_argmax(model(tok_s, sparse_pkv, step_state=st4[2:4])))
+        finally:
+            controller.set_enabled(False)
+        return torch.cat(drafted)
+
+    def verify_phase(draft: torch.Tensor, has_pending: bool) -> torch.Tensor:
+        ids = torch.cat([pending, draft]) if has_pending else draft
+        logits = model(ids.reshape(1, -1), dense_pkv, step_state=st4[0:2], all_logits=True)
+        return ops.greedy_accept(logits[0], draft.to(torch.int32), has_pending=has_pending,
+                                 dense_next=None if has_pending else dense_next_i32, rollback_lengths=st4)
+
+    def bonus_phase(res: torch.Tensor) -> torch.Tensor:
+        pending.copy_(res[1:2].to(torch.long))
+        controller.set_enabled(True)
+        try:
+            tok_s.copy_(_token_argmax(model(pending.reshape(1, 1), sparse_pkv, step_state=st4[2:4])))
+        finally:
+            controller.set_enabled(False)
+        return tok_s
+
+    def capture_round():
+        snap = (st4.clone(), tok_s.clone(), pending.clone())
+
+        def run_all():
+            bonus_phase(verify_phase(draft_phase(gamma), True))
+
+        def restore():
+            st4.copy_(snap[0])
+            tok_s.copy_(snap[1])
+            pending.copy_(snap[2])
+
+        holder = {}
+
+        def draft_static():
+            holder["draft"] = draft_phase(gamma)
+            return holder["draft"]
+
+        def verify_static(has_pending):
+            holder["res"] = verify_phase(holder["draft"], has_pending)
+            return holder["res"]
+
+        caps = _warm_and_capture(run_all, restore, [(draft_static, ()), (verify_static, (True,)),
+                                                    (lambda: bonus_phase(holder["res"]), ())])
+        return caps, holder["draft"], holder["res"]
+
     torch.cuda.synchronize()
     decode_start = time.time()
     while len(generated) < max_new_tokens:
@@ -404,23 +524,39 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         context_len = prompt_len + len(generated)
         dense_cached_len = context_len - len(dense_pending)
         sparse_prev_len = sparse_prompt_len + len(generated)
+        replay = use_graphs and bool(dense_pending) and propose_len == gamma
+        if replay and graphs is None:
+            graphs = capture_round()
 
         stage = _profile_mark(profile_decode)
-        draft_dev = _draft_tokens(model, sparse_next, propose_len, sparse_pkv, controller, start_position=context_len)
+        if replay:
+            graphs[0][0][0].replay()
+            draft_dev = graphs[1]
+        elif use_graphs:
+            draft_dev = draft_phase(propose_len)
+        else:
+            draft_dev = _draft_tokens(model, sparse_next, propose_len, sparse_pkv, controller,
+                                      start_position=context_len)
         draft_time += _profile_mark(profile_decode) - stage
         proposed_total += propose_len
         proposed_lengths.append(propose_len)
         pending_lengths.append(len(dense_pending))
 
         stage = _profile_mark(profile_decode)
-        if dense_pending:
-            pend = torch.tensor(dense_pending, dtype=torch.long).to(dev, non_blocking=True)
-            verify_ids = torch.cat([pend, draft_dev]).reshape(1, -1)
+        if replay:
+            graphs[0][1][0].replay()
+            res = graphs[2]
+        elif use_graphs:
+            res = verify_phase(draft_dev, bool(dense_pending))
         else:
-            verify_ids = draft_dev.reshape(1, -1)
-        logits = model(verify_ids, dense_pkv, all_logits=True)
-        res = ops.greedy_accept(logits[0], draft_dev.to(torch.int32), has_pending=bool(dense_pending),
-                                dense_next=None if dense_pending else dense_next_i32)
+            if dense_pending:
+                pend = torch.tensor(dense_pending, dtype=torch.long).to(dev, non_blocking=True)
+                verify_ids = torch.cat([pend, draft_dev]).reshape(1, -1)
+            else:
+                verify_ids = draft_dev.reshape(1, -1)
+            logits = model(verify_ids, dense_pkv, all_logits=True)
+            res = ops.greedy_accept(logits[0], draft_dev.to(torch.int32), has_pending=bool(dense_pending),
+                                    dense_next=None if dense_pending else dense_next_i32)
         host = torch.cat([res[:2], draft_dev.to(torch.int32)]).tolist()     # the round's one readback
         accept_len, bonus_token, draft = host[0], host[1], host[2:]
         verify_time += _profile_mark(profile_decode) - stage
@@ -457,9 +593,16 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
 
         dense_pending = [bonus_token]
         stage = _profile_mark(profile_decode)
-        bonus_dev = torch.tensor([bonus_token], dtype=torch.long).to(dev, non_blocking=True)
-        sparse_next = _append_sparse_tokens(model, bonus_dev, sparse_pkv, controller,
-                                            start_position=context_len + accept_len)
+        if replay:
+            graphs[0][2][0].replay()
+        elif use_graphs:
+            bonus_phase(res)
+        else:
+            bonus_dev = torch.tensor([bonus_token], dtype=torch.long).to(dev, non_blocking=True)
+            sparse_next = _append_sparse_tokens(model, bonus_dev, sparse_pkv, controller,
+                                                start_position=context_len + accept_len)
+        if use_graphs:
+            fill_cache_length(sparse_lengths, sparse_prev_len + accept_len + 1)
         bonus_time += _profile_mark(profile_decode) - stage
 
     torch.cuda.synchronize()

@@ -114,3 +114,56 @@ def test_full_selection_draft_equals_dense(tiny32):
     assert std.acceptance_rate == 1.0
     ar = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=36, ignore_eos=True)
     assert first_divergence(std.output_ids, ar.output_ids) is None
+
+
+def test_graph_rounds_equal_eager_rounds_fp32(tiny32):
+    """The graph-replayed loops (cache lengths and positions on the device,
+    rolled back by the acceptance kernel; one captured draft, verify and
+    bonus graph replayed per round) give the eager loops' tokens and accept
+    lengths, and STD still equals dense AR."""
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 5)
+    announce("e2e graph vs eager, STD and AR, tiny fp32, 40 tokens, gamma 4")
+    kw = dict(max_new_tokens=40, ignore_eos=True)
+    std_e, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, gamma=4,
+                                     target_k_plus_text=TARGET, use_graphs=False, **kw)
+    std_g, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, gamma=4,
+                                     target_k_plus_text=TARGET, use_graphs=True, **kw)
+    assert std_g.decode_rounds >= 3                       # rounds 2.. replay the captured graphs
+    assert std_g.accept_lengths == std_e.accept_lengths and std_g.proposed_lengths == std_e.proposed_lengths
+    assert first_divergence(std_g.output_ids, std_e.output_ids) is None
+    ar_e = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, use_graphs=False, **kw)
+    ar_g = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, use_graphs=True, **kw)
+    assert first_divergence(ar_g.output_ids, ar_e.output_ids) is None
+    assert first_divergence(std_g.output_ids, ar_g.output_ids) is None
+
+
+def test_graph_full_selection_accepts_every_draft(tiny32):
+    """Full selection with the graph-replayed rounds: any error in the device
+    positions, lengths or rollback would reject drafts."""
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 21, n_visual=300, n_text=20)
+    announce("e2e graph rounds, tiny fp32, k = all visual positions")
+    std, sel = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=40, gamma=5,
+                                     explicit_k=300, ignore_eos=True, use_graphs=True)
+    assert sel.compact_len == 320 and std.decode_rounds >= 4
+    assert std.accept_lengths == std.proposed_lengths, (std.accept_lengths, std.proposed_lengths)
+    ar = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=40, ignore_eos=True,
+                              use_graphs=True)
+    assert first_divergence(std.output_ids, ar.output_ids) is None
+
+
+def test_graph_rounds_bf16_with_eos_stop():
+    cfg = DecoderConfig.tiny(layers=2)
+    model = RandomDecoder(cfg, dev(), torch.bfloat16, seed=7)
+    inputs = _inputs(cfg, 9, dtype=torch.bfloat16)
+    announce("e2e graph rounds tiny bf16, 32 tokens, EOS stop")
+    std, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=32, gamma=9,
+                                   target_k_plus_text=TARGET, ignore_eos=True, use_graphs=True)
+    gen = std.output_ids[0, -std.generate_len:].tolist()
+    assert std.generate_len == 32 and all(0 <= a <= p for a, p in zip(std.accept_lengths, std.proposed_lengths))
+    eos = gen[5]
+    stop, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, eos, max_new_tokens=32, gamma=9,
+                                    target_k_plus_text=TARGET, ignore_eos=False, use_graphs=True)
+    got = stop.output_ids[0, -stop.generate_len:].tolist()
+    assert got == gen[:gen.index(eos) + 1]
