@@ -275,6 +275,28 @@ int std_attn_devlen(const void* q, const void* k_cache, const void* v_cache, voi
  * ------------------------------------------------------------------------ */
 size_t std_greedy_accept_workspace_bytes(int q_rows, int vocab);
 
+/* ------------------------------------------------------------------------
+ * Row argmax as int64 token ids (torch.argmax(logits, -1) semantics: first
+ * maximum, NaN counts as the maximum), with no memset and no global
+ * semaphore, so a captured HIP graph replays it correctly.
+ *
+ * Replaces the greedy next-token choice of the decode loops
+ *   (std_qwen25vl.py:544, :806 via torch.argmax). logits [rows][vocab] (row
+ * stride elements); workspace as std_greedy_accept_workspace_bytes(rows, vocab).
+ * ------------------------------------------------------------------------ */
+int std_argmax_rows(const void* logits, long long logits_row_stride, int rows, int vocab, int dtype,
+                    long long* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm, one workgroup per row, graph-capture safe (no global staging):
+ * out = weight * dtype(x * rsqrt(mean(x^2) + eps)).
+ *
+ * Replaces Qwen2RMSNorm.forward (modeling_qwen2_5_vl.py:192-197) in the
+ * decode steps; rows have strides x_row_stride / out_row_stride elements.
+ * ------------------------------------------------------------------------ */
+int std_rms_norm(const void* x, long long x_row_stride, const void* weight, void* out,
+                 long long out_row_stride, int rows, int hidden, float eps, int dtype, void* stream);
+
 int std_greedy_accept(const void* logits, long long logits_row_stride, int q_rows, int vocab,
                       int dtype, const int32_t* draft, int n_draft, int has_pending,
                       const int32_t* dense_next, int32_t* out,

@@ -94,6 +94,51 @@ accept_final_kernel(const uint2* __restrict__ part, int n_blocks, int q_rows, co
   }
 }
 
+// Final step of the row argmax: thread r reduces row r's block partials in
+// block order and writes the index as int64 (the token-id type of torch).
+__global__ void __launch_bounds__(256)
+argmax_final_kernel(const uint2* __restrict__ part, int n_blocks, int rows, long long* __restrict__ out) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  uint32_t bk = 0;
+  int bi = INT_MAX;
+  for (int b = 0; b < n_blocks; ++b) {
+    const uint2 v = part[(long long)r * n_blocks + b];
+    if (better(v.x, (int)v.y, bk, bi)) { bk = v.x; bi = (int)v.y; }
+  }
+  out[r] = bi;
+}
+
+// One block per row: out = weight * dtype(x * rsqrt(mean(x^2) + eps)), the
+// RMSNorm of modeling_qwen2_5_vl.py:192-197 with the products rounded to the
+// dtype as torch evaluates them; squares and their sum are fp32 (the sum in
+// this kernel's lane/wave order). No global staging, so it is safe to
+// capture in a HIP graph.
+template <typename T>
+__global__ void __launch_bounds__(256)
+rms_norm_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ out, int hidden, long long x_rs,
+                long long o_rs, float eps) {
+  __shared__ float red[4];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const T* xr = x + (long long)r * x_rs;
+  float ss = 0.f;
+  for (int i = tid; i < hidden; i += 256) {
+    const float v = to_f32<T>(xr[i]);
+    ss = __fadd_rn(ss, __fmul_rn(v, v));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float mean = ((red[0] + red[1]) + (red[2] + red[3])) * (1.0f / (float)hidden);
+  const float inv = rsqrtf(__fadd_rn(mean, eps));
+  T* orow = out + (long long)r * o_rs;
+  for (int i = tid; i < hidden; i += 256) {
+    const float n = to_f32<T>(from_f32<T>(__fmul_rn(to_f32<T>(xr[i]), inv)));
+    orow[i] = from_f32<T>(__fmul_rn(to_f32<T>(w[i]), n));
+  }
+}
+
 __global__ void __launch_bounds__(256)
 kv_append_kernel(char* __restrict__ ck, char* __restrict__ cv, const char* __restrict__ nk,
                  const char* __restrict__ nv, int rows, int row_bytes, long long chs_bytes, long long nhs_bytes,
@@ -194,5 +239,43 @@ extern "C" int std_len_add(int32_t* len_dev, int n, int delta, void* stream) {
   if (n < 1) return STD_E_SHAPE;
   hipLaunchKernelGGL(len_add_kernel, dim3((n + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), len_dev, n,
                      delta);
+  return launch_status();
+}
+
+extern "C" int std_argmax_rows(const void* logits, long long logits_row_stride, int rows, int vocab, int dtype,
+                               long long* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!logits || !out || !workspace) return STD_E_NULL;
+  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (rows < 1 || rows > 65535 || vocab < 1 || logits_row_stride < vocab) return STD_E_SHAPE;
+  if (workspace_bytes < std_greedy_accept_workspace_bytes(rows, vocab)) return STD_E_WORKSPACE;
+  const int nb = accept_blocks(vocab);
+  uint2* part = static_cast<uint2*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == STD_BF16)
+    hipLaunchKernelGGL(argmax_partial_kernel<bf16_t>, dim3(nb, rows), dim3(AM_THREADS), 0, st,
+                       static_cast<const bf16_t*>(logits), logits_row_stride, vocab, nb, part);
+  else
+    hipLaunchKernelGGL(argmax_partial_kernel<float>, dim3(nb, rows), dim3(AM_THREADS), 0, st,
+                       static_cast<const float*>(logits), logits_row_stride, vocab, nb, part);
+  int s = launch_status();
+  if (s) return s;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3((rows + 255) / 256), dim3(256), 0, st, part, nb, rows, out);
+  return launch_status();
+}
+
+extern "C" int std_rms_norm(const void* x, long long x_row_stride, const void* weight, void* out,
+                            long long out_row_stride, int rows, int hidden, float eps, int dtype, void* stream) {
+  if (!x || !weight || !out) return STD_E_NULL;
+  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (rows < 1 || hidden < 1 || x_row_stride < hidden || out_row_stride < hidden) return STD_E_SHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == STD_BF16)
+    hipLaunchKernelGGL(rms_norm_kernel<bf16_t>, dim3(rows), dim3(256), 0, st, static_cast<const bf16_t*>(x),
+                       static_cast<const bf16_t*>(weight), static_cast<bf16_t*>(out), hidden, x_row_stride,
+                       out_row_stride, eps);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel<float>, dim3(rows), dim3(256), 0, st, static_cast<const float*>(x),
+                       static_cast<const float*>(weight), static_cast<float*>(out), hidden, x_row_stride,
+                       out_row_stride, eps);
   return launch_status();
 }

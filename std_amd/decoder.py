@@ -113,9 +113,7 @@ class RandomDecoder:
 
     # -- pieces ---------------------------------------------------------------
     def _rms_norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.config.rms_norm_eps)
-        return weight * xf.to(x.dtype)
+        return ops.rms_norm(x, weight, self.config.rms_norm_eps)
 
     def _rope(self, position_ids: torch.Tensor):
         freqs = position_ids.to(torch.float32)[:, None] * self.inv_freq[None, :]

@@ -451,6 +451,41 @@ def attention_devlen(query: torch.Tensor, key_cache: torch.Tensor, value_cache: 
     return out
 
 
+def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
+    """int64 [rows] = argmax over the last dim of [rows, vocab] logits (first
+    maximum; NaN wins), graph-capture safe (torch.argmax over a large vocab
+    stages through a memset semaphore that captured graphs do not replay
+    correctly)."""
+    dev = _check_device(logits)
+    code = _dtype_code(logits)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [rows, vocab] with contiguous rows")
+    rows, vocab = logits.shape
+    out = torch.empty(rows, dtype=torch.long, device=dev)
+    ws_bytes = _lib.load_library().std_greedy_accept_workspace_bytes(rows, vocab)
+    ws_ptr, ws = _workspace(ws_bytes, dev)
+    _lib.call("std_argmax_rows", logits.data_ptr(), logits.stride(0), rows, vocab, code, out.data_ptr(), ws_ptr,
+              ws_bytes, _stream(dev))
+    return out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """Qwen2RMSNorm (modeling_qwen2_5_vl.py:192-197) over the last dim, one
+    HIP workgroup per row (graph-capture safe)."""
+    dev = _check_device(x, weight)
+    code = _dtype_code(x)
+    if weight.dtype != x.dtype or weight.dim() != 1 or weight.shape[0] != x.shape[-1] or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [hidden] tensor of the input dtype")
+    if x.stride(-1) != 1:
+        raise ValueError("x must be contiguous in the last dim")
+    hidden = x.shape[-1]
+    x2 = x.reshape(-1, hidden)
+    out = torch.empty(x2.shape, dtype=x.dtype, device=dev)
+    _lib.call("std_rms_norm", x2.data_ptr(), x2.stride(0), weight.data_ptr(), out.data_ptr(), out.stride(0),
+              x2.shape[0], hidden, float(eps), code, _stream(dev))
+    return out.view(x.shape)
+
+
 def len_add(length: torch.Tensor, delta: int) -> None:
     """length[:] += delta on the device."""
     dev = _check_device(length)

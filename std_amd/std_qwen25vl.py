@@ -147,7 +147,7 @@ def prefill_prompt(model, inputs: Dict[str, torch.Tensor], past_key_values, vide
         logits = model(text_ids, past_key_values)
     finally:
         model.capture_text_queries = False
-    next_token = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+    next_token = _token_argmax(logits)
     return input_ids, next_token, text_start
 
 
@@ -230,7 +230,8 @@ class SparseDraftController:
 
 
 def _token_argmax(logits: torch.Tensor) -> torch.Tensor:
-    return torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
+    """[1, 1] int64 next token of the last row (graph-capture safe argmax)."""
+    return ops.argmax_rows(logits[0, -1:, :]).view(1, 1)
 
 
 def _profile_mark(enabled: bool) -> float:

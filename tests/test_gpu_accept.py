@@ -109,3 +109,35 @@ def test_kv_append_past_capacity_is_skipped():
     ops.kv_append(ck, cv, nk, nk, length)
     torch.cuda.synchronize()
     assert torch.all(ck[:, :, 6:] == 1) and torch.all(ck[:, :, :6] == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_argmax_rows_matches_oracle_with_ties_and_nan(dtype):
+    announce(f"argmax_rows {dtype} 12 x 152064 with planted ties and a NaN")
+    g = torch.Generator().manual_seed(31)
+    logits = torch.randn(12, 152064, generator=g).to(dtype)
+    logits[3, 5000] = logits[3, 140000] = 50.0            # tie: the lower index wins
+    logits[7, 100] = float("nan")                           # NaN counts as the maximum
+    logits[9] = 0.0
+    logits[9, 77] = -0.0                                    # all equal: index 0
+    want = [int(p) for p in ref.verify_predictions(logits.float(), True)]
+    got = ops.argmax_rows(logits.to(dev()))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.long and got.cpu().tolist() == want
+    assert want[3] == 5000 and want[7] == 100 and want[9] == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rms_norm_matches_torch_formula(dtype):
+    announce(f"rms_norm {dtype} 33 x 3584")
+    g = torch.Generator().manual_seed(32)
+    x = (torch.randn(1, 33, 3584, generator=g) * 3).to(dtype)
+    w = (1 + 0.1 * torch.randn(3584, generator=g)).to(dtype)
+    got = ops.rms_norm(x.to(dev()), w.to(dev()), 1e-6).cpu()
+    xf = x.float()
+    want = w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype)   # modeling_qwen2_5_vl.py:192-197
+    if dtype == torch.bfloat16:                             # the fp32 sums differ in order only
+        diff = (got.float() - want.float()).abs()
+        assert (diff <= want.float().abs() * 2 ** -7).all() and (diff == 0).float().mean() > 0.99
+    else:
+        torch.testing.assert_close(got, want, rtol=2e-6, atol=1e-6)

@@ -77,3 +77,66 @@ def test_graph_replays_equal_eager_round():
         assert torch.equal(d, d0) and torch.equal(v, v0) and torch.equal(r, r0), f"replay {rep} differs"
         for k, t in state0.items():
             assert torch.equal(x[k], t), f"replay {rep}: {k} differs"
+
+
+def test_decoder_step_graph_replays_equal_eager_at_7b_shapes():
+    """A 2-layer decoder with the 7B layer and vocabulary shapes: captured AR
+    and verify steps (device lengths, HIP rope/append + attention, HIP RMSNorm
+    and argmax, torch GEMMs) replay bit-identically to the eager steps, three
+    times, with unrelated eager work between replays."""
+    from std_amd.decoder import DecoderConfig, RandomDecoder
+    from std_amd.kv_cache import initialize_past_key_values
+    from std_amd.std_qwen25vl import _token_argmax, _warm_and_capture
+
+    announce("decoder step graphs vs eager, 7B shapes, 2 layers")
+    cfg = DecoderConfig(num_hidden_layers=2)
+    model = RandomDecoder(cfg, dev(), torch.bfloat16, seed=3)
+    pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.bfloat16, 256)
+    gen = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, 150000, (1, 40), generator=gen).to(dev())
+    with torch.inference_mode():
+        first = _token_argmax(model(prompt, pkv))
+        L0 = 40
+        state = torch.tensor([L0, L0], dtype=torch.int32, device=dev())
+        tok = first.clone()
+        draft = torch.randint(0, 150000, (1, 9), generator=gen).to(dev())
+
+        def ar_step():
+            logits = model(tok, pkv, step_state=state)
+            tok.copy_(_token_argmax(logits))
+            return logits
+
+        def verify_step():
+            return model(torch.cat([tok, draft], 1), pkv, step_state=state, all_logits=True)
+
+        def run_eager():
+            state.copy_(torch.tensor([L0, L0], dtype=torch.int32))
+            tok.copy_(first)
+            outs = [ar_step().clone() for _ in range(3)]
+            outs.append(verify_step().clone())
+            torch.cuda.synchronize()
+            return outs
+
+        want = run_eager()
+        again = run_eager()
+        assert all(torch.equal(a, b) for a, b in zip(want, again)), "eager steps are not deterministic"
+
+        def restore():
+            state.copy_(torch.tensor([L0, L0], dtype=torch.int32))
+            tok.copy_(first)
+
+        (g_ar, out_ar), (g_v, out_v) = _warm_and_capture(lambda: (ar_step(), verify_step()), restore,
+                                                          [(ar_step, ()), (verify_step, ())])
+        for rep in range(3):
+            restore()
+            torch.randn(1 << 20, device=dev()).sum()          # unrelated eager work
+            torch.cuda.synchronize()
+            got = []
+            for _ in range(3):
+                g_ar.replay()
+                got.append(out_ar.clone())
+            g_v.replay()
+            got.append(out_v.clone())
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(got, want)):
+                assert torch.equal(a, b), f"replay {rep}, step {i} differs"
