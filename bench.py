@@ -43,6 +43,8 @@ def parse_args():
                     help="c2-c4: attention hot path at 16k/64k/128k context (default c4, the headline); "
                          "c5: end-to-end STD vs dense AR decode on a random-init Qwen2.5-VL-7B-shaped decoder")
     ap.add_argument("--new-tokens", type=int, default=128, help="c5: tokens to decode")
+    ap.add_argument("--eager", action="store_true",
+                    help="c5: run the decode loops eagerly (host lengths) instead of replaying captured HIP graphs")
     ap.add_argument("--layers", type=int, default=None, help="override the layer count (default: workload's)")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cold-iters", type=int, default=10)
@@ -376,20 +378,22 @@ def run_c5(args) -> None:
         vis = torch.randn(nv, cfg.hidden_size, generator=gen)
         return {"input_ids": ids.to(dev), "visual_embeds": vis.to(dev, torch.bfloat16)}
 
+    graphs = not args.eager
     warm = prompt(1024)
-    ar_generate_qwen25vl(model, warm, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=4, ignore_eos=True)
-    std_generate_qwen25vl(model, warm, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=12, gamma=gamma,
-                          target_k_plus_text=target, ignore_eos=True)
+    ar_generate_qwen25vl(model, warm, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=4, ignore_eos=True,
+                         use_graphs=graphs)
+    std_generate_qwen25vl(model, warm, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=24, gamma=gamma,
+                          target_k_plus_text=target, ignore_eos=True, use_graphs=graphs)
     log("c5: warm-up done")
     inputs = prompt(n_visual)
     t0 = time.perf_counter()
     ar = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=args.new_tokens,
-                              ignore_eos=True, profile_prefill=True)
+                              ignore_eos=True, profile_prefill=True, use_graphs=graphs)
     log(f"c5: AR done in {time.perf_counter() - t0:.1f} s (decode {ar.decoding_time:.3f} s)")
     t0 = time.perf_counter()
     std, sel = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id,
                                      max_new_tokens=args.new_tokens, gamma=gamma, target_k_plus_text=target,
-                                     ignore_eos=True, profile_decode=True, profile_prefill=True)
+                                     ignore_eos=True, profile_decode=True, profile_prefill=True, use_graphs=graphs)
     log(f"c5: STD done in {time.perf_counter() - t0:.1f} s (decode {std.decoding_time:.3f} s)")
     div = first_divergence(std.output_ids[0, -std.generate_len:], ar.output_ids[0, -ar.generate_len:])
     std_tps = std.generate_len / std.decoding_time
@@ -430,6 +434,8 @@ def run_c5(args) -> None:
         "k": sel.k,
         "compact_len": sel.compact_len,
         "first_divergence_vs_ar": div,
+        "decode_loop": "HIP graphs (device lengths; draft, verify+accept and bonus phases replayed per round)"
+                       if graphs else "eager (host lengths)",
         "note": "the prefill attention (not the decode path) runs as chunked fp32 torch matmuls",
     }
     print(json.dumps(result))
