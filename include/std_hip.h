@@ -297,6 +297,24 @@ int std_argmax_rows(const void* logits, long long logits_row_stride, int rows, i
 int std_rms_norm(const void* x, long long x_row_stride, const void* weight, void* out,
                  long long out_row_stride, int rows, int hidden, float eps, int dtype, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Weight-streaming projection for decode/verify rows (M <= 16), bf16:
+ * y[m][n] = sum_k x[m][k] * W[n][k] (+ bias[n]), fp32 accumulation.
+ *
+ * Replaces, at batch 1, the q/k/v, o, gate/up, down and lm_head projections
+ * of the draft, verify and AR steps (torch.nn.functional.linear in the
+ * decoder layers of modeling_qwen2_5_vl.py; the per-token GEMVs that A10 of
+ * the draft loop spends its time in). W [N][K] row-major (row stride
+ * w_row_stride), x [M][K], y [M][N]; K a multiple of 32. Workspace (fp32
+ * split-K partials, summed in split order: deterministic) sized by
+ * std_gemv_workspace_bytes; 0 means none is needed.
+ * ------------------------------------------------------------------------ */
+size_t std_gemv_workspace_bytes(int M, int N, int K);
+
+int std_gemv(const void* x, long long x_row_stride, const void* w, long long w_row_stride,
+             const void* bias, void* y, long long y_row_stride, int M, int N, int K, int dtype,
+             void* workspace, size_t workspace_bytes, void* stream);
+
 int std_greedy_accept(const void* logits, long long logits_row_stride, int q_rows, int vocab,
                       int dtype, const int32_t* draft, int n_draft, int has_pending,
                       const int32_t* dense_next, int32_t* out,

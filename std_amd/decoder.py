@@ -112,6 +112,14 @@ class RandomDecoder:
         self.captured_queries: List[Optional[torch.Tensor]] = [None] * c.num_hidden_layers
 
     # -- pieces ---------------------------------------------------------------
+    def _linear(self, x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Single-row bf16 projections (draft, AR and bonus steps) stream the
+        weights through the HIP GEMV; multi-row ones (verify, prefill) use
+        torch, which is as fast or faster there."""
+        if x.dtype == torch.bfloat16 and x.numel() == x.shape[-1]:
+            return ops.linear(x, weight, bias)
+        return F.linear(x, weight, bias)
+
     def _rms_norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         return ops.rms_norm(x, weight, self.config.rms_norm_eps)
 
@@ -173,7 +181,7 @@ class RandomDecoder:
         p = self.layers[li]
         n = h.shape[1]
         hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
-        qkv = F.linear(h, p["qkv_w"], p["qkv_b"])                            # [1, n, (hq + 2hkv) d]
+        qkv = self._linear(h, p["qkv_w"], p["qkv_b"])                        # [1, n, (hq + 2hkv) d]
         controller = self.sparse_controller
         if controller is not None and controller.enabled and n != 1:
             raise RuntimeError("Sparse draft attention currently expects autoregressive q_len=1 calls.")
@@ -185,7 +193,7 @@ class RandomDecoder:
             if host_lengths:
                 kc.advance(n)
                 vc.advance(n)
-            return F.linear(out.transpose(1, 2).reshape(1, n, hq * d), p["o_w"])
+            return self._linear(out.transpose(1, 2).reshape(1, n, hq * d), p["o_w"])
         q = qkv[..., :hq * d].view(1, n, hq, d).transpose(1, 2)
         k = qkv[..., hq * d:(hq + hkv) * d].view(1, n, hkv, d).transpose(1, 2)
         v = qkv[..., (hq + hkv) * d:].view(1, n, hkv, d).transpose(1, 2)
@@ -202,9 +210,9 @@ class RandomDecoder:
 
     def _mlp(self, li: int, h: torch.Tensor) -> torch.Tensor:
         p = self.layers[li]
-        gu = F.linear(h, p["gate_up_w"])
+        gu = self._linear(h, p["gate_up_w"])
         gate, up = gu.chunk(2, dim=-1)
-        return F.linear(F.silu(gate) * up, p["down_w"])
+        return self._linear((F.silu(gate) * up).contiguous(), p["down_w"])
 
     # -- forward ----------------------------------------------------------------
     @torch.inference_mode()
@@ -254,6 +262,6 @@ class RandomDecoder:
             ops.len_add(step_state, n)
         if not all_logits:
             x = x[:, -1:]
-        return F.linear(self._rms_norm(x, self.norm), self.lm_head)
+        return self._linear(self._rms_norm(x, self.norm), self.lm_head)
 
     __call__ = forward

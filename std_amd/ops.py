@@ -451,6 +451,29 @@ def attention_devlen(query: torch.Tensor, key_cache: torch.Tensor, value_cache: 
     return out
 
 
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """torch.nn.functional.linear for at most 16 bf16 rows: the HIP
+    weight-streaming projection (weight [N, K] read once, fp32 accumulation,
+    deterministic). x [..., K] with at most 16 rows in total."""
+    dev = _check_device(x, weight)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("linear: bf16 only")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M, (N, Kw) = x2.shape[0], weight.shape
+    if Kw != K or weight.stride(1) != 1 or x2.stride(1) != 1:
+        raise ValueError("linear: weight must be [N, K] and x [..., K], both contiguous in K")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (N,) or not bias.is_contiguous()):
+        raise ValueError("linear: bias must be a contiguous bf16 [N]")
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ws_bytes = _lib.load_library().std_gemv_workspace_bytes(M, N, K)
+    ws_ptr, ws = _workspace(ws_bytes, dev)
+    _lib.call("std_gemv", x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0),
+              bias.data_ptr() if bias is not None else None, y.data_ptr(), y.stride(0), M, N, K, _lib.STD_BF16,
+              ws_ptr, ws_bytes, _stream(dev))
+    return y.view(*x.shape[:-1], N)
+
+
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     """int64 [rows] = argmax over the last dim of [rows, vocab] logits (first
     maximum; NaN wins), graph-capture safe (torch.argmax over a large vocab
