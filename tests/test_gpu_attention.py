@@ -214,3 +214,25 @@ def test_decode_batched_matches_oracle(dtype, S, B):
     for b in range(B):
         assert_close(out[b], ref.gqa_sdpa(q[b], k[b], v[b]), dtype)
     assert torch.equal(one[0], single)
+
+
+def test_decode_repeats_and_alternates_on_one_workspace():
+    """40 decode launches alternating between two problems with different split
+    counts on the same persistent workspace: every launch reproduces its first
+    result bit for bit and matches the oracle (no state leaks between calls)."""
+    announce("decode, 40 alternating launches on one workspace")
+    g = torch.Generator().manual_seed(41)
+    cases = []
+    for S in (1034, 1800):
+        q = torch.randn(1, 28, 1, 128, generator=g).to(torch.bfloat16)
+        k = torch.randn(1, 4, S, 128, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, 4, S, 128, generator=g).to(torch.bfloat16)
+        cases.append((q.to(dev()), k.to(dev()), v.to(dev()), ref.gqa_sdpa(q, k, v)))
+    first = [ops.gqa_decode(q, k, v).clone() for q, k, v, _ in cases]
+    for it in range(40):
+        q, k, v, want = cases[it % 2]
+        got = ops.gqa_decode(q, k, v)
+        torch.cuda.synchronize()
+        assert torch.equal(got, first[it % 2]), f"launch {it} differs from the first launch"
+        if it < 2:
+            assert_close(got, want, torch.bfloat16)
