@@ -305,9 +305,10 @@ int std_rms_norm(const void* x, long long x_row_stride, const void* weight, void
  * of the draft, verify and AR steps (torch.nn.functional.linear in the
  * decoder layers of modeling_qwen2_5_vl.py; the per-token GEMVs that A10 of
  * the draft loop spends its time in). W [N][K] row-major (row stride
- * w_row_stride), x [M][K], y [M][N]; K a multiple of 32. Workspace (fp32
- * split-K partials, summed in split order: deterministic) sized by
- * std_gemv_workspace_bytes; 0 means none is needed.
+ * w_row_stride), x [M][K], y [M][N]; K a multiple of 32. One launch;
+ * deterministic (K is split over the waves of a workgroup and their partial
+ * sums are added in a fixed order). std_gemv_workspace_bytes returns 0 (no
+ * workspace is used; the arguments are kept for interface stability).
  * ------------------------------------------------------------------------ */
 size_t std_gemv_workspace_bytes(int M, int N, int K);
 
