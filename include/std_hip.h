@@ -316,6 +316,23 @@ int std_gemv(const void* x, long long x_row_stride, const void* w, long long w_r
              const void* bias, void* y, long long y_row_stride, int M, int N, int K, int dtype,
              void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same projection with the decoder's neighbouring elementwise ops in its
+ * epilogue (one launch instead of two or three at batch 1):
+ *   gated = 0: y = residual + (x W^T + bias)     (residual may be NULL)
+ *   gated = 1: W is [2N][K], the gate rows over the up rows (bias, if any,
+ *              [2N]); y[m][n] = silu(g) * u with g = (x W^T + b)[m][n] and
+ *              u = (x W^T + b)[m][N + n], each rounded to bf16.
+ * Every op is rounded to bf16 as torch evaluates it on bf16 tensors:
+ * Qwen2MLP's act_fn(gate_proj(x)) * up_proj(x) (modeling_qwen2_5_vl.py:686)
+ * and the decoder layer's "hidden_states = residual + hidden_states"
+ * (modeling_qwen2_5_vl.py:1215, 1221). residual [M][N] has row stride
+ * residual_row_stride; x [M][K]; y [M][N]. gated and residual together are
+ * allowed. No workspace.
+ */
+int std_gemv_ex(const void* x, long long x_row_stride, const void* w, long long w_row_stride,
+                const void* bias, const void* residual, long long residual_row_stride, void* y,
+                long long y_row_stride, int M, int N, int K, int gated, int dtype, void* stream);
+
 int std_greedy_accept(const void* logits, long long logits_row_stride, int q_rows, int vocab,
                       int dtype, const int32_t* draft, int n_draft, int has_pending,
                       const int32_t* dense_next, int32_t* out,

@@ -57,6 +57,8 @@ SIGNATURES = {
     "std_gemv_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "std_gemv": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_int, c_int,
                          c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "std_gemv_ex": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_void_p,
+                            c_longlong, c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "std_argmax_rows": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "std_rms_norm": (c_int, [c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_int, c_int, c_float, c_int,
                              c_void_p]),

@@ -12,7 +12,9 @@
 // Splitting K over the workgroup's waves (rather than over workgroups with a
 // second reduction launch) keeps one launch per projection and enough waves
 // per CU to keep the weight stream in flight; the waves' partial tiles are
-// added through LDS in wave order, so the result is deterministic.
+// added through LDS in wave order, so the result is deterministic. The
+// epilogue can also add the decoder's residual or apply the MLP's
+// silu(gate) * up, so those elementwise ops cost no launch of their own.
 #include "common.h"
 
 namespace stdhip {
@@ -29,62 +31,100 @@ __device__ __forceinline__ bf16x8_t ld16(const bf16_t* p) {
 
 // grid (ceil(N / 16)): a workgroup owns 16 output columns and its WK waves
 // split K into WK contiguous ranges (multiples of 32); the waves' 16 x M fp32
-// results are added in wave order through LDS by wave 0, which adds the bias
-// and writes bf16. One launch, deterministic, no workspace.
-template <int WK>
+// results are added in wave order through LDS by wave 0, which runs the
+// epilogue and writes bf16. One launch, deterministic, no workspace.
+//
+// GATED (the MLP's gate/up projection, W = [gate rows; up rows], N = the
+// intermediate size): the workgroup accumulates gate row n and up row N + n
+// side by side and writes act[m][n] = silu(g) * u with g, u the projections
+// rounded to bf16 -- torch.nn.functional.silu(gate) * up on the bf16 output
+// of the [2N, K] linear, each op rounded to bf16 -- so the activation needs
+// no launch of its own. residual (may be NULL): y = residual + round(x W^T +
+// bias), the decoder's residual add rounded as torch rounds it.
+__device__ __forceinline__ float round_bf16(float v) { return to_f32<bf16_t>(from_f32<bf16_t>(v)); }
+
+template <int WK, bool GATED>
 __global__ void __launch_bounds__(64 * WK)
 gemv_bf16_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
-                 const bf16_t* __restrict__ bias, bf16_t* __restrict__ y, long long y_rs, int M, int N, int K) {
-  __shared__ f32x4 red[WK][64];
+                 const bf16_t* __restrict__ bias, const bf16_t* __restrict__ residual, long long r_rs,
+                 bf16_t* __restrict__ y, long long y_rs, int M, int N, int K) {
+  constexpr int kMat = GATED ? 2 : 1;          // weight row sets streamed per step
+  constexpr int kU = kUnroll / kMat;           // k-steps of 32 per step (8 loads of 16 B per lane either way)
+  constexpr int kStep = 32 * kU;
+  __shared__ f32x4 red[kMat][WK][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;        // this wave's K range
   const int k_begin = min(K, wave * kw), k_end = min(K, k_begin + kw);
-  const bf16_t* wr = w + (long long)min(n0 + ln, N - 1) * w_rs + 8 * lg;
+  const bf16_t* wr[kMat];
+  wr[0] = w + (long long)min(n0 + ln, N - 1) * w_rs + 8 * lg;
+  if constexpr (GATED) wr[kMat - 1] = wr[0] + (long long)N * w_rs;
   const bool xm = ln < M;
   const bf16_t* xr = x + (long long)(xm ? ln : 0) * x_rs + 8 * lg;
   const bf16x8_t zero = {};
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[kMat];
+#pragma unroll
+  for (int j = 0; j < kMat; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   int k = k_begin;
   // Two steps of loads in flight: the next step's weights are requested
   // before the current step's MFMAs consume theirs.
-  bf16x8_t a[kUnroll], b[kUnroll];
-  auto load = [&](int kk, bf16x8_t* aa, bf16x8_t* bb) {
+  bf16x8_t a[kMat][kU], b[kU];
+  auto load = [&](int kk, bf16x8_t (*aa)[kU], bf16x8_t* bb) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      aa[u] = ld16(wr + kk + 32 * u);
+    for (int u = 0; u < kU; ++u) {
+#pragma unroll
+      for (int j = 0; j < kMat; ++j) aa[j][u] = ld16(wr[j] + kk + 32 * u);
       bb[u] = xm ? ld16(xr + kk + 32 * u) : zero;
     }
   };
-  if (k + kStepK <= k_end) load(k, a, b);
-  for (; k + kStepK <= k_end; k += kStepK) {
-    bf16x8_t an[kUnroll], bn[kUnroll];
-    const bool more = k + 2 * kStepK <= k_end;
-    if (more) load(k + kStepK, an, bn);
+  if (k + kStep <= k_end) load(k, a, b);
+  for (; k + kStep <= k_end; k += kStep) {
+    bf16x8_t an[kMat][kU], bn[kU];
+    const bool more = k + 2 * kStep <= k_end;
+    if (more) load(k + kStep, an, bn);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], b[u], acc, 0, 0, 0);
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int j = 0; j < kMat; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][u], b[u], acc[j], 0, 0, 0);
     if (more) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) { a[u] = an[u]; b[u] = bn[u]; }
+      for (int u = 0; u < kU; ++u) {
+#pragma unroll
+        for (int j = 0; j < kMat; ++j) a[j][u] = an[j][u];
+        b[u] = bn[u];
+      }
     }
   }
   for (; k < k_end; k += 32) {                 // K is a multiple of 32
-    const bf16x8_t av = ld16(wr + k), bv = xm ? ld16(xr + k) : zero;
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+    const bf16x8_t bv = xm ? ld16(xr + k) : zero;
+#pragma unroll
+    for (int j = 0; j < kMat; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ld16(wr[j] + k), bv, acc[j], 0, 0, 0);
   }
-  red[wave][lane] = acc;
+#pragma unroll
+  for (int j = 0; j < kMat; ++j) red[j][wave][lane] = acc[j];
   __syncthreads();
   if (wave != 0 || !xm) return;
-  f32x4 t = red[0][lane];
+  f32x4 t[kMat];
 #pragma unroll
-  for (int i = 1; i < WK; ++i) t += red[i][lane];
+  for (int j = 0; j < kMat; ++j) {
+    t[j] = red[j][0][lane];
+#pragma unroll
+    for (int i = 1; i < WK; ++i) t[j] += red[j][i][lane];
+  }
   const int n = n0 + 4 * lg;                   // this lane's 4 columns of row m = ln
   bf16_t* dst = y + (long long)ln * y_rs + n;
+  const bf16_t* res = residual ? residual + (long long)ln * r_rs + n : nullptr;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (n + i < N) {
-      const float v = bias ? t[i] + to_f32<bf16_t>(bias[n + i]) : t[i];
+      float v = round_bf16(bias ? t[0][i] + to_f32<bf16_t>(bias[n + i]) : t[0][i]);
+      if constexpr (GATED) {
+        const float u = round_bf16(bias ? t[kMat - 1][i] + to_f32<bf16_t>(bias[N + n + i]) : t[kMat - 1][i]);
+        const float s = round_bf16(__fdiv_rn(v, __fadd_rn(1.0f, expf(-v))));   // silu(g) in fp32, rounded
+        v = round_bf16(s * u);
+      }
+      if (res) v = __fadd_rn(to_f32<bf16_t>(res[i]), v);
       dst[i] = from_f32<bf16_t>(v);
     }
 }
@@ -101,26 +141,53 @@ extern "C" size_t std_gemv_workspace_bytes(int M, int N, int K) {
   return 0;
 }
 
+namespace stdhip {
+namespace {
+
+template <bool GATED>
+int launch_gemv(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias, const void* residual,
+                long long r_rs, void* y, long long y_rs, int M, int N, int K, hipStream_t st) {
+  const dim3 grid((N + 15) / 16);
+  // K per wave: about 512-2400 k (eight waves once K is large)
+  if (K > 4096)
+    hipLaunchKernelGGL((gemv_bf16_kernel<8, GATED>), grid, dim3(512), 0, st, static_cast<const bf16_t*>(w), w_rs,
+                       static_cast<const bf16_t*>(x), x_rs, static_cast<const bf16_t*>(bias),
+                       static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
+  else
+    hipLaunchKernelGGL((gemv_bf16_kernel<4, GATED>), grid, dim3(256), 0, st, static_cast<const bf16_t*>(w), w_rs,
+                       static_cast<const bf16_t*>(x), x_rs, static_cast<const bf16_t*>(bias),
+                       static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
+  return launch_status();
+}
+
+int gemv_entry(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias, const void* residual,
+               long long r_rs, void* y, long long y_rs, int M, int N, int K, int dtype, bool gated, void* stream) {
+  if (!x || !w || !y) return STD_E_NULL;
+  if (dtype != STD_BF16) return STD_E_DTYPE;
+  if (M < 1 || M > 16 || N < 1 || K < 32 || K % 32 != 0) return STD_E_SHAPE;
+  if (x_rs < K || w_rs < K || y_rs < N) return STD_E_SHAPE;
+  if (residual && r_rs < N) return STD_E_SHAPE;
+  if (!aligned16(x) || !aligned16(w) || (x_rs * 2) % 16 || (w_rs * 2) % 16) return STD_E_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return gated ? launch_gemv<true>(x, x_rs, w, w_rs, bias, residual, r_rs, y, y_rs, M, N, K, st)
+               : launch_gemv<false>(x, x_rs, w, w_rs, bias, residual, r_rs, y, y_rs, M, N, K, st);
+}
+
+}  // namespace
+}  // namespace stdhip
+
 extern "C" int std_gemv(const void* x, long long x_row_stride, const void* w, long long w_row_stride,
                         const void* bias, void* y, long long y_row_stride, int M, int N, int K, int dtype,
                         void* workspace, size_t workspace_bytes, void* stream) {
   (void)workspace;
   (void)workspace_bytes;
-  if (!x || !w || !y) return STD_E_NULL;
-  if (dtype != STD_BF16) return STD_E_DTYPE;
-  if (M < 1 || M > 16 || N < 1 || K < 32 || K % 32 != 0) return STD_E_SHAPE;
-  if (x_row_stride < K || w_row_stride < K || y_row_stride < N) return STD_E_SHAPE;
-  if (!aligned16(x) || !aligned16(w) || (x_row_stride * 2) % 16 || (w_row_stride * 2) % 16) return STD_E_ALIGN;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((N + 15) / 16);
-  // K per wave: about 512-2400 k (eight waves once K is large)
-  if (K > 4096)
-    hipLaunchKernelGGL(gemv_bf16_kernel<8>, grid, dim3(512), 0, st, static_cast<const bf16_t*>(w), w_row_stride,
-                       static_cast<const bf16_t*>(x), x_row_stride, static_cast<const bf16_t*>(bias),
-                       static_cast<bf16_t*>(y), y_row_stride, M, N, K);
-  else
-    hipLaunchKernelGGL(gemv_bf16_kernel<4>, grid, dim3(256), 0, st, static_cast<const bf16_t*>(w), w_row_stride,
-                       static_cast<const bf16_t*>(x), x_row_stride, static_cast<const bf16_t*>(bias),
-                       static_cast<bf16_t*>(y), y_row_stride, M, N, K);
-  return launch_status();
+  return gemv_entry(x, x_row_stride, w, w_row_stride, bias, nullptr, 0, y, y_row_stride, M, N, K, dtype, false,
+                    stream);
+}
+
+extern "C" int std_gemv_ex(const void* x, long long x_row_stride, const void* w, long long w_row_stride,
+                           const void* bias, const void* residual, long long residual_row_stride, void* y,
+                           long long y_row_stride, int M, int N, int K, int gated, int dtype, void* stream) {
+  return gemv_entry(x, x_row_stride, w, w_row_stride, bias, residual, residual_row_stride, y, y_row_stride, M, N, K,
+                    dtype, gated != 0, stream);
 }

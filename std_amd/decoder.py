@@ -112,13 +112,19 @@ class RandomDecoder:
         self.captured_queries: List[Optional[torch.Tensor]] = [None] * c.num_hidden_layers
 
     # -- pieces ---------------------------------------------------------------
-    def _linear(self, x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Single-row bf16 projections (draft, AR and bonus steps) stream the
-        weights through the HIP GEMV; multi-row ones (verify, prefill) use
+    def _single_row(self, x: torch.Tensor) -> bool:
+        return x.dtype == torch.bfloat16 and x.numel() == x.shape[-1]
+
+    def _linear(self, x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """linear(x) (+ residual). Single-row bf16 projections (draft, AR and
+        bonus steps) stream the weights through the HIP GEMV, with the
+        residual add in its epilogue; multi-row ones (verify, prefill) use
         torch, which is as fast or faster there."""
-        if x.dtype == torch.bfloat16 and x.numel() == x.shape[-1]:
-            return ops.linear(x, weight, bias)
-        return F.linear(x, weight, bias)
+        if self._single_row(x):
+            return ops.linear(x, weight, bias, residual=residual)
+        y = F.linear(x, weight, bias)
+        return y if residual is None else residual + y
 
     def _rms_norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         return ops.rms_norm(x, weight, self.config.rms_norm_eps)
@@ -176,7 +182,8 @@ class RandomDecoder:
         return n * (c.num_attention_heads // c.num_key_value_heads) <= MAX_FUSED_ROWS
 
     def _attention(self, li: int, h: torch.Tensor, cos, sin, kc: KVCache, vc: KVCache,
-                   state: Optional[torch.Tensor], host_lengths: bool) -> torch.Tensor:
+                   state: Optional[torch.Tensor], host_lengths: bool, residual: torch.Tensor) -> torch.Tensor:
+        """residual + self-attention block output (o_proj included)."""
         c = self.config
         p = self.layers[li]
         n = h.shape[1]
@@ -193,7 +200,7 @@ class RandomDecoder:
             if host_lengths:
                 kc.advance(n)
                 vc.advance(n)
-            return self._linear(out.transpose(1, 2).reshape(1, n, hq * d), p["o_w"])
+            return self._linear(out.transpose(1, 2).reshape(1, n, hq * d), p["o_w"], residual=residual)
         q = qkv[..., :hq * d].view(1, n, hq, d).transpose(1, 2)
         k = qkv[..., hq * d:(hq + hkv) * d].view(1, n, hkv, d).transpose(1, 2)
         v = qkv[..., (hq + hkv) * d:].view(1, n, hkv, d).transpose(1, 2)
@@ -206,13 +213,16 @@ class RandomDecoder:
             raise ValueError("a device-state step must have at most 96 query rows per KV head")
         out = self._prefill_attention(q, k, v, kc, vc)
         out = out.transpose(1, 2).reshape(1, n, hq * d)
-        return F.linear(out, p["o_w"])
+        return residual + F.linear(out, p["o_w"])
 
-    def _mlp(self, li: int, h: torch.Tensor) -> torch.Tensor:
+    def _mlp(self, li: int, h: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """residual + down(silu(gate(h)) * up(h)); a single bf16 row takes two
+        HIP launches (activation and residual add in the GEMV epilogues)."""
         p = self.layers[li]
-        gu = self._linear(h, p["gate_up_w"])
-        gate, up = gu.chunk(2, dim=-1)
-        return self._linear((F.silu(gate) * up).contiguous(), p["down_w"])
+        if self._single_row(h):
+            return ops.linear(ops.gated_linear(h, p["gate_up_w"]), p["down_w"], residual=residual)
+        gate, up = F.linear(h, p["gate_up_w"]).chunk(2, dim=-1)
+        return residual + F.linear(F.silu(gate) * up, p["down_w"])
 
     # -- forward ----------------------------------------------------------------
     @torch.inference_mode()
@@ -255,9 +265,9 @@ class RandomDecoder:
             cos, sin = self._rope(position_ids)
         for li in range(self.config.num_hidden_layers):
             kc, vc = past_key_values[li]
-            x = x + self._attention(li, self._rms_norm(x, self.layers[li]["ln1"]), cos, sin, kc, vc, step_state,
-                                    host_lengths)
-            x = x + self._mlp(li, self._rms_norm(x, self.layers[li]["ln2"]))
+            x = self._attention(li, self._rms_norm(x, self.layers[li]["ln1"]), cos, sin, kc, vc, step_state,
+                                host_lengths, residual=x)
+            x = self._mlp(li, self._rms_norm(x, self.layers[li]["ln2"]), residual=x)
         if not host_lengths:
             ops.len_add(step_state, n)
         if not all_logits:

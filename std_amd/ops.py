@@ -451,27 +451,53 @@ def attention_devlen(query: torch.Tensor, key_cache: torch.Tensor, value_cache: 
     return out
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """torch.nn.functional.linear for at most 16 bf16 rows: the HIP
-    weight-streaming projection (weight [N, K] read once, fp32 accumulation,
-    deterministic). x [..., K] with at most 16 rows in total."""
+def _gemv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], residual: Optional[torch.Tensor],
+          gated: bool, name: str) -> torch.Tensor:
     dev = _check_device(x, weight)
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
-        raise TypeError("linear: bf16 only")
+        raise TypeError(f"{name}: bf16 only")
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
-    M, (N, Kw) = x2.shape[0], weight.shape
+    M, (NW, Kw) = x2.shape[0], weight.shape
     if Kw != K or weight.stride(1) != 1 or x2.stride(1) != 1:
-        raise ValueError("linear: weight must be [N, K] and x [..., K], both contiguous in K")
-    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (N,) or not bias.is_contiguous()):
-        raise ValueError("linear: bias must be a contiguous bf16 [N]")
+        raise ValueError(f"{name}: weight must be [N, K] and x [..., K], both contiguous in K")
+    if gated and NW % 2:
+        raise ValueError(f"{name}: weight must stack the gate and up rows, [2 * N, K]")
+    N = NW // 2 if gated else NW
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (NW,) or not bias.is_contiguous()):
+        raise ValueError(f"{name}: bias must be a contiguous bf16 [{NW}]")
+    r2 = None
+    if residual is not None:
+        _check_device(residual)
+        if residual.dtype != torch.bfloat16 or residual.shape != (*x.shape[:-1], N):
+            raise ValueError(f"{name}: residual must be bf16 shaped [..., {N}] like the output")
+        r2 = residual.reshape(-1, N)
+        if r2.stride(1) != 1:
+            raise ValueError(f"{name}: residual rows must be contiguous")
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    ws_bytes = _lib.load_library().std_gemv_workspace_bytes(M, N, K)
-    ws_ptr, ws = _workspace(ws_bytes, dev)
-    _lib.call("std_gemv", x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0),
-              bias.data_ptr() if bias is not None else None, y.data_ptr(), y.stride(0), M, N, K, _lib.STD_BF16,
-              ws_ptr, ws_bytes, _stream(dev))
+    _lib.call("std_gemv_ex", x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0),
+              bias.data_ptr() if bias is not None else None, r2.data_ptr() if r2 is not None else None,
+              r2.stride(0) if r2 is not None else 0, y.data_ptr(), y.stride(0), M, N, K, int(gated), _lib.STD_BF16,
+              _stream(dev))
     return y.view(*x.shape[:-1], N)
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+           residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """torch.nn.functional.linear for at most 16 bf16 rows: the HIP
+    weight-streaming projection (weight [N, K] read once, fp32 accumulation,
+    deterministic). x [..., K] with at most 16 rows in total. With residual
+    ([..., N] bf16) it returns residual + linear(x, weight, bias), the
+    decoder's residual add, rounded as torch rounds the two ops."""
+    return _gemv(x, weight, bias, residual, False, "linear")
+
+
+def gated_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(gate) * up of gate, up = linear(x, weight, bias).chunk(2, -1) for
+    at most 16 bf16 rows (the MLP's fused gate/up projection and activation,
+    each op rounded to bf16 as torch rounds it): weight [2 I, K] stacks the
+    gate rows over the up rows; returns [..., I]."""
+    return _gemv(x, weight, bias, None, True, "gated_linear")
 
 
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:

@@ -112,6 +112,17 @@ def test_select_validation():
                                NULL) == -5
 
 
+def test_gemv_validation():
+    lib = _lib.load_library()
+    # K must be a multiple of 32; at most 16 rows; bf16 only; 16-byte aligned rows
+    assert lib.std_gemv_ex(16, 100, 16, 100, NULL, NULL, 0, 16, 64, 1, 64, 100, 0, 1, NULL) == -3
+    assert lib.std_gemv_ex(16, 128, 16, 128, NULL, NULL, 0, 16, 64, 17, 64, 128, 0, 1, NULL) == -3
+    assert lib.std_gemv_ex(16, 128, 16, 128, NULL, NULL, 0, 16, 64, 1, 64, 128, 0, 0, NULL) == -2
+    assert lib.std_gemv_ex(16, 128, 16, 128, NULL, 16, 10, 16, 64, 1, 64, 128, 0, 1, NULL) == -3  # residual stride
+    assert lib.std_gemv_ex(16, 132, 16, 128, NULL, NULL, 0, 16, 64, 2, 64, 128, 1, 1, NULL) == -5  # x row stride
+    assert lib.std_gemv(NULL, 128, 16, 128, NULL, 16, 64, 1, 64, 128, 1, NULL, 0, NULL) == -1
+
+
 def test_accept_and_append_validation():
     lib = _lib.load_library()
     # q_rows must be n_draft + has_pending

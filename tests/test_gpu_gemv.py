@@ -36,3 +36,68 @@ def test_gemv_keeps_leading_dims_and_strided_rows():
     got = ops.linear(x, w)
     assert got.shape == (1, 10, 640)
     torch.testing.assert_close(got.float(), F.linear(x.float(), w.float()), rtol=1e-2, atol=2e-3)
+
+
+def _bf16_ulp(t: torch.Tensor) -> torch.Tensor:
+    """One bf16 unit in the last place of each element (of its magnitude)."""
+    a = t.float().abs().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+
+@pytest.mark.parametrize("M,I,K,bias", [(1, 18944, 3584, False), (10, 18944, 3584, False), (3, 100, 96, True),
+                                         (16, 48, 4128, True)])
+def test_gated_linear_equals_torch_activation_of_the_projection(M, I, K, bias):
+    """The gate/up epilogue (silu(g) * u with g, u rounded to bf16) against
+    torch's own bf16 F.silu(gate) * up of the same projection: the sums are
+    the non-gated kernel's, bit for bit, so any difference comes from the
+    silu evaluation alone and is held to one bf16 ulp on a tiny fraction."""
+    announce(f"gated_linear M={M} I={I} K={K} bias={bias}")
+    g = torch.Generator(device=dev()).manual_seed(M + I + K)
+    x = torch.randn(M, K, generator=g, device=dev()).to(torch.bfloat16)
+    w = (torch.randn(2 * I, K, generator=g, device=dev()) * 0.03).to(torch.bfloat16)
+    b = (torch.randn(2 * I, generator=g, device=dev()) * 0.5).to(torch.bfloat16) if bias else None
+    got = ops.gated_linear(x, w, b)
+    gate, up = ops.linear(x, w, b).chunk(2, dim=-1)
+    want = F.silu(gate) * up
+    torch.cuda.synchronize()
+    assert got.shape == (M, I)
+    diff = (got.float() - want.float()).abs()
+    assert (diff <= _bf16_ulp(want)).all()
+    assert (diff == 0).float().mean() >= 0.999
+    ref = F.silu(F.linear(x.float(), w[:I].float(), b[:I].float() if bias else None)) * \
+        F.linear(x.float(), w[I:].float(), b[I:].float() if bias else None)
+    torch.testing.assert_close(got.float(), ref, rtol=2e-2, atol=2e-3)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 3584, 3584), (1, 3584, 18944), (10, 3584, 18944), (5, 72, 160)])
+def test_linear_residual_epilogue_equals_torch_add(M, N, K):
+    announce(f"linear + residual M={M} N={N} K={K}")
+    g = torch.Generator(device=dev()).manual_seed(3 * M + N + K)
+    x = torch.randn(1, M, K, generator=g, device=dev()).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev()) * 0.02).to(torch.bfloat16)
+    r = (torch.randn(1, M, N, generator=g, device=dev()) * 4).to(torch.bfloat16)
+    got = ops.linear(x, w, residual=r)
+    want = r + ops.linear(x, w)
+    torch.cuda.synchronize()
+    assert got.shape == (1, M, N)
+    assert torch.equal(got, want)
+
+
+def test_gated_linear_with_residual_and_validation():
+    announce("std_gemv_ex gated + residual; host-side shape checks")
+    M, I, K = 4, 160, 256
+    g = torch.Generator(device=dev()).manual_seed(5)
+    x = torch.randn(M, K, generator=g, device=dev()).to(torch.bfloat16)
+    w = (torch.randn(2 * I, K, generator=g, device=dev()) * 0.05).to(torch.bfloat16)
+    r = torch.randn(M, I, generator=g, device=dev()).to(torch.bfloat16)
+    y = torch.empty(M, I, dtype=torch.bfloat16, device=dev())
+    from std_amd import _lib
+    _lib.call("std_gemv_ex", x.data_ptr(), K, w.data_ptr(), K, None, r.data_ptr(), I, y.data_ptr(), I, M, I, K, 1,
+              _lib.STD_BF16, torch.cuda.current_stream().cuda_stream)
+    want = r + ops.gated_linear(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(y, want)
+    with pytest.raises(ValueError):
+        ops.gated_linear(x, w[:-1])                      # odd row count: not a gate/up stack
+    with pytest.raises(ValueError):
+        ops.linear(x, w, residual=r)                     # residual shaped like a different output
