@@ -254,34 +254,66 @@ def main():
         for l in range(L):
             ops.gqa_decode(q_draft[l], sparse_k[l][:, :, :S0], sparse_v[l][:, :, :S0], out=draft_out[l])
 
+    dense_decode_out = torch.empty_like(draft_out)
+
+    def dense_decode_only():
+        # the same decode kernel over the full dense cache (a dense AR step's attention)
+        for l in range(L):
+            ops.gqa_decode(q_draft[l], dense_k[l][:, :, :P], dense_v[l][:, :, :P], out=dense_decode_out[l])
+
     def draft_all_layers():
         # the all-layer roofline unit of one draft step: the L layers' decodes as one batched launch
         ops.gqa_decode_batched(q_draft, sparse_k[:, :, :, :S0], sparse_v[:, :, :, :S0], out=draft_out)
 
-    def time_graph(graph, iters, flush=None):
+    def repeated(fn, n):
+        """n back-to-back copies of a phase in one graph: the per-copy time
+        excludes the latency of launching the graph itself."""
+        def body():
+            for _ in range(n):
+                fn()
+        return body
+
+    def time_graph(graph, iters, per_replay, warm=2):
+        """Median per-copy time over iters replays, after warm replays (the
+        first replays of a new graph run slower)."""
         stream = torch.cuda.current_stream()
+        for _ in range(warm):
+            graph.replay()
+        torch.cuda.synchronize()
         times = []
         for _ in range(iters):
-            if flush is not None:
-                flush.fill_(1)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
             graph.replay()
             e1.record(stream)
             torch.cuda.synchronize()
-            times.append(e0.elapsed_time(e1) * 1e3)
+            times.append(e0.elapsed_time(e1) * 1e3 / per_replay)
         return statistics.median(times)
 
-    verify_graph, _ = capture(verify_only)
-    draft_graph, _ = capture(draft_only)
-    draft_all_graph, _ = capture(draft_all_layers)
-    verify_call_us = time_graph(verify_graph, 10) / L
-    draft_call_us = time_graph(draft_graph, 50) / L
-    draft_all_warm_us = time_graph(draft_all_graph, 50)
+    rep = 10
+    verify_graph, _ = capture(repeated(verify_only, 2))
+    draft_graph, _ = capture(repeated(draft_only, rep))
+    draft_all_graph, _ = capture(repeated(draft_all_layers, rep))
+    verify_call_us = time_graph(verify_graph, 10, 2 * L)
+    draft_call_us = time_graph(draft_graph, 20, rep * L)
+    draft_all_warm_us = time_graph(draft_all_graph, 20, rep)
+    dense_decode_graph, _ = capture(dense_decode_only)
+    dense_decode_us = time_graph(dense_decode_graph, 5, L)
+    del dense_decode_graph
+    # Cold: each copy follows a 1 GiB write that evicts the caches; the time of
+    # the writes alone (same graph shape) is subtracted.
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    draft_step_cold_us = time_graph(draft_graph, args.cold_iters, flush)      # 1 GiB written before each
-    draft_all_cold_us = time_graph(draft_all_graph, args.cold_iters, flush)
-    del flush
+
+    def write_flush():
+        flush.fill_(1)
+
+    flush_graph, _ = capture(repeated(write_flush, rep))
+    step_cold_graph, _ = capture(repeated(lambda: (write_flush(), draft_only()), rep))
+    all_cold_graph, _ = capture(repeated(lambda: (write_flush(), draft_all_layers()), rep))
+    flush_us = time_graph(flush_graph, args.cold_iters, rep)
+    draft_step_cold_us = time_graph(step_cold_graph, args.cold_iters, rep) - flush_us
+    draft_all_cold_us = time_graph(all_cold_graph, args.cold_iters, rep) - flush_us
+    del flush, flush_graph, step_cold_graph, all_cold_graph
     d_bytes = draft_bytes(Hq, Hkv, S0, D, es)
     v_bytes = verify_bytes(Hq, Hkv, Q, P + Q, D, es)
     verify_gbps = v_bytes / (verify_call_us * 1e-6) / 1e9
@@ -325,6 +357,10 @@ def main():
         "draft_one_launch_hbm_gbps_cold": round(L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9, 1),
         "draft_one_launch_pct_peak_cold": round(100 * L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
                                                 2),
+        "dense_decode_us_per_layer": round(dense_decode_us, 3),
+        "dense_decode_hbm_gbps": round(draft_bytes(Hq, Hkv, P, D, es) / (dense_decode_us * 1e-6) / 1e9, 1),
+        "dense_decode_pct_peak": round(100 * draft_bytes(Hq, Hkv, P, D, es) / (dense_decode_us * 1e-6) / 1e9
+                                       / HBM_PEAK_GBPS, 2),
         "verify_attn_us_per_step": round(verify_call_us * L, 2),
         "verify_attn_us_per_layer": round(verify_call_us, 3),
         "verify_hbm_gbps": round(verify_gbps, 1),

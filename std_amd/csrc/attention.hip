@@ -349,7 +349,9 @@ __device__ __forceinline__ float xor32_sum(float x) {
 // its key range a wave holds complete row statistics and output rows and
 // writes them straight from registers (no cross-wave merge, no LDS epilogue).
 // Waves w >= NT only help issue the DMA ring. Decode (NT == 1) runs four
-// waves, verify eight.
+// waves, verify eight. KS (key split, NT == 1 only) instead lets all four
+// waves compute, each on its own 16 keys of every tile, and merges them at
+// the end; it pays once a workgroup streams several tiles.
 template <int NT>
 struct Bf16Cfg {
   static constexpr int kWaves = NT == 1 ? 4 : 8;
@@ -358,7 +360,7 @@ struct Bf16Cfg {
   static constexpr int kLoadsPerTile = 2 * kSegsPerWave;
 };
 
-template <int NT>
+template <int NT, bool KS>
 __global__ void __launch_bounds__(NT == 1 ? 256 : 512)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
                  bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
@@ -371,7 +373,11 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   const int g = blockIdx.y, split = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool computes = w < NT;                 // wave-uniform
+  // Key split: every wave computes, on its own 16 keys of each tile;
+  // otherwise waves w < NT compute (one 16-row tile each) and the rest only
+  // help issue the DMA ring.
+  static_assert(!KS || NT == 1, "the key split serves one row tile");
+  const bool computes = KS || w < NT;           // wave-uniform
   const int ln = lane & 15, lg = lane >> 4;
   const int R = group * q_len;
   {
@@ -429,7 +435,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
 
   // This wave's query row is the lane's column ln of the S^T tiles; padding
   // rows (and the helper waves) carry zero queries and are never written.
-  const int row = w * 16 + ln;
+  const int row = KS ? ln : w * 16 + ln;
   const bool row_ok = computes && row < R;
   const int lim = row_ok ? causal_off + (row % q_len) : INT_MAX;
   // Q^T operand, 32-wide chunk c: lane (ln, lg) holds q[row][32c + 8lg, +8).
@@ -447,6 +453,10 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   // them) here: the compiler counts only its own loads, and a wait for them
   // placed inside the loop would drain the ring there.
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  // The key split runs QK^T and PV of a tile in the same step, so only one
+  // stage is held by compute and three tiles stay in flight; the first of
+  // them is issued here.
+  if (KS && ntiles > 2) issue(2, stage(2));
 
   // Running statistics in the log2 domain (scores pre-multiplied by
   // scale*log2(e)): m_run is the row's running max; the row sum is
@@ -563,9 +573,107 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   // Tile u lives in ring stage u % NSTAGE. The loop is unrolled by two only
   // for the score ping-pong; stage addresses are computed at run time, which
   // keeps the loop body small (it is fetched cold by every CU).
-  for (int u = 0; u <= ntiles; u += 2) {
-    step(u, stage(u), stage(u + 3), stage(u + 2), sA, sB);
-    step(u + 1, stage(u + 1), stage(u), stage(u + 3), sB, sA);
+  if constexpr (KS) {
+    // Key split: wave w scores keys 16w..16w+15 of every tile (one S^T sub-tile,
+    // lane (ln, lg) element i = key 16w + 4lg + i of row ln) and accumulates
+    // P V over them with 16x16x16 MFMAs, whose contraction slots 4lg..4lg+3
+    // are exactly the lane's own four keys (P^T operand) and, through one
+    // transposed LDS read per 16 output columns, the same keys of V (V^T
+    // operand). Each wave keeps its own running max, row sum and output rows;
+    // they are merged across the four waves after the loop.
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const s16x4 ones4 = {0x3f80, 0x3f80, 0x3f80, 0x3f80};
+    auto decode_tile = [&](int tt, const char* st) {
+      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + sw_off(16 * w + ln, 4 * c + lg));
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], sc, 0, 0, 0);
+      }
+      const char* Vs = st + TILEB;
+      const int rv = 16 * w + 4 * lg + (ln >> 2);
+      s16x4 vf[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int chunk = 2 * t + ((ln >> 1) & 1), half = (ln & 1) << 3;
+        vf[t] = __builtin_bit_cast(s16x4,
+                                   __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Vs + sw_off(rv, chunk) + half)));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[i] *= scale_log2;
+      const int key0 = key_begin + tt * TK + 16 * w + 4 * lg;
+      if (key_begin + tt * TK + TK > key_end || key_begin + tt * TK + TK - 1 > causal_off) {   // wave-uniform
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[i] = (key0 + i < key_end && key0 + i <= lim) ? sc[i] : -INFINITY;
+      }
+      const float lm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      if (__ballot(lm > m_run + kRescaleSlack)) {
+        const float mt = xor32_max(xor16_max(lm));
+        const float m_new = mt > m_run + kRescaleSlack ? mt : m_run;
+        const float alpha = fast_exp2(m_run - m_new);
+        lsum *= alpha;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] *= alpha;
+        m_run = m_new;
+      }
+      const s16x4 pb = __builtin_bit_cast(s16x4, pack_bf16x4(fast_exp2(sc[0] - m_run), fast_exp2(sc[1] - m_run),
+                                                             fast_exp2(sc[2] - m_run), fast_exp2(sc[3] - m_run)));
+      lsum = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ones4, pb, lsum, 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[t], pb, acc[t], 0, 0, 0);
+    };
+    // Step u: tiles u+1 and u+2 may still be in flight when tile u is
+    // complete; after the barrier (every wave is done with tile u-1) tile u+3
+    // goes into tile u-1's stage, then tile u is scored and accumulated.
+    for (int u = 0; u < ntiles; ++u) {
+      wait_vm_ahead<C::kLoadsPerTile>(min(2, ntiles - 1 - u));
+      wg_barrier();
+      if (u + 3 < ntiles) issue(u + 3, stage(u + 3));
+      decode_tile(u, stage(u));
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();                             // the ring is free: reuse it for the merge
+    // Merge the four waves' (m, l, O) rows: every wave stores its own, then
+    // each output element is the sum over the waves, in wave order, of O
+    // rescaled from the wave's max to the common one.
+    float2* mlw = reinterpret_cast<float2*>(ring);                  // [4][16]
+    float* Ow = reinterpret_cast<float*>(ring + 1024);               // [4][16][OROW]
+    if (lg == 0) mlw[w * 16 + ln] = make_float2(m_run, lsum[0]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) *reinterpret_cast<f32x4*>(Ow + (w * 16 + ln) * OROW + 16 * t + 4 * lg) = acc[t];
+    __syncthreads();
+    for (int item = tid; item < 16 * (D / 4); item += C::kThreads) {
+      const int r = item / (D / 4), d4 = item % (D / 4);
+      if (r >= R) break;                         // items are row-major: the rest are padding rows
+      float2 ml[4];
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) ml[ww] = mlw[ww * 16 + r];
+      const float Mr = fmaxf(fmaxf(ml[0].x, ml[1].x), fmaxf(ml[2].x, ml[3].x));
+      float Lr = 0.f;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) {
+        const float e = fast_exp2(ml[ww].x - Mr);
+        Lr += ml[ww].y * e;
+        o += *reinterpret_cast<const f32x4*>(Ow + (ww * 16 + r) * OROW + 4 * d4) * e;
+      }
+      const int hl = r / q_len, i = r - hl * q_len;
+      if (n_split == 1) {
+        bf16_t* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
+        const f32x4 on = o / Lr;
+        *reinterpret_cast<i16x4*>(dst) = pack_bf16x4(on[0], on[1], on[2], on[3]);
+      } else {
+        const long long prow = (long long)g * n_split * R + (long long)split * R + r;
+        *reinterpret_cast<f32x4*>(ws_o + prow * D + 4 * d4) = o;
+        if (d4 == 0) ws_ml[prow] = make_float2(Mr, Lr);
+      }
+    }
+    return;
+  } else {
+    for (int u = 0; u <= ntiles; u += 2) {
+      step(u, stage(u), stage(u + 3), stage(u + 2), sA, sB);
+      step(u + 1, stage(u + 1), stage(u), stage(u + 3), sB, sA);
+    }
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   if (!row_ok) return;
@@ -843,7 +951,10 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   const float scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(p.n_split, n_kv, n_batch);
   if (dtype == STD_BF16) {
-    hipLaunchKernelGGL((attn_bf16_kernel<NT>), grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
+    // One row tile and at least two tiles per split on average: key split.
+    const bool ks = NT == 1 && p.ntiles >= 2 * p.n_split;
+    auto kern = ks ? attn_bf16_kernel<NT, NT == 1> : attn_bf16_kernel<NT, false>;
+    hipLaunchKernelGGL(kern, grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
                        static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                        static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
                        p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
