@@ -373,11 +373,18 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   const int g = blockIdx.y, split = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // Key split: every wave computes, on its own 16 keys of each tile;
-  // otherwise waves w < NT compute (one 16-row tile each) and the rest only
-  // help issue the DMA ring.
+  // Wave roles. Key split (KS, one row tile): every wave computes, on its own
+  // 16 keys of each tile. Otherwise waves w < NT own one 16-row tile each
+  // (row owners) and the rest only help issue the DMA ring -- except with
+  // five row tiles (HYB, the 70-row verify), where waves 0-3 own row tiles
+  // 0-3 and waves 4-7, one per SIMD, share row tile 4 by keys as in the key
+  // split, so that no SIMD carries two row tiles.
   static_assert(!KS || NT == 1, "the key split serves one row tile");
-  const bool computes = KS || w < NT;           // wave-uniform
+  constexpr bool HYB = NT == 5 && !KS;
+  constexpr int kOwners = HYB ? 4 : NT;
+  const bool computes = !KS && w < kOwners;     // row owner (wave-uniform)
+  const bool ksw = KS || (HYB && w >= 4);       // key-split wave (wave-uniform)
+  const int ks_sub = KS ? w : w - 4;            // its 16 keys of each tile: 16 ks_sub ...
   const int ln = lane & 15, lg = lane >> 4;
   const int R = group * q_len;
   {
@@ -435,8 +442,8 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
 
   // This wave's query row is the lane's column ln of the S^T tiles; padding
   // rows (and the helper waves) carry zero queries and are never written.
-  const int row = KS ? ln : w * 16 + ln;
-  const bool row_ok = computes && row < R;
+  const int row = KS ? ln : ksw ? 16 * kOwners + ln : w * 16 + ln;
+  const bool row_ok = (computes || ksw) && row < R;
   const int lim = row_ok ? causal_off + (row % q_len) : INT_MAX;
   // Q^T operand, 32-wide chunk c: lane (ln, lg) holds q[row][32c + 8lg, +8).
   bf16x8 qf[4];
@@ -553,6 +560,106 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       for (int p = 0; p < 2; ++p) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[p][t], pb[p], acc[t], 0, 0, 0);
   };
 
+  // Key-split tile (KS waves, and the HYB waves on the last row tile): wave
+  // sub-tile ks_sub scores keys 16 ks_sub .. 16 ks_sub + 15 of the tile (one
+  // S^T sub-tile, lane (ln, lg) element i = key 16 ks_sub + 4lg + i of row
+  // ln) and accumulates P V over them with 16x16x16 MFMAs, whose contraction
+  // slots 4lg..4lg+3 are exactly the lane's own four keys (P^T operand) and,
+  // through one transposed LDS read per 16 output columns, the same keys of V
+  // (V^T operand). Each such wave keeps its own running max, row sum and
+  // output rows; ks_merge combines the four.
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 ones4 = {0x3f80, 0x3f80, 0x3f80, 0x3f80};
+  auto ks_tile = [&](int tt, const char* st) {
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + sw_off(16 * ks_sub + ln, 4 * c + lg));
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], sc, 0, 0, 0);
+    }
+    const char* Vs = st + TILEB;
+    const int rv = 16 * ks_sub + 4 * lg + (ln >> 2);
+    s16x4 vf[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int chunk = 2 * t + ((ln >> 1) & 1), half = (ln & 1) << 3;
+      vf[t] = __builtin_bit_cast(s16x4,
+                                 __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Vs + sw_off(rv, chunk) + half)));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] *= scale_log2;
+    const int key0 = key_begin + tt * TK + 16 * ks_sub + 4 * lg;
+    if (key_begin + tt * TK + TK > key_end || key_begin + tt * TK + TK - 1 > causal_off) {   // wave-uniform
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[i] = (key0 + i < key_end && key0 + i <= lim) ? sc[i] : -INFINITY;
+    }
+    const float lm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    if (__ballot(lm > m_run + kRescaleSlack)) {
+      const float mt = xor32_max(xor16_max(lm));
+      const float m_new = mt > m_run + kRescaleSlack ? mt : m_run;
+      const float alpha = fast_exp2(m_run - m_new);
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] *= alpha;
+      m_run = m_new;
+    }
+    const s16x4 pb = __builtin_bit_cast(s16x4, pack_bf16x4(fast_exp2(sc[0] - m_run), fast_exp2(sc[1] - m_run),
+                                                           fast_exp2(sc[2] - m_run), fast_exp2(sc[3] - m_run)));
+    lsum = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ones4, pb, lsum, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[t], pb, acc[t], 0, 0, 0);
+  };
+  // Merge of the four key-split waves' (m, l, O) rows r0 + 0..15: each
+  // stores its own into LDS (mlw, Ow at ring offset 0 and 1 KiB; the caller
+  // guarantees that nobody reads those bytes any more), one barrier, then
+  // nthr threads (thread index t) form each output element as the sum over
+  // the waves, in wave order, of O rescaled from the wave's max to the common
+  // one, and write the normalised row (one split) or the (m, l, O) partial.
+  static_assert(1024 + 4 * 16 * OROW * 4 <= 2 * STAGEB, "key-split merge region exceeds two ring stages");
+  auto ks_store = [&](char* region) {
+    float2* mlw = reinterpret_cast<float2*>(region);
+    float* Ow = reinterpret_cast<float*>(region + 1024);
+    if (lg == 0) mlw[ks_sub * 16 + ln] = make_float2(m_run, lsum[0]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      *reinterpret_cast<f32x4*>(Ow + (ks_sub * 16 + ln) * OROW + 16 * t + 4 * lg) = acc[t];
+  };
+  auto ks_merge_rows = [&](const char* region, int r0, int nthr, int t0) {
+    const float2* mlw = reinterpret_cast<const float2*>(region);
+    const float* Ow = reinterpret_cast<const float*>(region + 1024);
+    for (int item = t0; item < 16 * (D / 4); item += nthr) {
+      const int rl = item / (D / 4), d4 = item % (D / 4), r = r0 + rl;
+      if (r >= R) break;                         // items are row-major: the rest are padding rows
+      float2 ml[4];
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) ml[ww] = mlw[ww * 16 + rl];
+      const float Mr = fmaxf(fmaxf(ml[0].x, ml[1].x), fmaxf(ml[2].x, ml[3].x));
+      float Lr = 0.f;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) {
+        const float e = fast_exp2(ml[ww].x - Mr);
+        Lr += ml[ww].y * e;
+        o += *reinterpret_cast<const f32x4*>(Ow + (ww * 16 + rl) * OROW + 4 * d4) * e;
+      }
+      const int hl = r / q_len, i = r - hl * q_len;
+      if (n_split == 1) {
+        bf16_t* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
+        const f32x4 on = o / Lr;
+        *reinterpret_cast<i16x4*>(dst) = pack_bf16x4(on[0], on[1], on[2], on[3]);
+      } else {
+        const long long prow = (long long)g * n_split * R + (long long)split * R + r;
+        *reinterpret_cast<f32x4*>(ws_o + prow * D + 4 * d4) = o;
+        if (d4 == 0) ws_ml[prow] = make_float2(Mr, Lr);
+      }
+    }
+  };
+  auto ks_merge = [&](char* region, int r0, int nthr, int t0) {
+    ks_store(region);
+    __syncthreads();
+    ks_merge_rows(region, r0, nthr, t0);
+  };
+
   // Software pipeline, one step per tile u (steps 0..ntiles): after the
   // barrier, tile u+2 is prefetched into the stage tile u-2 used (every wave
   // finished tile u-2's PV before this barrier), the QK^T MFMAs of tile u are
@@ -569,105 +676,24 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       if (u < ntiles) qk(cur, s_new);
       if (u > 0) softmax_pv(u - 1, prev, s_old);
     }
+    if (HYB && ksw && u < ntiles) ks_tile(u, cur);
   };
   // Tile u lives in ring stage u % NSTAGE. The loop is unrolled by two only
   // for the score ping-pong; stage addresses are computed at run time, which
   // keeps the loop body small (it is fetched cold by every CU).
   if constexpr (KS) {
-    // Key split: wave w scores keys 16w..16w+15 of every tile (one S^T sub-tile,
-    // lane (ln, lg) element i = key 16w + 4lg + i of row ln) and accumulates
-    // P V over them with 16x16x16 MFMAs, whose contraction slots 4lg..4lg+3
-    // are exactly the lane's own four keys (P^T operand) and, through one
-    // transposed LDS read per 16 output columns, the same keys of V (V^T
-    // operand). Each wave keeps its own running max, row sum and output rows;
-    // they are merged across the four waves after the loop.
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
-    const s16x4 ones4 = {0x3f80, 0x3f80, 0x3f80, 0x3f80};
-    auto decode_tile = [&](int tt, const char* st) {
-      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + sw_off(16 * w + ln, 4 * c + lg));
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], sc, 0, 0, 0);
-      }
-      const char* Vs = st + TILEB;
-      const int rv = 16 * w + 4 * lg + (ln >> 2);
-      s16x4 vf[8];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int chunk = 2 * t + ((ln >> 1) & 1), half = (ln & 1) << 3;
-        vf[t] = __builtin_bit_cast(s16x4,
-                                   __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Vs + sw_off(rv, chunk) + half)));
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] *= scale_log2;
-      const int key0 = key_begin + tt * TK + 16 * w + 4 * lg;
-      if (key_begin + tt * TK + TK > key_end || key_begin + tt * TK + TK - 1 > causal_off) {   // wave-uniform
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = (key0 + i < key_end && key0 + i <= lim) ? sc[i] : -INFINITY;
-      }
-      const float lm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      if (__ballot(lm > m_run + kRescaleSlack)) {
-        const float mt = xor32_max(xor16_max(lm));
-        const float m_new = mt > m_run + kRescaleSlack ? mt : m_run;
-        const float alpha = fast_exp2(m_run - m_new);
-        lsum *= alpha;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) acc[t] *= alpha;
-        m_run = m_new;
-      }
-      const s16x4 pb = __builtin_bit_cast(s16x4, pack_bf16x4(fast_exp2(sc[0] - m_run), fast_exp2(sc[1] - m_run),
-                                                             fast_exp2(sc[2] - m_run), fast_exp2(sc[3] - m_run)));
-      lsum = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ones4, pb, lsum, 0, 0, 0);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[t], pb, acc[t], 0, 0, 0);
-    };
-    // Step u: tiles u+1 and u+2 may still be in flight when tile u is
+    // Key split: QK^T and PV of tile u in step u; tiles u+1 and u+2 may still be in flight when tile u is
     // complete; after the barrier (every wave is done with tile u-1) tile u+3
     // goes into tile u-1's stage, then tile u is scored and accumulated.
     for (int u = 0; u < ntiles; ++u) {
       wait_vm_ahead<C::kLoadsPerTile>(min(2, ntiles - 1 - u));
       wg_barrier();
       if (u + 3 < ntiles) issue(u + 3, stage(u + 3));
-      decode_tile(u, stage(u));
+      ks_tile(u, stage(u));
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();                             // the ring is free: reuse it for the merge
-    // Merge the four waves' (m, l, O) rows: every wave stores its own, then
-    // each output element is the sum over the waves, in wave order, of O
-    // rescaled from the wave's max to the common one.
-    float2* mlw = reinterpret_cast<float2*>(ring);                  // [4][16]
-    float* Ow = reinterpret_cast<float*>(ring + 1024);               // [4][16][OROW]
-    if (lg == 0) mlw[w * 16 + ln] = make_float2(m_run, lsum[0]);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) *reinterpret_cast<f32x4*>(Ow + (w * 16 + ln) * OROW + 16 * t + 4 * lg) = acc[t];
-    __syncthreads();
-    for (int item = tid; item < 16 * (D / 4); item += C::kThreads) {
-      const int r = item / (D / 4), d4 = item % (D / 4);
-      if (r >= R) break;                         // items are row-major: the rest are padding rows
-      float2 ml[4];
-#pragma unroll
-      for (int ww = 0; ww < 4; ++ww) ml[ww] = mlw[ww * 16 + r];
-      const float Mr = fmaxf(fmaxf(ml[0].x, ml[1].x), fmaxf(ml[2].x, ml[3].x));
-      float Lr = 0.f;
-      f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ww = 0; ww < 4; ++ww) {
-        const float e = fast_exp2(ml[ww].x - Mr);
-        Lr += ml[ww].y * e;
-        o += *reinterpret_cast<const f32x4*>(Ow + (ww * 16 + r) * OROW + 4 * d4) * e;
-      }
-      const int hl = r / q_len, i = r - hl * q_len;
-      if (n_split == 1) {
-        bf16_t* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
-        const f32x4 on = o / Lr;
-        *reinterpret_cast<i16x4*>(dst) = pack_bf16x4(on[0], on[1], on[2], on[3]);
-      } else {
-        const long long prow = (long long)g * n_split * R + (long long)split * R + r;
-        *reinterpret_cast<f32x4*>(ws_o + prow * D + 4 * d4) = o;
-        if (d4 == 0) ws_ml[prow] = make_float2(Mr, Lr);
-      }
-    }
+    ks_merge(ring, 0, C::kThreads, tid);
     return;
   } else {
     for (int u = 0; u <= ntiles; u += 2) {
@@ -676,6 +702,19 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     }
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  if constexpr (HYB) {
+    // The row owners may still read the last tile's stage (their final PV);
+    // the key-split waves merge through two other stages, then write the last
+    // row tile while the owners write theirs.
+    const int sl = (ntiles - 1) & (NSTAGE - 1);
+    char* region = ring + (sl <= 1 ? (sl + 1) * STAGEB : 0);
+    if (ksw) ks_store(region);
+    __syncthreads();
+    if (ksw) {
+      ks_merge_rows(region, 16 * kOwners, C::kThreads - 64 * kOwners, tid - 64 * kOwners);
+      return;
+    }
+  }
   if (!row_ok) return;
 
   // Complete rows: normalised output (one split) or the (m, l, O) partial.
