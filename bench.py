@@ -45,6 +45,8 @@ def parse_args():
     ap.add_argument("--new-tokens", type=int, default=128, help="c5: tokens to decode")
     ap.add_argument("--eager", action="store_true",
                     help="c5: run the decode loops eagerly (host lengths) instead of replaying captured HIP graphs")
+    ap.add_argument("--sparse-kv", default="compact", choices=["compact", "indexed"],
+                    help="c5: draft reads the selected prompt rows from a compacted copy or through index lists")
     ap.add_argument("--layers", type=int, default=None, help="override the layer count (default: workload's)")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cold-iters", type=int, default=10)
@@ -166,12 +168,15 @@ def main():
     torch.cuda.synchronize()
     select_ms_first = (time.perf_counter() - t0) * 1e3
     t0 = time.perf_counter()
+    indices = []
     for l in range(L):
         topk = ops.select_topk(q_text[l], dense_k[l, :, :, :P], P - T, vis, w.k)
         idx = ops.build_compact_index(nonvis, topk)
         ops.compact_kv(dense_k[l], dense_v[l], sparse_k[l], sparse_v[l], idx)
+        indices.append(idx)
     torch.cuda.synchronize()
     select_ms = (time.perf_counter() - t0) * 1e3
+    indices = [ops.pad_index(i) for i in indices]     # index-addressed draft: the same key lists
 
     S0 = w.compact_len
     lengths0 = torch.tensor([P, S0], dtype=torch.int32, device=dev)     # [dense_len, sparse_len]
@@ -255,6 +260,13 @@ def main():
             ops.gqa_decode(q_draft[l], sparse_k[l][:, :, :S0], sparse_v[l][:, :, :S0], out=draft_out[l])
 
     dense_decode_out = torch.empty_like(draft_out)
+    draft_indexed_out = torch.empty_like(draft_out)
+
+    def draft_indexed_only():
+        # the draft decode reading its prompt keys through the index lists (no compaction copy)
+        for l in range(L):
+            ops.gqa_decode_indexed(q_draft[l], dense_k[l], dense_v[l], indices[l], S0, sparse_k[l], sparse_v[l],
+                                   kv_len=S0, out=draft_indexed_out[l])
 
     def dense_decode_only():
         # the same decode kernel over the full dense cache (a dense AR step's attention)
@@ -297,6 +309,14 @@ def main():
     verify_call_us = time_graph(verify_graph, 10, 2 * L)
     draft_call_us = time_graph(draft_graph, 20, rep * L)
     draft_all_warm_us = time_graph(draft_all_graph, 20, rep)
+    draft_only()
+    draft_indexed_only()
+    torch.cuda.synchronize()
+    indexed_equal = bool(torch.equal(draft_indexed_out, draft_out))
+    assert indexed_equal, "index-addressed draft differs from the compacted draft"
+    draft_indexed_graph, _ = capture(repeated(draft_indexed_only, rep))
+    draft_indexed_us = time_graph(draft_indexed_graph, 20, rep * L)
+    del draft_indexed_graph
     dense_decode_graph, _ = capture(dense_decode_only)
     dense_decode_us = time_graph(dense_decode_graph, 5, L)
     del dense_decode_graph
@@ -357,6 +377,8 @@ def main():
         "draft_one_launch_hbm_gbps_cold": round(L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9, 1),
         "draft_one_launch_pct_peak_cold": round(100 * L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
                                                 2),
+        "draft_indexed_us_per_layer": round(draft_indexed_us, 3),
+        "draft_indexed_equals_compacted": indexed_equal,
         "dense_decode_us_per_layer": round(dense_decode_us, 3),
         "dense_decode_hbm_gbps": round(draft_bytes(Hq, Hkv, P, D, es) / (dense_decode_us * 1e-6) / 1e9, 1),
         "dense_decode_pct_peak": round(100 * draft_bytes(Hq, Hkv, P, D, es) / (dense_decode_us * 1e-6) / 1e9
@@ -419,7 +441,7 @@ def run_c5(args) -> None:
     ar_generate_qwen25vl(model, warm, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=4, ignore_eos=True,
                          use_graphs=graphs)
     std_generate_qwen25vl(model, warm, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=24, gamma=gamma,
-                          target_k_plus_text=target, ignore_eos=True, use_graphs=graphs)
+                          target_k_plus_text=target, ignore_eos=True, use_graphs=graphs, sparse_kv=args.sparse_kv)
     log("c5: warm-up done")
     inputs = prompt(n_visual)
     t0 = time.perf_counter()
@@ -429,7 +451,8 @@ def run_c5(args) -> None:
     t0 = time.perf_counter()
     std, sel = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id,
                                      max_new_tokens=args.new_tokens, gamma=gamma, target_k_plus_text=target,
-                                     ignore_eos=True, profile_decode=True, profile_prefill=True, use_graphs=graphs)
+                                     ignore_eos=True, profile_decode=True, profile_prefill=True, use_graphs=graphs,
+                                     sparse_kv=args.sparse_kv)
     log(f"c5: STD done in {time.perf_counter() - t0:.1f} s (decode {std.decoding_time:.3f} s)")
     div = first_divergence(std.output_ids[0, -std.generate_len:], ar.output_ids[0, -ar.generate_len:])
     std_tps = std.generate_len / std.decoding_time
@@ -472,6 +495,7 @@ def run_c5(args) -> None:
         "first_divergence_vs_ar": div,
         "decode_loop": "HIP graphs (device lengths; draft, verify+accept and bonus phases replayed per round)"
                        if graphs else "eager (host lengths)",
+        "sparse_kv": args.sparse_kv,
         "note": "the prefill attention (not the decode path) runs as chunked fp32 torch matmuls",
     }
     print(json.dumps(result))

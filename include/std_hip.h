@@ -256,6 +256,35 @@ int std_attn_devlen(const void* q, const void* k_cache, const void* v_cache, voi
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Sparse draft decode with index-addressed prompt keys (no compaction copy).
+ *
+ * Replaces compact_sparse_prompt_cache (std_qwen25vl.py:265-298: the gather of
+ * each head's sorted non-visual + top-k prompt rows into the sparse cache)
+ * together with the draft's fused_gqa_attention call on that cache
+ * (triton_attention.py:83-112 via std_qwen25vl.py:399-431): key j < n_index
+ * of KV head g is row index[g * index_head_stride + j] of the dense cache
+ * (dense_k / dense_v, dense_rows rows per head; an index outside
+ * [0, dense_rows) is clamped); keys n_index <= j < the key count are rows j
+ * of k_cache / v_cache (the sparse cache: the draft's own appended rows; its
+ * first n_index rows are never read). A selection refresh then rewrites
+ * n_index integers per head instead of copying rows.
+ *
+ * len_dev == NULL: kv_len keys. Otherwise the key count is *len_dev + 1 (this
+ * step's row last, as std_attn_devlen with q_len = 1) and kv_len is the
+ * maximum the launch is planned for. Single query row per head, bf16. index:
+ * int32, 16-byte aligned, index_head_stride >= n_index rounded up to 16 (the
+ * row is read 16 entries at a time). Workspace:
+ * std_gqa_decode_workspace_bytes(n_q, n_kv, kv_len, d).
+ * ------------------------------------------------------------------------ */
+int std_gqa_decode_indexed(const void* q, const void* dense_k, const void* dense_v, int dense_rows,
+                           long long dense_k_head_stride, long long dense_v_head_stride,
+                           const int32_t* index, long long index_head_stride, int n_index,
+                           const void* k_cache, const void* v_cache, long long k_head_stride,
+                           long long v_head_stride, void* out, int n_q, int n_kv, int kv_len,
+                           const int32_t* len_dev, int d, float scale, int dtype, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Greedy acceptance plus cache rollback on the device.
  *
  * Replaces the verify tail of std_generate_qwen25vl

@@ -54,6 +54,10 @@ SIGNATURES = {
     "std_kv_append": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_longlong,
                               c_longlong, c_longlong, c_int, c_void_p, c_int, c_void_p]),
     "std_len_add": (c_int, [c_void_p, c_int, c_int, c_void_p]),
+    "std_gqa_decode_indexed": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_longlong, c_longlong, c_void_p,
+                                       c_longlong, c_int, c_void_p, c_void_p, c_longlong, c_longlong, c_void_p,
+                                       c_int, c_int, c_int, c_void_p, c_int, c_float, c_int, c_void_p, c_size_t,
+                                       c_void_p]),
     "std_gemv_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "std_gemv": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_int, c_int,
                          c_int, c_int, c_void_p, c_size_t, c_void_p]),

@@ -98,7 +98,7 @@ accept_final_kernel(const uint2* __restrict__ part, int n_blocks, int q_rows, co
 // block order and writes the index as int64 (the token-id type of torch).
 __global__ void __launch_bounds__(256)
 argmax_final_kernel(const uint2* __restrict__ part, int n_blocks, int rows, long long* __restrict__ out) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = blockIdx.x * 256 + threadIdx.x;
   if (r >= rows) return;
   uint32_t bk = 0;
   int bi = INT_MAX;
@@ -145,7 +145,7 @@ kv_append_kernel(char* __restrict__ ck, char* __restrict__ cv, const char* __res
                  long long nrs_bytes, int capacity, const int32_t* __restrict__ len_dev) {
   const int g = blockIdx.y, kv = blockIdx.z;
   const int cpr = row_bytes / 16;
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = blockIdx.x * 256 + threadIdx.x;
   const int s = c / cpr, col = c - s * cpr;
   if (s >= rows) return;
   const int pos = *len_dev + s;
@@ -155,8 +155,8 @@ kv_append_kernel(char* __restrict__ ck, char* __restrict__ cv, const char* __res
   *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
 }
 
-__global__ void len_add_kernel(int32_t* len, int n, int delta) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void __launch_bounds__(256) len_add_kernel(int32_t* len, int n, int delta) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n) len[i] += delta;
 }
 

@@ -70,6 +70,22 @@ SplitPlan plan_splits(int n_kv, int rows, int kv_len, int dtype) {
 // (blockIdx.z); all zero for a single problem.
 struct BatchStrides {
   long long q, k, v, o;
+  long long w;          // partial rows per problem in the split workspace (set at launch)
+};
+
+// Index-addressed keys (decode, bf16): key j < n_idx of KV head g is row
+// idx[g * idx_hs + j] of the dense cache (k, v with head strides k_hs, v_hs
+// and dense_rows rows per head; an index outside [0, dense_rows) is clamped),
+// keys j >= n_idx are rows j of the launch's own cache, as without indices.
+// idx == nullptr: no gather.
+struct GatherArgs {
+  const int32_t* idx;
+  long long idx_hs;
+  int n_idx;
+  int dense_rows;
+  const bf16_t* k;
+  const bf16_t* v;
+  long long k_hs, v_hs;
 };
 
 struct WsLayout {
@@ -163,7 +179,7 @@ constexpr int kMergePrefetch = 8;
 template <typename T>
 __global__ void __launch_bounds__(kMergeThreads)
 attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
-                  int n_split, int q_len, int group, long long out_bs) {
+                  int n_split, int q_len, int group, long long out_bs, int n_kv) {
   __shared__ float wts[kMaxSplit];
   __shared__ float red[2][kMergeThreads / 64];
   __shared__ f32x4 part[kMergeGroups][D / 4];
@@ -171,7 +187,7 @@ attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_
   const int d4 = tid & (D / 4 - 1), sg = tid / (D / 4);
   const int R = group * q_len;
   out += blockIdx.z * out_bs;
-  const long long base = ((long long)blockIdx.z * gridDim.y + g) * n_split * R + r;
+  const long long base = ((long long)blockIdx.z * n_kv + g) * n_split * R + r;
   const f32x4* col = reinterpret_cast<const f32x4*>(ws_o + base * D) + d4;
   const long long step = (long long)R * (D / 4);
   f32x4 pre[kMergePrefetch];
@@ -294,6 +310,12 @@ __device__ __forceinline__ void lds_dma16_sbase(const void* sbase, uint32_t voff
                : "memory", "m0");
 }
 
+// The same copy from a per-lane 64-bit address (gathered rows).
+__device__ __forceinline__ void lds_dma16_vaddr(const void* addr, uint32_t lds_base) {
+  const uint32_t lds = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lds_base));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(addr), "s"(lds) : "memory", "m0");
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   typedef const __attribute__((address_space(3))) char* lds_cptr;
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr)(p)));
@@ -360,13 +382,14 @@ struct Bf16Cfg {
   static constexpr int kLoadsPerTile = 2 * kSegsPerWave;
 };
 
-template <int NT, bool KS>
+template <int NT, bool KS, bool GA>
 __global__ void __launch_bounds__(NT == 1 ? 256 : 512)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
                  bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                  int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
-                 long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev) {
+                 long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev,
+                 GatherArgs ga, const int32_t* __restrict__ gidx) {
   using C = Bf16Cfg<NT>;
   __shared__ __align__(16) char ring[NSTAGE * STAGEB];
 
@@ -394,8 +417,8 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     vc += b * bs.v;
     out += b * bs.o;
     if (n_split > 1) {
-      ws_o += b * gridDim.y * n_split * R * D;
-      ws_ml += b * gridDim.y * n_split * R;
+      ws_o += b * bs.w * D;
+      ws_ml += b * bs.w;
     }
   }
   if (len_dev != nullptr) device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
@@ -424,6 +447,71 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   auto issue = [&](int tt, char* stage) {
     const int key0 = key_begin + tt * TK;
     const int last = key_end - 1 - key0;               // wave-uniform
+    if constexpr (GA) {
+      static_assert(NT == 1, "gathered keys serve the single-row decode");
+      if (key0 < ga.n_idx) {                             // wave-uniform: a tile with gathered keys
+        // This wave's DMA rows are 4 kSegsPerWave consecutive rows from wrow0;
+        // their indices come through scalar loads (gidx is read-only and not
+        // aliased, so the compiler can use them; they are counted apart from
+        // the ring's vector-memory count), then each lane copies from its row's
+        // own address: gathered dense row or own-cache row.
+        constexpr int kRows = 4 * C::kSegsPerWave;
+        const int wrow0 = w * kRows;
+        int sidx[kRows];
+        if (key0 + wrow0 < ga.n_idx) {
+          const int4* ip = reinterpret_cast<const int4*>(gidx + g * ga.idx_hs + key0 + wrow0);
+#pragma unroll
+          for (int i = 0; i < kRows / 4; ++i) {
+            const int4 v4 = ip[i];
+            sidx[4 * i] = v4.x;
+            sidx[4 * i + 1] = v4.y;
+            sidx[4 * i + 2] = v4.z;
+            sidx[4 * i + 3] = v4.w;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < kRows; ++i) sidx[i] = 0;
+        }
+        const char* gkh = reinterpret_cast<const char*>(ga.k + g * ga.k_hs);
+        const char* gvh = reinterpret_cast<const char*>(ga.v + g * ga.v_hs);
+        // Rows past the split's last key re-read that key from where it really
+        // lives (a gathered dense row or an own-cache row), as the compacted
+        // cache would: own-cache rows below n_idx are never written.
+        const int klast = key0 + last;
+        const char *lk, *lv;
+        if (klast < ga.n_idx) {
+          const int il = min(max(gidx[g * ga.idx_hs + klast], 0), ga.dense_rows - 1);
+          lk = gkh + (long long)il * ROWB;
+          lv = gvh + (long long)il * ROWB;
+        } else {
+          lk = reinterpret_cast<const char*>(kh + (long long)klast * D);
+          lv = reinterpret_cast<const char*>(vh + (long long)klast * D);
+        }
+        const int sel = lane >> 4;
+#pragma unroll
+        for (int j = 0; j < C::kSegsPerWave; ++j) {
+          const int r = dma_row[j];
+          const int key = key0 + r;
+          int ix = sel == 0 ? sidx[4 * j] : sel == 1 ? sidx[4 * j + 1] : sel == 2 ? sidx[4 * j + 2] : sidx[4 * j + 3];
+          ix = min(max(ix, 0), ga.dense_rows - 1);
+          const char *ka, *va;
+          if (r > last) {
+            ka = lk;
+            va = lv;
+          } else if (key < ga.n_idx) {
+            ka = gkh + (long long)ix * ROWB;
+            va = gvh + (long long)ix * ROWB;
+          } else {
+            ka = reinterpret_cast<const char*>(kh + (long long)key * D);
+            va = reinterpret_cast<const char*>(vh + (long long)key * D);
+          }
+          const uint32_t dst = lds_addr(stage) + (w * C::kSegsPerWave + j) * 1024;
+          lds_dma16_vaddr(ka + dma_chunk[j], dst);
+          lds_dma16_vaddr(va + dma_chunk[j], dst + TILEB);
+        }
+        return;
+      }
+    }
     const bf16_t* kt = kh + (long long)key0 * D;
     const bf16_t* vt = vh + (long long)key0 * D;
 #pragma unroll
@@ -811,8 +899,8 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
     vc += b * bs.v;
     out += b * bs.o;
     if (n_split > 1) {
-      ws_o += b * gridDim.y * n_split * R * D;
-      ws_ml += b * gridDim.y * n_split * R;
+      ws_o += b * bs.w * D;
+      ws_ml += b * bs.w;
     }
   }
   if (len_dev != nullptr) device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
@@ -980,7 +1068,7 @@ template <int NT>
 int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
               long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
               long long n_hs, long long n_rs, int n_new, int n_batch, BatchStrides bs, const int32_t* len_dev,
-              hipStream_t st) {
+              GatherArgs ga, hipStream_t st) {
   const int R = group * q_len;
   const SplitPlan p = plan_splits(n_kv * n_batch, R, kv_len, dtype);
   const WsLayout wl = ws_layout(n_kv * n_batch, R, p);
@@ -989,15 +1077,21 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
   const float scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(p.n_split, n_kv, n_batch);
+  bs.w = (long long)n_kv * p.n_split * R;
   if (dtype == STD_BF16) {
     // One row tile and at least two tiles per split on average: key split.
     const bool ks = NT == 1 && p.ntiles >= 2 * p.n_split;
-    auto kern = ks ? attn_bf16_kernel<NT, NT == 1> : attn_bf16_kernel<NT, false>;
+    // Gathered keys (decode only): a separate instantiation, so the plain
+    // kernels carry none of the gather code or arguments.
+    auto kern = NT == 1 && ga.idx != nullptr ? (ks ? attn_bf16_kernel<NT, NT == 1, NT == 1>
+                                                   : attn_bf16_kernel<NT, false, NT == 1>)
+                                             : (ks ? attn_bf16_kernel<NT, NT == 1, false>
+                                                   : attn_bf16_kernel<NT, false, false>);
     hipLaunchKernelGGL(kern, grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
                        static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                        static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
                        p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
-                       static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev);
+                       static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev, ga, ga.idx);
   } else {
     hipLaunchKernelGGL((attn_f32_kernel<NT>), grid, dim3(NTHREADS), 0, st, static_cast<const float*>(q),
                        static_cast<float*>(k), static_cast<float*>(v), static_cast<float*>(out), ws_o, ws_ml, q_len,
@@ -1008,20 +1102,20 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   if (s != 0 || p.n_split == 1) return s;
   if (dtype == STD_BF16)
     hipLaunchKernelGGL((attn_merge_kernel<bf16_t>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st, ws_o,
-                       ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len, group, bs.o);
+                       ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len, group, bs.o, n_kv);
   else
     hipLaunchKernelGGL((attn_merge_kernel<float>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st, ws_o,
-                       ws_ml, static_cast<float*>(out), p.n_split, q_len, group, bs.o);
+                       ws_ml, static_cast<float*>(out), p.n_split, q_len, group, bs.o, n_kv);
   return launch_status();
 }
 
 int launch_attn(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
                 long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
                 long long n_hs, long long n_rs, int n_new, int n_batch, BatchStrides bs, const int32_t* len_dev,
-                hipStream_t st) {
+                GatherArgs ga, hipStream_t st) {
 #define STD_LAUNCH_NT(N)                                                                                       \
   launch_nt<N>(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs, n_new, \
-               n_batch, bs, len_dev, st)
+               n_batch, bs, len_dev, ga, st)
   switch ((group * q_len + 15) / 16) {
     case 1: return STD_LAUNCH_NT(1);
     case 2: return STD_LAUNCH_NT(2);
@@ -1041,8 +1135,23 @@ size_t attn_workspace_bytes(int n_kv, int rows, int kv_len, int dtype) {
 int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, int q_len, int kv_len, int d,
                long long k_hs, long long v_hs, float scale, int dtype, void* ws, size_t ws_bytes, const void* nk,
                const void* nv, long long n_hs, long long n_rs, int n_new, void* stream, int n_batch = 1,
-               BatchStrides bs = BatchStrides{0, 0, 0, 0}, const int32_t* len_dev = nullptr) {
+               BatchStrides bs = BatchStrides{0, 0, 0, 0}, const int32_t* len_dev = nullptr,
+               GatherArgs ga = GatherArgs{nullptr, 0, 0, 0, nullptr, nullptr, 0, 0}) {
   if (!q || !k || !v || !out) return STD_E_NULL;
+  if (ga.idx != nullptr) {
+    // Gathered keys: one bf16 decode problem; indices padded to 16 per row of
+    // the index array and 16-byte aligned (they are read four at a time).
+    if (!ga.k || !ga.v) return STD_E_NULL;
+    if (dtype != STD_BF16) return STD_E_DTYPE;
+    if (q_len != 1 || n_batch != 1 || n_new > 0) return STD_E_SHAPE;
+    if (ga.n_idx < 0 || ga.n_idx > kv_len || ga.dense_rows < 1) return STD_E_SHAPE;
+    if (ga.idx_hs < (long long)round_up((size_t)ga.n_idx, 16)) return STD_E_SHAPE;
+    if (n_kv > 1 && (ga.k_hs < (long long)ga.dense_rows * D || ga.v_hs < (long long)ga.dense_rows * D))
+      return STD_E_SHAPE;
+    if (!aligned16(ga.idx) || ga.idx_hs % 4 != 0 || !aligned16(ga.k) || !aligned16(ga.v) ||
+        (ga.k_hs * 2) % 16 != 0 || (ga.v_hs * 2) % 16 != 0)
+      return STD_E_ALIGN;
+  }
   if (n_batch < 1 || n_batch > 65535) return STD_E_SHAPE;
   if (n_batch == 1) {
     bs = BatchStrides{0, 0, 0, 0};
@@ -1068,7 +1177,7 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
   if (need > 0 && (ws == nullptr || ws_bytes < need)) return STD_E_WORKSPACE;
   if (need > 0 && !aligned16(ws)) return STD_E_ALIGN;
   return launch_attn(q, k, v, out, n_kv, q_len, kv_len, group, k_hs, v_hs, scale, dtype, ws, nk, nv, n_hs, n_rs,
-                     n_new, n_batch, bs, len_dev, static_cast<hipStream_t>(stream));
+                     n_new, n_batch, bs, len_dev, ga, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -1147,4 +1256,19 @@ extern "C" int std_attn_devlen(const void* q, const void* k_cache, const void* v
   return attn_entry(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), out, n_q, n_kv, q_len, max_kv_len, d,
                     k_head_stride, v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0, 0,
                     stream, 1, BatchStrides{0, 0, 0, 0}, len_dev);
+}
+
+extern "C" int std_gqa_decode_indexed(const void* q, const void* dense_k, const void* dense_v, int dense_rows,
+                                      long long dense_k_head_stride, long long dense_v_head_stride,
+                                      const int32_t* index, long long index_head_stride, int n_index,
+                                      const void* k_cache, const void* v_cache, long long k_head_stride,
+                                      long long v_head_stride, void* out, int n_q, int n_kv, int kv_len,
+                                      const int32_t* len_dev, int d, float scale, int dtype, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  if (!index) return STD_E_NULL;
+  const GatherArgs ga{index, index_head_stride, n_index, dense_rows, static_cast<const bf16_t*>(dense_k),
+                      static_cast<const bf16_t*>(dense_v), dense_k_head_stride, dense_v_head_stride};
+  return attn_entry(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), out, n_q, n_kv, 1, kv_len, d,
+                    k_head_stride, v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0,
+                    0, stream, 1, BatchStrides{0, 0, 0, 0}, len_dev, ga);
 }

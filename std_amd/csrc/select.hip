@@ -224,7 +224,7 @@ sel_rowstats_kernel(const T* __restrict__ q, const T* __restrict__ k, double2* _
 // lse[g][r] from the n_kb partials, in block order.
 __global__ void __launch_bounds__(256)
 sel_lse_kernel(const double2* __restrict__ part, double* __restrict__ lse, int R, int n_kb, int n_kv) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
   if (idx >= n_kv * R) return;
   const int g = idx / R, r = idx - g * R;
   const double2* p = part + (long long)g * n_kb * R + r;
@@ -329,7 +329,7 @@ sel_keys_kernel(const double* __restrict__ colpart, int n_rg2, int n_kv, int pro
                 const int32_t* __restrict__ vis, int n_vis, unsigned long long* __restrict__ keys,
                 double* __restrict__ scores_out, unsigned* __restrict__ hist) {
   const int g = blockIdx.y;
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.x * 256 + threadIdx.x;
   if (blockIdx.x == 0)
     for (int p = 0; p < 8; ++p) hist[((long long)p * n_kv + g) * 256 + threadIdx.x] = 0u;
   if (t < n_vis) {
@@ -472,7 +472,7 @@ __device__ __forceinline__ void slice_range(int n_vis, int& t0, int& t1) {
 // grid (topk_blocks(n_vis), n_kv): counts[g][blk] = (keys > T, keys == T).
 __global__ void __launch_bounds__(TOPK_THREADS)
 sel_topk_count_kernel(const unsigned long long* __restrict__ keys_all, int n_vis, int k_sel, int n_kv,
-                      const unsigned* __restrict__ hist, int2* __restrict__ counts) {
+                      const unsigned* __restrict__ hist, int2* __restrict__ counts, int n_tb) {
   __shared__ int wave_tot[TOPK_THREADS / 64];
   __shared__ int sh[3];
   __shared__ int s_gt;
@@ -488,7 +488,7 @@ sel_topk_count_kernel(const unsigned long long* __restrict__ keys_all, int n_vis
   }
   block_exclusive_scan(gt, wave_tot, &s_gt);
   block_exclusive_scan(eq, wave_tot, sh + 2);
-  if (threadIdx.x == 0) counts[(long long)g * gridDim.x + blockIdx.x] = make_int2(s_gt, sh[2]);
+  if (threadIdx.x == 0) counts[(long long)g * n_tb + blockIdx.x] = make_int2(s_gt, sh[2]);
 }
 
 // grid (topk_blocks(n_vis), n_kv): emit the block's selected positions at
@@ -496,7 +496,7 @@ sel_topk_count_kernel(const unsigned long long* __restrict__ keys_all, int n_vis
 __global__ void __launch_bounds__(TOPK_THREADS)
 sel_topk_emit_kernel(const unsigned long long* __restrict__ keys_all, const int32_t* __restrict__ vis, int n_vis,
                      int k_sel, int n_kv, const unsigned* __restrict__ hist, const int2* __restrict__ counts,
-                     int32_t* __restrict__ topk_out) {
+                     int32_t* __restrict__ topk_out, int n_tb) {
   __shared__ int wave_tot[TOPK_THREADS / 64];
   __shared__ int sh[3];
   __shared__ int s_before[2];
@@ -507,7 +507,7 @@ sel_topk_emit_kernel(const unsigned long long* __restrict__ keys_all, const int3
   if (tid == 0) {
     int eq_before = 0, sel_before = 0;
     for (int b = 0; b < (int)blockIdx.x; ++b) {
-      const int2 c = counts[(long long)g * gridDim.x + b];
+      const int2 c = counts[(long long)g * n_tb + b];
       sel_before += c.x + min(max(kk - eq_before, 0), c.y);
       eq_before += c.y;
     }
@@ -555,7 +555,7 @@ __global__ void __launch_bounds__(256)
 compact_index_kernel(const int32_t* __restrict__ nonvis, int n_nv, const int32_t* __restrict__ topk, int k_sel,
                      int32_t* __restrict__ idx_out) {
   const int g = blockIdx.y;
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.x * 256 + threadIdx.x;
   const int total = n_nv + k_sel;
   if (t >= total) return;
   const int32_t* tk = topk + (long long)g * k_sel;
@@ -577,7 +577,7 @@ compact_kv_kernel(const char* __restrict__ dk, const char* __restrict__ dv, char
                   long long dhs_bytes, int dense_rows, long long shs_bytes, int sparse_rows) {
   const int g = blockIdx.y, kv = blockIdx.z;
   const int cpr = row_bytes / 16;
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = blockIdx.x * 256 + threadIdx.x;
   const int s = c / cpr, col = c - s * cpr;
   if (s >= compact_len || s >= sparse_rows) return;
   const int src_row = idx[(long long)g * compact_len + s];
@@ -658,10 +658,11 @@ int launch_select(const void* q_text, const void* k, int n_q, int n_kv, int text
     hipLaunchKernelGGL(sel_topk_hist_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, pass);
     if ((s = launch_status())) return s;
   }
-  hipLaunchKernelGGL(sel_topk_count_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, counts);
+  hipLaunchKernelGGL(sel_topk_count_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, counts,
+                     (int)tgrid.x);
   if ((s = launch_status())) return s;
   hipLaunchKernelGGL(sel_topk_emit_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, vis, n_vis, k_sel, n_kv, hist,
-                     counts, topk_out);
+                     counts, topk_out, (int)tgrid.x);
   return launch_status();
 }
 

@@ -196,7 +196,13 @@ class RandomDecoder:
             q = ops.rope_append(qkv, hq, kc.data, vc.data, state[0:1], state[1:2], self.inv_freq)
             if self.capture_text_queries:
                 self.captured_queries[li] = q
-            out = ops.attention_devlen(q, kc.data, vc.data, state[0:1], max_kv_len=kc.capacity)
+            gather = controller.gather_for(li) if controller is not None and controller.enabled else None
+            if gather is not None:        # index-addressed sparse cache: prompt keys read from the dense cache
+                dk, dv, index, n_index = gather
+                out = ops.gqa_decode_indexed(q, dk, dv, index, n_index, kc.data, vc.data, length=state[0:1],
+                                             max_kv_len=kc.capacity)
+            else:
+                out = ops.attention_devlen(q, kc.data, vc.data, state[0:1], max_kv_len=kc.capacity)
             if host_lengths:
                 kc.advance(n)
                 vc.advance(n)

@@ -482,6 +482,78 @@ def _gemv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], r
     return y.view(*x.shape[:-1], N)
 
 
+def pad_index(index: torch.Tensor) -> torch.Tensor:
+    """int32 [n_kv, n] -> int32 [n_kv, n rounded up to 16] (padding entries 0):
+    the row layout gqa_decode_indexed reads, 16 entries at a time."""
+    if index.dtype != torch.int32 or index.dim() != 2:
+        raise TypeError("index must be int32 [n_kv, n]")
+    n_kv, n = index.shape
+    out = torch.zeros(n_kv, (n + 15) // 16 * 16, dtype=torch.int32, device=index.device)
+    out[:, :n] = index
+    return out
+
+
+def gqa_decode_indexed(query: torch.Tensor, dense_k: torch.Tensor, dense_v: torch.Tensor, index: torch.Tensor,
+                       n_index: int, key_cache: torch.Tensor, value_cache: torch.Tensor, kv_len: Optional[int] = None,
+                       length: Optional[torch.Tensor] = None, max_kv_len: Optional[int] = None,
+                       scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Draft decode whose first n_index keys per KV head are rows
+    index[g, j] of the dense cache (no compaction copy); keys j >= n_index
+    are rows j of the sparse cache key_cache / value_cache.
+
+    query [1, n_q, 1, D] bf16; dense_* and key/value caches [1, n_kv, capacity, D]
+    views with contiguous rows; index int32 [n_kv, >= n_index rounded up to 16]
+    (see pad_index). Host length: kv_len keys. Device length: length[0] + 1
+    keys (this step's row written at length[0]), planned for max_kv_len."""
+    dev = _check_device(query, dense_k, dense_v, index, key_cache, value_cache)
+    if query.dtype != torch.bfloat16:
+        raise TypeError("gqa_decode_indexed: bf16 only")
+    for name, t in (("dense_k", dense_k), ("dense_v", dense_v), ("key_cache", key_cache), ("value_cache", value_cache)):
+        _check_cache_view(name, t)
+        if t.dtype != query.dtype:
+            raise TypeError("query and caches must share a dtype")
+    if query.dim() != 4 or query.shape[0] != 1 or query.shape[2] != 1:
+        raise ValueError(f"Expected query [1, n_q, 1, D], got {tuple(query.shape)}")
+    _check_rows_contiguous("query", query)
+    n_q, d = query.shape[1], query.shape[3]
+    n_kv = key_cache.shape[1]
+    if dense_k.shape[1] != n_kv or dense_v.shape != dense_k.shape or value_cache.shape != key_cache.shape:
+        raise ValueError("dense and sparse caches must have the same KV heads")
+    if d != HEAD_DIM or n_q % n_kv:
+        raise ValueError("unsupported head_dim or head counts")
+    if index.dtype != torch.int32 or index.dim() != 2 or index.shape[0] != n_kv or index.stride(1) != 1:
+        raise TypeError("index must be int32 [n_kv, n] with contiguous rows")
+    n_index = int(n_index)
+    if not (0 <= n_index <= index.shape[1]) or index.shape[1] < (n_index + 15) // 16 * 16:
+        raise ValueError("index rows must hold n_index entries rounded up to 16 (see pad_index)")
+    if (length is None) == (kv_len is None):
+        raise ValueError("give exactly one of kv_len (host length) and length (device length)")
+    if length is not None:
+        _check_device(length)
+        _check_dev_scalar("length", length)
+        if max_kv_len is None:
+            raise ValueError("a device-length launch needs max_kv_len")
+        plan = int(max_kv_len)
+    else:
+        plan = int(kv_len)
+    if not (max(1, n_index) <= plan <= key_cache.shape[2]):
+        raise ValueError(f"key count {plan} must be in [n_index, cache capacity {key_cache.shape[2]}]")
+    if out is None:
+        out = torch.empty_like(query)
+    elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like query")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    ws_bytes = _lib.load_library().std_gqa_decode_workspace_bytes(n_q, n_kv, plan, d)
+    ws_ptr = _attn_workspace(ws_bytes, dev)
+    _lib.call("std_gqa_decode_indexed", query.data_ptr(), dense_k.data_ptr(), dense_v.data_ptr(), dense_k.shape[2],
+              dense_k.stride(1), dense_v.stride(1), index.data_ptr(), index.stride(0), n_index, key_cache.data_ptr(),
+              value_cache.data_ptr(), key_cache.stride(1), value_cache.stride(1), out.data_ptr(), n_q, n_kv, plan,
+              length.data_ptr() if length is not None else None, d, float(scale), _lib.STD_BF16, ws_ptr, ws_bytes,
+              _stream(dev))
+    return out
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
            residual: Optional[torch.Tensor] = None) -> torch.Tensor:
     """torch.nn.functional.linear for at most 16 bf16 rows: the HIP

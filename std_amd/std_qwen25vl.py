@@ -34,6 +34,11 @@ from . import ops
 from .kv_cache import KVCache, fill_cache_length, initialize_past_key_values
 
 SPARSE_ATTN_MODES = {"hip"}
+# "compact": the selected prompt rows are copied into the sparse cache
+# (compact_sparse_prompt_cache, std_qwen25vl.py:265-298); "indexed": the draft
+# reads them from the dense cache through the per-head index lists (no copy;
+# a selection refresh rewrites the indices only).
+SPARSE_KV_MODES = {"compact", "indexed"}
 
 
 @dataclass
@@ -202,9 +207,30 @@ def compact_sparse_prompt_cache(past_key_values, current_length_data: torch.Tens
     return compact_len
 
 
+def index_sparse_prompt_cache(past_key_values, current_length_data: torch.Tensor, selection: SparseSelection,
+                              dense_past_key_values):
+    """The index-addressed counterpart of compact_sparse_prompt_cache: builds
+    each layer's sorted per-head key list (padded for the indexed decode),
+    copies nothing, and sets the sparse length to compact_len as if the rows
+    were there. Returns (compact_len, per-layer (dense K, dense V, index))."""
+    compact_len = selection.compact_len
+    dev = past_key_values[0][0].data.device
+    non_visual = selection.non_visual_positions.to(dev, torch.int32)
+    gathers = []
+    for layer_idx, dense_layer in enumerate(dense_past_key_values):
+        index = ops.build_compact_index(non_visual, selection.topk_device[layer_idx])
+        if index.shape[1] != compact_len:
+            raise RuntimeError("Sparse key list has an unexpected length.")
+        gathers.append((dense_layer[0].data, dense_layer[1].data, ops.pad_index(index)))
+    fill_cache_length(current_length_data, compact_len)
+    return compact_len, gathers
+
+
 class SparseDraftController:
     """Routes the model's q_len = 1 attention to the sparse cache with the
-    HIP decode kernel while enabled (std_qwen25vl.py:234-262)."""
+    HIP decode kernel while enabled (std_qwen25vl.py:234-262); with index
+    lists set (index-addressed sparse KV) the first compact_len keys of each
+    layer are read from the dense cache through them."""
 
     def __init__(self, model, selection: SparseSelection, sparse_attn_mode: str = "hip",
                  use_compile: bool = False):
@@ -218,6 +244,15 @@ class SparseDraftController:
         self.enabled = False
         self._installed = False
         self.compiled_forward = None
+        self.gathers = None               # per layer (dense K, dense V, index) in the indexed mode
+        self.n_index = 0
+
+    def gather_for(self, layer_idx: int):
+        """(dense K, dense V, index, n_index) of a layer, or None (compacted cache)."""
+        if self.gathers is None:
+            return None
+        dk, dv, index = self.gathers[layer_idx]
+        return dk, dv, index, self.n_index
 
     def install(self) -> None:
         if self._installed:
@@ -385,8 +420,8 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
                           adaptive_gamma_min: Optional[int] = None, adaptive_gamma_mode: str = "accept_len",
                           copy_sparse_prefill: bool = True, profile_prefill: bool = False,
                           verify_attn_backend: str = "math", verify_margin_threshold: Optional[float] = None,
-                          use_compile: bool = False, ignore_eos: bool = False, use_graphs: bool = False
-                          ) -> Tuple[GenerateResult, SparseSelection]:
+                          use_compile: bool = False, ignore_eos: bool = False, use_graphs: bool = False,
+                          sparse_kv: str = "compact") -> Tuple[GenerateResult, SparseSelection]:
     """Sparse-to-Dense greedy decoding (std_qwen25vl.py:609-978).
 
     use_graphs: keep both caches' lengths and positions on the device (the
@@ -394,7 +429,15 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     pending token as three captured HIP graphs (gamma sparse draft steps; the
     dense verify forward with greedy acceptance; the sparse bonus step), with
     one readback per round; the first round and any shorter round run the same
-    device-state steps eagerly."""
+    device-state steps eagerly.
+
+    sparse_kv: "compact" gathers the selected prompt rows into the sparse
+    cache; "indexed" (bf16) has the draft read them from the dense cache
+    through the per-head index lists instead (same keys, same results)."""
+    if sparse_kv not in SPARSE_KV_MODES:
+        raise ValueError(f"Unsupported sparse_kv={sparse_kv!r}; choose one of {sorted(SPARSE_KV_MODES)}.")
+    if sparse_kv == "indexed" and model.dtype != torch.bfloat16:
+        raise ValueError("the index-addressed sparse cache serves bf16 models")
     if verify_mode != "parallel":
         raise ValueError(f"Unsupported verify_mode={verify_mode!r}; the HIP path implements 'parallel'.")
     if verify_fallback != "none" or verify_margin_threshold is not None:
@@ -437,7 +480,12 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     stage = _profile_mark(profile_prefill)
     sparse_pkv, _, sparse_lengths = initialize_past_key_values(
         model.config, dev, model.dtype, _cache_capacity(selection.compact_len, max_new_tokens, gamma))
-    sparse_prompt_len = compact_sparse_prompt_cache(sparse_pkv, sparse_lengths, selection, dense_pkv)
+    if sparse_kv == "indexed":
+        sparse_prompt_len, controller.gathers = index_sparse_prompt_cache(sparse_pkv, sparse_lengths, selection,
+                                                                          dense_pkv)
+        controller.n_index = sparse_prompt_len
+    else:
+        sparse_prompt_len = compact_sparse_prompt_cache(sparse_pkv, sparse_lengths, selection, dense_pkv)
     sparse_next = dense_next.clone()
     sparse_cache_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
 

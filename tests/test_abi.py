@@ -112,6 +112,24 @@ def test_select_validation():
                                NULL) == -5
 
 
+def test_indexed_decode_validation():
+    lib = _lib.load_library()
+    hs = 128 * 4096
+    # fp32 is not served; the index must be present, aligned and padded to 16 entries per row
+    args = dict(q=16, dk=16, dv=16, rows=4096, dks=hs, dvs=hs, idx=16, ihs=1024, n=1024, k=16, v=16, ks=hs, vs=hs,
+                out=16, nq=28, nkv=4, kv=1100, ld=NULL, d=128, scale=0.088, dt=1, ws=16, wsb=1 << 30, st=NULL)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.std_gqa_decode_indexed(*a.values())
+    assert call(dt=0) == -2
+    assert call(idx=NULL) == -1
+    assert call(idx=20) == -5
+    assert call(ihs=1000) == -3                 # below n_index
+    assert call(n=2000) == -3                   # more indexed keys than keys
+    assert call(ihs=1026, n=1024) == -5         # row stride not a multiple of 4 entries
+
+
 def test_gemv_validation():
     lib = _lib.load_library()
     # K must be a multiple of 32; at most 16 rows; bf16 only; 16-byte aligned rows

@@ -167,3 +167,19 @@ def test_graph_rounds_bf16_with_eos_stop():
                                     target_k_plus_text=TARGET, ignore_eos=False, use_graphs=True)
     got = stop.output_ids[0, -stop.generate_len:].tolist()
     assert got == gen[:gen.index(eos) + 1]
+
+
+@pytest.mark.parametrize("use_graphs", [False, True])
+def test_indexed_sparse_kv_tokens_equal_compact(use_graphs):
+    """The index-addressed sparse cache (the draft reads the selected prompt
+    rows from the dense cache through the index lists) sees the same keys in
+    the same order as the compacted cache: identical tokens and acceptance."""
+    cfg = DecoderConfig.tiny(layers=2)
+    model = RandomDecoder(cfg, dev(), torch.bfloat16, seed=7)
+    inputs = _inputs(cfg, 9, dtype=torch.bfloat16)
+    announce(f"e2e STD tiny bf16, sparse_kv indexed vs compact, graphs={use_graphs}")
+    kw = dict(max_new_tokens=32, gamma=9, target_k_plus_text=TARGET, ignore_eos=True, use_graphs=use_graphs)
+    comp, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, **kw)
+    idx, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, sparse_kv="indexed", **kw)
+    assert torch.equal(idx.output_ids, comp.output_ids)
+    assert idx.accept_lengths == comp.accept_lengths and idx.generate_len == 32

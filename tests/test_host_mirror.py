@@ -1,5 +1,7 @@
 """Host-side logic of the std_qwen25vl / kv_cache mirror (CPU only: no
 kernel is launched)."""
+import types
+
 import pytest
 import torch
 
@@ -95,10 +97,17 @@ def test_controller_validates_mode():
 
 @pytest.mark.parametrize("kwargs", [dict(verify_mode="sequential"), dict(verify_fallback="sequential_on_reject"),
                                     dict(adaptive_gamma_min=0), dict(verify_attn_backend="flash"),
-                                    dict(copy_sparse_prefill=False)])
+                                    dict(copy_sparse_prefill=False), dict(sparse_kv="paged")])
 def test_std_generate_rejects_unsupported_options(kwargs):
     with pytest.raises(ValueError):
         std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
+
+
+def test_indexed_sparse_kv_needs_bf16():
+    fp32_model = types.SimpleNamespace(dtype=torch.float32)
+    with pytest.raises(ValueError):
+        std_generate_qwen25vl(fp32_model, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8,
+                              sparse_kv="indexed")
 
 
 def test_generate_result_fields_and_rate():
