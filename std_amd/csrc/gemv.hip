@@ -144,19 +144,35 @@ extern "C" size_t std_gemv_workspace_bytes(int M, int N, int K) {
 namespace stdhip {
 namespace {
 
+// Waves per workgroup by the number of 16-column blocks (measured at one row
+// on the 7B projection shapes, graph-replayed): few blocks (o, down: 224)
+// need eight waves per block to keep enough loads in flight; 288 (q/k/v) run
+// best at four; 1184 (the gated gate/up: 56 vs 58 us at four) at one; 9504
+// (lm_head: 190 vs 228 us at four) at two.
+inline int gemv_waves(int N) {
+  const int blocks = (N + 15) / 16;
+  return blocks < 256 ? 8 : blocks < 1024 ? 4 : blocks < 4096 ? 1 : 2;
+}
+
+template <bool GATED, int WK>
+void launch_gemv_wk(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias,
+                    const void* residual, long long r_rs, void* y, long long y_rs, int M, int N, int K,
+                    hipStream_t st) {
+  hipLaunchKernelGGL((gemv_bf16_kernel<WK, GATED>), dim3((N + 15) / 16), dim3(64 * WK), 0, st,
+                     static_cast<const bf16_t*>(w), w_rs, static_cast<const bf16_t*>(x), x_rs,
+                     static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(residual), r_rs,
+                     static_cast<bf16_t*>(y), y_rs, M, N, K);
+}
+
 template <bool GATED>
 int launch_gemv(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias, const void* residual,
                 long long r_rs, void* y, long long y_rs, int M, int N, int K, hipStream_t st) {
-  const dim3 grid((N + 15) / 16);
-  // K per wave: about 512-2400 k (eight waves once K is large)
-  if (K > 4096)
-    hipLaunchKernelGGL((gemv_bf16_kernel<8, GATED>), grid, dim3(512), 0, st, static_cast<const bf16_t*>(w), w_rs,
-                       static_cast<const bf16_t*>(x), x_rs, static_cast<const bf16_t*>(bias),
-                       static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
-  else
-    hipLaunchKernelGGL((gemv_bf16_kernel<4, GATED>), grid, dim3(256), 0, st, static_cast<const bf16_t*>(w), w_rs,
-                       static_cast<const bf16_t*>(x), x_rs, static_cast<const bf16_t*>(bias),
-                       static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
+  switch (gemv_waves(N)) {
+    case 1: launch_gemv_wk<GATED, 1>(x, x_rs, w, w_rs, bias, residual, r_rs, y, y_rs, M, N, K, st); break;
+    case 2: launch_gemv_wk<GATED, 2>(x, x_rs, w, w_rs, bias, residual, r_rs, y, y_rs, M, N, K, st); break;
+    case 4: launch_gemv_wk<GATED, 4>(x, x_rs, w, w_rs, bias, residual, r_rs, y, y_rs, M, N, K, st); break;
+    default: launch_gemv_wk<GATED, 8>(x, x_rs, w, w_rs, bias, residual, r_rs, y, y_rs, M, N, K, st); break;
+  }
   return launch_status();
 }
 
