@@ -390,7 +390,7 @@ def main():
         "select_compact_ms_all_layers": round(select_ms, 3),
         "select_compact_ms_first_call": round(select_ms_first, 3),
         "roofline": {
-            "kernel": "verify attention, one layer (attn_bf16_kernel<5> + attn_merge_kernel<bf16>)",
+            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false> + attn_merge_kernel<bf16>)",
             "bound": "hbm",
             "achieved": round(verify_gbps, 1),
             "peak": HBM_PEAK_GBPS,
