@@ -43,6 +43,45 @@ __device__ __forceinline__ bf16x8_t ld16(const bf16_t* p) {
 // bias), the decoder's residual add rounded as torch rounds it.
 __device__ __forceinline__ float round_bf16(float v) { return to_f32<bf16_t>(from_f32<bf16_t>(v)); }
 
+// The waves' 16 x M partial tiles are added in wave order through LDS by wave
+// 0, which applies the epilogue (bias, the gated activation, the residual)
+// and writes bf16 rows m < M.
+template <int WK, bool GATED>
+__device__ __forceinline__ void gemv_finish(f32x4 (*red)[WK][64], const f32x4* acc, int wave, int lane, int n0,
+                                            const bf16_t* __restrict__ bias, const bf16_t* __restrict__ residual,
+                                            long long r_rs, bf16_t* __restrict__ y, long long y_rs, int M, int N) {
+  constexpr int kMat = GATED ? 2 : 1;
+  const int ln = lane & 15, lg = lane >> 4;
+  const bool xm = ln < M;
+#pragma unroll
+  for (int j = 0; j < kMat; ++j) red[j][wave][lane] = acc[j];
+  __syncthreads();
+  if (wave != 0 || !xm) return;
+  f32x4 t[kMat];
+#pragma unroll
+  for (int j = 0; j < kMat; ++j) {
+    t[j] = red[j][0][lane];
+#pragma unroll
+    for (int i = 1; i < WK; ++i) t[j] += red[j][i][lane];
+  }
+  const int n = n0 + 4 * lg;                   // this lane's 4 columns of row m = ln
+  bf16_t* dst = y + (long long)ln * y_rs + n;
+  const bf16_t* res = residual ? residual + (long long)ln * r_rs + n : nullptr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (n + i < N) {
+      float v = round_bf16(bias ? t[0][i] + to_f32<bf16_t>(bias[n + i]) : t[0][i]);
+      if constexpr (GATED) {
+        const float u = round_bf16(bias ? t[kMat - 1][i] + to_f32<bf16_t>(bias[N + n + i]) : t[kMat - 1][i]);
+        const float s = round_bf16(__fdiv_rn(v, __fadd_rn(1.0f, expf(-v))));   // silu(g) in fp32, rounded
+        v = round_bf16(s * u);
+      }
+      if (res) v = __fadd_rn(to_f32<bf16_t>(res[i]), v);
+      dst[i] = from_f32<bf16_t>(v);
+    }
+}
+
+
 template <int WK, bool GATED>
 __global__ void __launch_bounds__(64 * WK)
 gemv_bf16_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
@@ -101,32 +140,61 @@ gemv_bf16_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __r
 #pragma unroll
     for (int j = 0; j < kMat; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ld16(wr[j] + k), bv, acc[j], 0, 0, 0);
   }
+  gemv_finish<WK, GATED>(red, acc, wave, lane, n0, bias, residual, r_rs, y, y_rs, M, N);
+}
+
+// Short K ranges at up to kShortRows rows (the q/k/v and o projections of a
+// decode step, latency-bound otherwise): every wave issues all of its weight
+// loads at once -- one memory round trip instead of a stream of dependent
+// steps -- and stages its slice of the activation rows in LDS meanwhile
+// (the wave reads back only what it wrote), then runs its MFMAs.
+constexpr int kShortSteps = 32;     // MFMA steps of 32 k per wave (128 VGPRs of weights)
+constexpr int kShortRows = 4;
+constexpr int kShortMaxK = 4096;
+
+template <int WK, bool GATED>
+__global__ void __launch_bounds__(64 * WK)
+gemv_short_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
+                  const bf16_t* __restrict__ bias, const bf16_t* __restrict__ residual, long long r_rs,
+                  bf16_t* __restrict__ y, long long y_rs, int M, int N, int K) {
+  constexpr int kMat = GATED ? 2 : 1;
+  constexpr int NS = kShortSteps / kMat;
+  __shared__ f32x4 red[kMat][WK][64];
+  __shared__ __align__(16) bf16_t xs[kShortRows * kShortMaxK];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;
+  const int k_begin = min(K, wave * kw), k_end = min(K, k_begin + kw);
+  const int nsteps = (k_end - k_begin) / 32;   // <= NS (checked on the host)
+  const bf16_t* wr[kMat];
+  wr[0] = w + (long long)min(n0 + ln, N - 1) * w_rs + k_begin + 8 * lg;
+  if constexpr (GATED) wr[kMat - 1] = wr[0] + (long long)N * w_rs;
+  bf16x8_t a[kMat][NS];
 #pragma unroll
-  for (int j = 0; j < kMat; ++j) red[j][wave][lane] = acc[j];
-  __syncthreads();
-  if (wave != 0 || !xm) return;
-  f32x4 t[kMat];
+  for (int u = 0; u < NS; ++u)
+    if (u < nsteps)
 #pragma unroll
-  for (int j = 0; j < kMat; ++j) {
-    t[j] = red[j][0][lane];
-#pragma unroll
-    for (int i = 1; i < WK; ++i) t[j] += red[j][i][lane];
+      for (int j = 0; j < kMat; ++j) a[j][u] = ld16(wr[j] + 32 * u);
+  const int cpr = (k_end - k_begin) / 8;       // 16-byte chunks per activation row
+  for (int c = lane; c < M * cpr; c += 64) {
+    const int m = c / cpr, kk = k_begin + (c - m * cpr) * 8;
+    *reinterpret_cast<uint4*>(xs + m * K + kk) = *reinterpret_cast<const uint4*>(x + (long long)m * x_rs + kk);
   }
-  const int n = n0 + 4 * lg;                   // this lane's 4 columns of row m = ln
-  bf16_t* dst = y + (long long)ln * y_rs + n;
-  const bf16_t* res = residual ? residual + (long long)ln * r_rs + n : nullptr;
+  const bool xm = ln < M;
+  const bf16_t* xl = xs + (xm ? ln : 0) * K + k_begin + 8 * lg;
+  const bf16x8_t zero = {};
+  f32x4 acc[kMat];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (n + i < N) {
-      float v = round_bf16(bias ? t[0][i] + to_f32<bf16_t>(bias[n + i]) : t[0][i]);
-      if constexpr (GATED) {
-        const float u = round_bf16(bias ? t[kMat - 1][i] + to_f32<bf16_t>(bias[N + n + i]) : t[kMat - 1][i]);
-        const float s = round_bf16(__fdiv_rn(v, __fadd_rn(1.0f, expf(-v))));   // silu(g) in fp32, rounded
-        v = round_bf16(s * u);
-      }
-      if (res) v = __fadd_rn(to_f32<bf16_t>(res[i]), v);
-      dst[i] = from_f32<bf16_t>(v);
+  for (int j = 0; j < kMat; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < NS; ++u)
+    if (u < nsteps) {
+      const bf16x8_t bv = xm ? ld16(xl + 32 * u) : zero;
+#pragma unroll
+      for (int j = 0; j < kMat; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][u], bv, acc[j], 0, 0, 0);
     }
+  gemv_finish<WK, GATED>(red, acc, wave, lane, n0, bias, residual, r_rs, y, y_rs, M, N);
 }
 
 }  // namespace
@@ -158,10 +226,13 @@ template <bool GATED, int WK>
 void launch_gemv_wk(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias,
                     const void* residual, long long r_rs, void* y, long long y_rs, int M, int N, int K,
                     hipStream_t st) {
-  hipLaunchKernelGGL((gemv_bf16_kernel<WK, GATED>), dim3((N + 15) / 16), dim3(64 * WK), 0, st,
-                     static_cast<const bf16_t*>(w), w_rs, static_cast<const bf16_t*>(x), x_rs,
-                     static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(residual), r_rs,
-                     static_cast<bf16_t*>(y), y_rs, M, N, K);
+  constexpr int kMat = GATED ? 2 : 1;
+  const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;
+  const bool short_k = M <= kShortRows && K <= kShortMaxK && kw / 32 <= kShortSteps / kMat;
+  auto kern = short_k ? gemv_short_kernel<WK, GATED> : gemv_bf16_kernel<WK, GATED>;
+  hipLaunchKernelGGL(kern, dim3((N + 15) / 16), dim3(64 * WK), 0, st, static_cast<const bf16_t*>(w), w_rs,
+                     static_cast<const bf16_t*>(x), x_rs, static_cast<const bf16_t*>(bias),
+                     static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
 }
 
 template <bool GATED>
