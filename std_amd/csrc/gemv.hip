@@ -21,7 +21,6 @@ namespace stdhip {
 namespace {
 
 constexpr int kUnroll = 8;                     // MFMAs (32 k each) per step
-constexpr int kStepK = 32 * kUnroll;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
@@ -82,7 +81,15 @@ __device__ __forceinline__ void gemv_finish(f32x4 (*red)[WK][64], const f32x4* a
 }
 
 
-template <int WK, bool GATED, int COLS>
+// Steps of loads kept in flight per wave by the streaming kernel: a ring of
+// kRing register buffers, refilled kRing - 1 steps ahead of the MFMAs (3 steps
+// = 24 KB per wave; 2 and 3 ring slots measured slower at one row).
+constexpr int kRing = 4;
+
+// Weight lanes of columns past N load column N - 1 (D[n][m] depends only on
+// weight row n and activation row m, and columns n >= N are not written);
+// activation lanes of rows m >= M load nothing and hold zeros.
+template <int WK, bool GATED>
 __global__ void __launch_bounds__(64 * WK)
 gemv_bf16_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
                  const bf16_t* __restrict__ bias, const bf16_t* __restrict__ residual, long long r_rs,
@@ -91,62 +98,127 @@ gemv_bf16_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __r
   constexpr int kU = kUnroll / kMat;           // k-steps of 32 per step (8 loads of 16 B per lane either way)
   constexpr int kStep = 32 * kU;
   __shared__ f32x4 red[kMat][WK][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // Wave-uniform, so the step loop below is scalar control flow.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15, lg = lane >> 4;
-  const int n0 = blockIdx.x * COLS;
-  const bool aw = ln < COLS;            // lanes past COLS carry zero weight rows
+  const int n0 = blockIdx.x * 16;
   const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;        // this wave's K range
   const int k_begin = min(K, wave * kw), k_end = min(K, k_begin + kw);
+  const int nsteps = (k_end - k_begin) / kStep;
   const bf16_t* wr[kMat];
-  wr[0] = w + (long long)min(n0 + ln, N - 1) * w_rs + 8 * lg;
+  wr[0] = w + (long long)min(n0 + ln, N - 1) * w_rs + k_begin + 8 * lg;
   if constexpr (GATED) wr[kMat - 1] = wr[0] + (long long)N * w_rs;
   const bool xm = ln < M;
-  const bf16_t* xr = x + (long long)(xm ? ln : 0) * x_rs + 8 * lg;
-  const bf16x8_t zero = {};
+  const bf16_t* xr = x + (long long)(xm ? ln : 0) * x_rs + k_begin + 8 * lg;
   f32x4 acc[kMat];
 #pragma unroll
   for (int j = 0; j < kMat; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  int k = k_begin;
-  // Two steps of loads in flight: the next step's weights are requested
-  // before the current step's MFMAs consume theirs.
-  bf16x8_t a[kMat][kU], b[kU];
+  // Ring slot r holds step t with t % kRing == r. The ring is indexed by
+  // compile-time constants only (the step loop is unrolled by kRing), so no
+  // register copy ever waits on a load that is still in flight. Every slot
+  // load is issued whatever the step count -- steps past the last one re-read
+  // the last step, which is still in cache -- so the number of weight loads
+  // issued after any slot is fixed and each MFMA waits only for its own slot
+  // (a skipped slot behind a scalar branch makes the compiler wait for all).
+  bf16x8_t a[kRing][kMat][kU], b[kRing][kU];
+  auto load = [&](int t, int r) {
+    const int kk = min(t, nsteps - 1) * kStep;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+#pragma unroll
+      for (int j = 0; j < kMat; ++j) a[r][j][u] = ld16(wr[j] + kk + 32 * u);
+      b[r][u] = xm ? ld16(xr + kk + 32 * u) : bf16x8_t{};
+    }
+  };
+  auto mma = [&](int r) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int j = 0; j < kMat; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[r][j][u], b[r][u], acc[j], 0, 0, 0);
+  };
+  if (nsteps > 0) {
+#pragma unroll
+    for (int r = 0; r < kRing - 1; ++r) load(r, r);
+    int t = 0;
+    for (; t + kRing <= nsteps; t += kRing) {
+#pragma unroll
+      for (int r = 0; r < kRing; ++r) {
+        load(t + r + kRing - 1, (r + kRing - 1) % kRing);
+        mma(r);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kRing - 1; ++r)        // the last nsteps % kRing steps, already loaded
+      if (t + r < nsteps) mma(r);
+  }
+  for (int k = nsteps * kStep; k < k_end - k_begin; k += 32) {   // K is a multiple of 32
+    const bf16x8_t bv = xm ? ld16(xr + k) : bf16x8_t{};
+#pragma unroll
+    for (int j = 0; j < kMat; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ld16(wr[j] + k), bv, acc[j], 0, 0, 0);
+  }
+  gemv_finish<WK, GATED, 16>(red, acc, wave, lane, n0, bias, residual, r_rs, y, y_rs, M, N);
+}
+
+// The gated projection at more than four rows (the ten-row verify step): one
+// wave per workgroup walks all of K, requesting the next step's loads before
+// the current step's MFMAs and draining them after (the copy into the
+// current step's registers waits for them). Measured 53.4 us at ten rows on
+// the 7B gate/up against 57-65 us for the ring kernel at one to four waves.
+__global__ void __launch_bounds__(64)
+gemv_gated_rows_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
+                       const bf16_t* __restrict__ bias, const bf16_t* __restrict__ residual, long long r_rs,
+                       bf16_t* __restrict__ y, long long y_rs, int M, int N, int K) {
+  constexpr int kU = kUnroll / 2;
+  constexpr int kStep = 32 * kU;
+  __shared__ f32x4 red[2][1][64];
+  const int lane = threadIdx.x;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const bf16_t* wr[2];
+  wr[0] = w + (long long)min(n0 + ln, N - 1) * w_rs + 8 * lg;
+  wr[1] = wr[0] + (long long)N * w_rs;
+  const bool xm = ln < M;
+  const bf16_t* xr = x + (long long)(xm ? ln : 0) * x_rs + 8 * lg;
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  bf16x8_t a[2][kU], b[kU];
   auto load = [&](int kk, bf16x8_t (*aa)[kU], bf16x8_t* bb) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
 #pragma unroll
-      for (int j = 0; j < kMat; ++j) aa[j][u] = aw ? ld16(wr[j] + kk + 32 * u) : zero;
-      bb[u] = xm ? ld16(xr + kk + 32 * u) : zero;
+      for (int j = 0; j < 2; ++j) aa[j][u] = ld16(wr[j] + kk + 32 * u);
+      bb[u] = xm ? ld16(xr + kk + 32 * u) : bf16x8_t{};
     }
   };
-  if (k + kStep <= k_end) load(k, a, b);
-  for (; k + kStep <= k_end; k += kStep) {
-    bf16x8_t an[kMat][kU], bn[kU];
-    const bool more = k + 2 * kStep <= k_end;
+  int k = 0;
+  if (k + kStep <= K) load(k, a, b);
+  for (; k + kStep <= K; k += kStep) {
+    bf16x8_t an[2][kU], bn[kU];
+    const bool more = k + 2 * kStep <= K;
     if (more) load(k + kStep, an, bn);
 #pragma unroll
     for (int u = 0; u < kU; ++u)
 #pragma unroll
-      for (int j = 0; j < kMat; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][u], b[u], acc[j], 0, 0, 0);
+      for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][u], b[u], acc[j], 0, 0, 0);
     if (more) {
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
 #pragma unroll
-        for (int j = 0; j < kMat; ++j) a[j][u] = an[j][u];
+        for (int j = 0; j < 2; ++j) a[j][u] = an[j][u];
         b[u] = bn[u];
       }
     }
   }
-  for (; k < k_end; k += 32) {                 // K is a multiple of 32
-    const bf16x8_t bv = xm ? ld16(xr + k) : zero;
+  for (; k < K; k += 32) {                     // K is a multiple of 32
+    const bf16x8_t bv = xm ? ld16(xr + k) : bf16x8_t{};
 #pragma unroll
-    for (int j = 0; j < kMat; ++j)
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aw ? ld16(wr[j] + k) : zero, bv, acc[j], 0, 0, 0);
+    for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ld16(wr[j] + k), bv, acc[j], 0, 0, 0);
   }
-  gemv_finish<WK, GATED, COLS>(red, acc, wave, lane, n0, bias, residual, r_rs, y, y_rs, M, N);
+  gemv_finish<1, true, 16>(red, acc, 0, lane, n0, bias, residual, r_rs, y, y_rs, M, N);
 }
 
-// Short K ranges at up to kShortRows rows (the q/k/v and o projections of a
-// decode step, latency-bound otherwise): every wave issues all of its weight
+// Short K ranges at up to kShortRows rows (the q/k/v and lm_head projections
+// of a decode step): every wave issues all of its weight
 // loads at once -- one memory round trip instead of a stream of dependent
 // steps -- and stages its slice of the activation rows in LDS meanwhile
 // (the wave reads back only what it wrote), then runs its MFMAs.
@@ -215,48 +287,50 @@ extern "C" size_t std_gemv_workspace_bytes(int M, int N, int K) {
 namespace stdhip {
 namespace {
 
-// Waves per workgroup by the number of 16-column blocks (measured at one row
-// on the 7B projection shapes, graph-replayed): few blocks (o, down: 224)
-// need eight waves per block to keep enough loads in flight; 288 (q/k/v) run
-// best at four; 1184 (the gated gate/up: 56 vs 58 us at four) at one; 9504
-// (lm_head: 190 vs 228 us at four) at two.
-inline int gemv_waves(int N) {
-  const int blocks = (N + 15) / 16;
-  return blocks < 256 ? 8 : blocks < 1024 ? 4 : blocks < 4096 ? 1 : 2;
-}
-
-template <bool GATED, int WK, int COLS>
-void launch_gemv_wk(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias,
-                    const void* residual, long long r_rs, void* y, long long y_rs, int M, int N, int K, bool short_k,
-                    hipStream_t st) {
-  auto kern = short_k ? gemv_short_kernel<WK, GATED, COLS> : gemv_bf16_kernel<WK, GATED, COLS>;
-  hipLaunchKernelGGL(kern, dim3((N + COLS - 1) / COLS), dim3(64 * WK), 0, st, static_cast<const bf16_t*>(w), w_rs,
-                     static_cast<const bf16_t*>(x), x_rs, static_cast<const bf16_t*>(bias),
-                     static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
+// Waves per workgroup (the K split), from kernel durations at one and ten
+// rows on the 7B projection shapes (16-column blocks: q/k/v 288, o and down
+// 224, gate/up 1184 of 2368 stacked, lm_head 9504). The split is chosen from
+// the non-gated projection of all N_rows weight rows, so a gated launch adds
+// exactly the sums of the plain projection of its stacked [gate; up] weight:
+//  - up to kShortRows rows, K <= kShortMaxK and >= 256 blocks: four waves
+//    (a K range of at most 1024 = kShortSteps steps per wave) -- the short
+//    kernel, eight-column workgroups below 1024 blocks so the work spreads
+//    over every CU (q/k/v 11.3 us; lm_head 171 us against 179 us streaming);
+//    gated, the ring kernel (gate/up 48.5 us against 50.3 us at one wave);
+//  - other shapes up to kShortRows rows: two waves, ring kernel (o 7.6 us
+//    against 8.6 us on the short path; down 25.7 us);
+//  - more rows: one wave (at ten rows o 9.0 us, down 32.3 us; gate/up 53.4 us
+//    in gemv_gated_rows_kernel against 57-65 us for the ring kernel).
+inline int gemv_waves(int M, int n_rows, int K) {
+  if (M > kShortRows) return 1;
+  return K <= kShortMaxK && (n_rows + 15) / 16 >= 256 ? 4 : 2;
 }
 
 template <bool GATED>
 int launch_gemv(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias, const void* residual,
                 long long r_rs, void* y, long long y_rs, int M, int N, int K, hipStream_t st) {
-  constexpr int kMat = GATED ? 2 : 1;
-  const int wk = gemv_waves(N);
-  const int kw = (((K + wk - 1) / wk) + 31) / 32 * 32;
-  const bool short_k = M <= kShortRows && K <= kShortMaxK && kw / 32 <= kShortSteps / kMat;
-  // 256-1023 column blocks on the short path (q/k/v: 288): eight-column
-  // workgroups spread the work over every CU (11.1 vs 12.4 us at one row;
-  // the same K split, so the same results).
   const int blocks = (N + 15) / 16;
-  const bool cols8 = short_k && blocks >= 256 && blocks < 1024;
-#define STD_GEMV_LAUNCH(W)                                                                                        \
-  (cols8 ? launch_gemv_wk<GATED, W, 8>(x, x_rs, w, w_rs, bias, residual, r_rs, y, y_rs, M, N, K, short_k, st)     \
-         : launch_gemv_wk<GATED, W, 16>(x, x_rs, w, w_rs, bias, residual, r_rs, y, y_rs, M, N, K, short_k, st))
-  switch (wk) {
-    case 1: STD_GEMV_LAUNCH(1); break;
-    case 2: STD_GEMV_LAUNCH(2); break;
-    case 4: STD_GEMV_LAUNCH(4); break;
-    default: STD_GEMV_LAUNCH(8); break;
+  const int wk = gemv_waves(M, GATED ? 2 * N : N, K);
+  auto launch = [&](auto kern, int grid, int waves) {
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * waves), 0, st, static_cast<const bf16_t*>(w), w_rs,
+                       static_cast<const bf16_t*>(x), x_rs, static_cast<const bf16_t*>(bias),
+                       static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
+  };
+  static_assert((kShortMaxK / 4) / 32 <= kShortSteps, "four waves cover K in kShortSteps steps each");
+  if constexpr (GATED) {
+    if (wk == 4) launch(gemv_bf16_kernel<4, true>, blocks, 4);
+    else if (wk == 2) launch(gemv_bf16_kernel<2, true>, blocks, 2);
+    else launch(gemv_gated_rows_kernel, blocks, 1);
+  } else {
+    if (wk == 4) {
+      if (blocks < 1024) launch(gemv_short_kernel<4, false, 8>, (N + 7) / 8, 4);
+      else launch(gemv_short_kernel<4, false, 16>, blocks, 4);
+    } else if (wk == 2) {
+      launch(gemv_bf16_kernel<2, false>, blocks, 2);
+    } else {
+      launch(gemv_bf16_kernel<1, false>, blocks, 1);
+    }
   }
-#undef STD_GEMV_LAUNCH
   return launch_status();
 }
 
