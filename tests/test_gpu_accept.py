@@ -127,12 +127,15 @@ def test_argmax_rows_matches_oracle_with_ties_and_nan(dtype):
     assert want[3] == 5000 and want[7] == 100 and want[9] == 0
 
 
+@pytest.mark.parametrize("hidden", [3584, 100, 4096, 4097, 9000])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_rms_norm_matches_torch_formula(dtype):
-    announce(f"rms_norm {dtype} 33 x 3584")
+def test_rms_norm_matches_torch_formula(dtype, hidden):
+    """Row widths of one load batch (up to 16 x 256 elements: 3584, 100,
+    4096) and of several (4097, 9000)."""
+    announce(f"rms_norm {dtype} 33 x {hidden}")
     g = torch.Generator().manual_seed(32)
-    x = (torch.randn(1, 33, 3584, generator=g) * 3).to(dtype)
-    w = (1 + 0.1 * torch.randn(3584, generator=g)).to(dtype)
+    x = (torch.randn(1, 33, hidden, generator=g) * 3).to(dtype)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(dtype)
     got = ops.rms_norm(x.to(dev()), w.to(dev()), 1e-6).cpu()
     xf = x.float()
     want = w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype)   # modeling_qwen2_5_vl.py:192-197
