@@ -39,9 +39,10 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c4", choices=["c2", "c3", "c4", "c5"],
+    ap.add_argument("--workload", default="c4", choices=["c2", "c3", "c4", "c5", "gemv"],
                     help="c2-c4: attention hot path at 16k/64k/128k context (default c4, the headline); "
-                         "c5: end-to-end STD vs dense AR decode on a random-init Qwen2.5-VL-7B-shaped decoder")
+                         "c5: end-to-end STD vs dense AR decode on a random-init Qwen2.5-VL-7B-shaped decoder; "
+                         "gemv: the decoder's weight-streaming projections at one and ten rows")
     ap.add_argument("--new-tokens", type=int, default=128, help="c5: tokens to decode")
     ap.add_argument("--eager", action="store_true",
                     help="c5: run the decode loops eagerly (host lengths) instead of replaying captured HIP graphs")
@@ -111,6 +112,9 @@ def main():
 
     if args.workload == "c5":
         run_c5(args)
+        return
+    if args.workload == "gemv":
+        run_gemv(args)
         return
     w = WORKLOADS[args.workload]
     if args.pmc_run:
@@ -499,6 +503,77 @@ def run_c5(args) -> None:
         "note": "the prefill attention (not the decode path) runs as chunked fp32 torch matmuls",
     }
     print(json.dumps(result))
+
+
+def run_gemv(args) -> None:
+    """The Qwen2.5-VL-7B decoder's projections through the HIP GEMV at one
+    (draft / AR / bonus step) and ten (verify step) rows: q/k/v with bias, o
+    and down with the residual epilogue, gate/up with the activation epilogue,
+    lm_head. Weights ~ N(0, 0.02) bf16 in enough copies (>= 768 MB) that the
+    256 MB last-level cache holds none of them between launches; 24 launches
+    cycling the copies are captured in one HIP graph and replayed (the graph
+    launch is amortised over the 24), timed with events. Prints one JSON line."""
+    import torch
+
+    from std_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    H, I, V, QKV = 3584, 18944, 152064, 4608
+    shapes = [("q/k/v", QKV, H, "bias"), ("o", H, H, "residual"), ("gate/up", I, H, "gated"),
+              ("down", H, I, "residual"), ("lm_head", V, H, None)]
+    g = torch.Generator(device=dev).manual_seed(7)
+    results = []
+    for rows in (1, 10):
+        for name, N, K, kind in shapes:
+            NW = 2 * N if kind == "gated" else N
+            nbytes = NW * K * 2
+            copies = max(2, -(-768 * 2 ** 20 // nbytes))
+            ws = [(torch.randn(NW, K, generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(copies)]
+            x = torch.randn(1, rows, K, generator=g, device=dev).to(torch.bfloat16)
+            b = (torch.randn(NW, generator=g, device=dev) * 0.02).to(torch.bfloat16) if kind == "bias" else None
+            r = torch.randn(1, rows, N, generator=g, device=dev).to(torch.bfloat16) if kind == "residual" else None
+
+            def one(w):
+                if kind == "gated":
+                    return ops.gated_linear(x, w)
+                return ops.linear(x, w, b, residual=r)
+
+            def body():
+                for i in range(24):
+                    one(ws[i % copies])
+            body()
+            torch.cuda.synchronize()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                body()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                body()
+            for _ in range(3):
+                graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = max(2, args.steps // 4)
+            e0.record()
+            for _ in range(reps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * 24)
+            results.append({"projection": name, "rows": rows, "N": N, "K": K, "epilogue": kind, "us": round(us, 2),
+                            "weight_GB_s": round(nbytes / us / 1e3, 1),
+                            "pct_of_8TB_s": round(100 * nbytes / us / 1e3 / 8000, 1)})
+            log(f"gemv: {name} rows={rows}: {us:.2f} us ({nbytes / us / 1e3:.0f} GB/s)")
+            del ws, graph
+            torch.cuda.empty_cache()
+    print(json.dumps({"metric": "7B decoder projection time through the HIP GEMV (weights streamed from HBM)",
+                      "unit": "us", "n_gpus": 1, "dtype": "bf16", "data": "synthetic (weights ~ N(0, 0.02))",
+                      "config": {"workload": "gemv: Qwen2.5-VL-7B projections (hidden 3584, SwiGLU 18944, vocab "
+                                             "152064) at 1 and 10 rows"},
+                      "results": results}))
 
 
 def cpu_baseline(w, L):
