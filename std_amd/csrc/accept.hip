@@ -33,11 +33,18 @@ argmax_partial_kernel(const T* __restrict__ logits, long long row_stride, int vo
   const int b = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const T* x = logits + (long long)row * row_stride;
   const int start = b * AM_CHUNK, end = min(vocab, start + AM_CHUNK);
+  // All of a thread's loads are issued before the first compare (indices past
+  // the chunk re-read its last entry and are skipped): one memory round trip.
+  T v[AM_PER_THREAD];
+#pragma unroll
+  for (int j = 0; j < AM_PER_THREAD; ++j) v[j] = x[min(start + tid + j * AM_THREADS, end - 1)];
   uint32_t bk = 0;
   int bi = INT_MAX;
-  for (int e = start + tid; e < end; e += AM_THREADS) {
-    const uint32_t k = order_key(to_f32<T>(x[e]));
-    if (better(k, e, bk, bi)) { bk = k; bi = e; }
+#pragma unroll
+  for (int j = 0; j < AM_PER_THREAD; ++j) {
+    const int e = start + tid + j * AM_THREADS;
+    const uint32_t k = order_key(to_f32<T>(v[j]));
+    if (e < end && better(k, e, bk, bi)) { bk = k; bi = e; }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -55,9 +62,32 @@ argmax_partial_kernel(const T* __restrict__ logits, long long row_stride, int vo
   }
 }
 
-// One block of kFinalThreads: wave w reduces rows w, w + kFinalWaves, ... (each
-// lane takes every 64th block partial, then a shuffle reduction with the same
-// ordering), then thread 0 forms the greedy prefix, the bonus and the rollback.
+// The best (key, index) of one row's block partials, in every lane of the
+// calling wave: lane l takes partials l, l + 64, ..., kFinalBatch of them per
+// memory round trip (indices past the row re-read its last partial and are
+// skipped), then a shuffle reduction. better() is a strict total order, so
+// the result does not depend on the reduction order.
+constexpr int kFinalBatch = 4;
+
+__device__ __forceinline__ void row_best(const uint2* __restrict__ p, int n_blocks, int lane, uint32_t& bk, int& bi) {
+  for (int b0 = 0; b0 < n_blocks; b0 += 64 * kFinalBatch) {
+    uint2 v[kFinalBatch];
+#pragma unroll
+    for (int j = 0; j < kFinalBatch; ++j) v[j] = p[min(b0 + lane + 64 * j, n_blocks - 1)];
+#pragma unroll
+    for (int j = 0; j < kFinalBatch; ++j)
+      if (b0 + lane + 64 * j < n_blocks && better(v[j].x, (int)v[j].y, bk, bi)) { bk = v[j].x; bi = (int)v[j].y; }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t ok = __shfl_xor(bk, off);
+    const int oi = __shfl_xor(bi, off);
+    if (better(ok, oi, bk, bi)) { bk = ok; bi = oi; }
+  }
+}
+
+// One block of kFinalThreads: wave w reduces rows w, w + kFinalWaves, ...
+// (row_best), then thread 0 forms the greedy prefix, the bonus and the rollback.
 constexpr int kFinalThreads = 256;
 constexpr int kFinalWaves = kFinalThreads / 64;
 
@@ -70,16 +100,7 @@ accept_final_kernel(const uint2* __restrict__ part, int n_blocks, int q_rows, co
   for (int row = w; row < q_rows; row += kFinalWaves) {
     uint32_t bk = 0;
     int bi = INT_MAX;
-    for (int b = lane; b < n_blocks; b += 64) {
-      const uint2 v = part[(long long)row * n_blocks + b];
-      if (better(v.x, (int)v.y, bk, bi)) { bk = v.x; bi = (int)v.y; }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const uint32_t ok = __shfl_xor(bk, off);
-      const int oi = __shfl_xor(bi, off);
-      if (better(ok, oi, bk, bi)) { bk = ok; bi = oi; }
-    }
+    row_best(part + (long long)row * n_blocks, n_blocks, lane, bk, bi);
     if (lane == 0) pred[row + (has_pending ? 0 : 1)] = bi;
   }
   if (tid == 0 && !has_pending) pred[0] = *dense_next;
@@ -94,19 +115,15 @@ accept_final_kernel(const uint2* __restrict__ part, int n_blocks, int q_rows, co
   }
 }
 
-// Final step of the row argmax: thread r reduces row r's block partials in
-// block order and writes the index as int64 (the token-id type of torch).
-__global__ void __launch_bounds__(256)
-argmax_final_kernel(const uint2* __restrict__ part, int n_blocks, int rows, long long* __restrict__ out) {
-  const int r = blockIdx.x * 256 + threadIdx.x;
-  if (r >= rows) return;
+// Final step of the row argmax: one wave per row reduces its block partials
+// (row_best) and writes the index as int64 (the token-id type of torch).
+__global__ void __launch_bounds__(64)
+argmax_final_kernel(const uint2* __restrict__ part, int n_blocks, long long* __restrict__ out) {
+  const int r = blockIdx.x, lane = threadIdx.x;
   uint32_t bk = 0;
   int bi = INT_MAX;
-  for (int b = 0; b < n_blocks; ++b) {
-    const uint2 v = part[(long long)r * n_blocks + b];
-    if (better(v.x, (int)v.y, bk, bi)) { bk = v.x; bi = (int)v.y; }
-  }
-  out[r] = bi;
+  row_best(part + (long long)r * n_blocks, n_blocks, lane, bk, bi);
+  if (lane == 0) out[r] = bi;
 }
 
 // One block per row: out = weight * dtype(x * rsqrt(mean(x^2) + eps)), the
@@ -303,7 +320,7 @@ extern "C" int std_argmax_rows(const void* logits, long long logits_row_stride, 
                        static_cast<const float*>(logits), logits_row_stride, vocab, nb, part);
   int s = launch_status();
   if (s) return s;
-  hipLaunchKernelGGL(argmax_final_kernel, dim3((rows + 255) / 256), dim3(256), 0, st, part, nb, rows, out);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, st, part, nb, out);
   return launch_status();
 }
 

@@ -190,19 +190,20 @@ attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_
   const long long base = ((long long)blockIdx.z * n_kv + g) * n_split * R + r;
   const f32x4* col = reinterpret_cast<const f32x4*>(ws_o + base * D) + d4;
   const long long step = (long long)R * (D / 4);
+  // Every load below is issued before the first use: splits past n_split
+  // re-read the last one and are masked after the load (a load under a
+  // condition would compile to a branch that waits for it).
   f32x4 pre[kMergePrefetch];
 #pragma unroll
-  for (int j = 0; j < kMergePrefetch; ++j) {
-    const int sp = sg + j * kMergeGroups;
-    pre[j] = sp < n_split ? col[sp * step] : f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int j = 0; j < kMergePrefetch; ++j) pre[j] = col[min(sg + j * kMergeGroups, n_split - 1) * step];
   constexpr int kMlPerThread = kMaxSplit / kMergeThreads;
   float2 mls[kMlPerThread];
+#pragma unroll
+  for (int i = 0; i < kMlPerThread; ++i) mls[i] = ws_ml[base + (long long)min(tid + i * kMergeThreads, n_split - 1) * R];
   float m = -1e30f;
 #pragma unroll
   for (int i = 0; i < kMlPerThread; ++i) {
-    const int sp = tid + i * kMergeThreads;
-    mls[i] = sp < n_split ? ws_ml[base + (long long)sp * R] : make_float2(-1e30f, 0.f);
+    if (tid + i * kMergeThreads >= n_split) mls[i] = make_float2(-1e30f, 0.f);
     m = fmaxf(m, mls[i].x);
   }
 #pragma unroll
