@@ -362,6 +362,24 @@ int std_gemv_ex(const void* x, long long x_row_stride, const void* w, long long 
                 const void* bias, const void* residual, long long residual_row_stride, void* y,
                 long long y_row_stride, int M, int N, int K, int gated, int dtype, void* stream);
 
+/* The q|k|v projection of a decode step fused with std_rope_append (one
+ * launch instead of two): x [n_rows][K] (n_rows <= 4, K <= 4096, a multiple
+ * of 32) times W [(n_q + 2 n_kv) * 128][K] (the q_proj, k_proj, v_proj rows
+ * stacked, modeling_qwen2_5_vl.py:778-780, 798-800) plus bias, each output rounded to
+ * bf16 as F.linear rounds it, then exactly std_rope_append's rotary embedding
+ * and cache append (modeling_qwen2_5_vl.py:690-732, kv_cache.py:54-69): rows
+ * at position pos_dev[0] + pos_offset + r, rotated queries to q_out
+ * [n_q][n_rows][128], rotated keys and the values to cache row len_dev[0] + r
+ * (not written at or past capacity). Outputs equal std_gemv_ex followed by
+ * std_rope_append bit for bit. bf16 only; head_dim 128; the length is not
+ * advanced.
+ */
+int std_qkv_rope_append(const void* x, long long x_row_stride, int n_rows, int K, const void* w,
+                        long long w_row_stride, const void* bias, int n_q, int n_kv, int d, void* q_out,
+                        void* cache_k, void* cache_v, long long cache_head_stride, int capacity,
+                        const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
+                        const float* inv_freq, int dtype, void* stream);
+
 int std_greedy_accept(const void* logits, long long logits_row_stride, int q_rows, int vocab,
                       int dtype, const int32_t* draft, int n_draft, int has_pending,
                       const int32_t* dense_next, int32_t* out,

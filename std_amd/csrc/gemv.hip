@@ -287,6 +287,102 @@ extern "C" size_t std_gemv_workspace_bytes(int M, int N, int K) {
 namespace stdhip {
 namespace {
 
+// The fused q|k|v projection of up to kShortRows decode rows followed by the
+// rotary embedding and the K/V cache append of rope.hip (one launch instead of
+// two). The rotary embedding pairs columns j and j + 64 of a head, so a
+// workgroup owns four pairs of one head -- output columns p..p+3 and
+// p+64..p+67, p = 4 (block % 16), head = block / 16 -- and lanes lg = 0 and 1
+// hold the two halves of the same pairs (exchanged with a lane shuffle). The
+// projection itself is gemv_short_kernel's with eight columns: four waves split
+// K, every weight load of a wave issued at once, the activation slice staged in
+// LDS. The epilogue repeats rope_append_kernel's arithmetic op for op: the
+// projection rounded to bf16 (bias added first), angle = float(pos) *
+// inv_freq[j], cos / sin rounded to bf16, lo = x1 c - x2 s and hi = x2 c + x1 s
+// with each product and the sum rounded. Query heads go to q_out
+// [n_q][M][128]; key heads, rotated, and value heads, as projected, go to cache
+// row len + m of their KV head (rows at or past the capacity are not written).
+struct RopeArgs {
+  bf16_t* q_out;
+  bf16_t* ck;
+  bf16_t* cv;
+  long long chs;                  // cache head stride (elements)
+  int n_q, n_kv, capacity, pos_offset;
+};
+
+__global__ void __launch_bounds__(256)
+gemv_qkv_rope_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
+                     const bf16_t* __restrict__ bias, int M, int K, RopeArgs ra, const int32_t* __restrict__ len_dev,
+                     const int32_t* __restrict__ pos_dev, const float* __restrict__ inv_freq) {
+  constexpr int WK = 4, NS = kShortSteps, HALF = kHeadDim / 2;
+  __shared__ f32x4 red[WK][64];
+  __shared__ __align__(16) bf16_t xs[kShortRows * kShortMaxK];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int head = blockIdx.x / 16, p = (blockIdx.x % 16) * 4;
+  const bool aw = ln < 8;                      // lanes past eight carry zero weight rows
+  const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;
+  const int k_begin = min(K, wave * kw), k_end = min(K, k_begin + kw);
+  const int nsteps = (k_end - k_begin) / 32;   // <= NS (checked on the host)
+  // weight row of lane ln: pair p + (ln & 3), first (ln < 4) or second half
+  const bf16_t* wr = w + (long long)(head * kHeadDim + (ln >> 2 & 1) * HALF + p + (ln & 3)) * w_rs + k_begin + 8 * lg;
+  bf16x8_t a[NS];
+#pragma unroll
+  for (int u = 0; u < NS; ++u)
+    if (u < nsteps) a[u] = aw ? ld16(wr + 32 * u) : bf16x8_t{};
+  const int cpr = (k_end - k_begin) / 8;       // 16-byte chunks per activation row
+  for (int c = lane; c < M * cpr; c += 64) {
+    const int m = c / cpr, kk = k_begin + (c - m * cpr) * 8;
+    *reinterpret_cast<uint4*>(xs + m * K + kk) = *reinterpret_cast<const uint4*>(x + (long long)m * x_rs + kk);
+  }
+  const bool xm = ln < M;
+  const bf16_t* xl = xs + (xm ? ln : 0) * K + k_begin + 8 * lg;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < NS; ++u)
+    if (u < nsteps) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], xm ? ld16(xl + 32 * u) : bf16x8_t{}, acc, 0, 0, 0);
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 t = red[0][lane];
+#pragma unroll
+  for (int i = 1; i < WK; ++i) t += red[i][lane];
+  // lane (ln, lg < 2): row m = ln, pairs p + i, half lg
+  const int half = lg & 1;
+  const int col = head * kHeadDim + half * HALF + p;
+  float v[4], partner[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = round_bf16(bias ? t[i] + to_f32<bf16_t>(bias[col + i]) : t[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(v[i], 16);
+  if (!xm || lg >= 2) return;
+  const int kv_head = head - ra.n_q;
+  bf16_t* dst;
+  if (head < ra.n_q) {
+    dst = ra.q_out + ((long long)head * M + ln) * kHeadDim;
+  } else {
+    const int crow = *len_dev + ln;
+    if (crow < 0 || crow >= ra.capacity) return;
+    dst = (kv_head < ra.n_kv ? ra.ck + (long long)kv_head * ra.chs : ra.cv + (long long)(kv_head - ra.n_kv) * ra.chs) +
+          (long long)crow * kHeadDim;
+  }
+  dst += half * HALF + p;
+  if (kv_head >= ra.n_kv) {                    // value heads: the projection as is
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = from_f32<bf16_t>(v[i]);
+    return;
+  }
+  const int pos = *pos_dev + ra.pos_offset + ln;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float ang = __fmul_rn((float)pos, inv_freq[p + i]);
+    const float c = round_bf16(cosf(ang)), s = round_bf16(sinf(ang));
+    const float x1 = half ? partner[i] : v[i], x2 = half ? v[i] : partner[i];
+    const float r = half ? round_bf16(__fadd_rn(round_bf16(__fmul_rn(x2, c)), round_bf16(__fmul_rn(x1, s))))
+                         : round_bf16(__fadd_rn(round_bf16(__fmul_rn(x1, c)), round_bf16(__fmul_rn(-x2, s))));
+    dst[i] = from_f32<bf16_t>(r);
+  }
+}
+
 // Waves per workgroup (the K split), from kernel durations at one and ten
 // rows on the 7B projection shapes (16-column blocks: q/k/v 288, o and down
 // 224, gate/up 1184 of 2368 stacked, lm_head 9504). The split is chosen from
@@ -364,4 +460,25 @@ extern "C" int std_gemv_ex(const void* x, long long x_row_stride, const void* w,
                            long long y_row_stride, int M, int N, int K, int gated, int dtype, void* stream) {
   return gemv_entry(x, x_row_stride, w, w_row_stride, bias, residual, residual_row_stride, y, y_row_stride, M, N, K,
                     dtype, gated != 0, stream);
+}
+
+extern "C" int std_qkv_rope_append(const void* x, long long x_row_stride, int n_rows, int K, const void* w,
+                                   long long w_row_stride, const void* bias, int n_q, int n_kv, int d, void* q_out,
+                                   void* cache_k, void* cache_v, long long cache_head_stride, int capacity,
+                                   const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
+                                   const float* inv_freq, int dtype, void* stream) {
+  if (!x || !w || !q_out || !cache_k || !cache_v || !len_dev || !pos_dev || !inv_freq) return STD_E_NULL;
+  if (dtype != STD_BF16) return STD_E_DTYPE;
+  if (d != kHeadDim || n_rows < 1 || n_rows > kShortRows || n_q < 1 || n_kv < 1 || n_q % n_kv != 0 || capacity < 1)
+    return STD_E_SHAPE;
+  if (K < 32 || K % 32 != 0 || K > kShortMaxK || x_row_stride < K || w_row_stride < K) return STD_E_SHAPE;
+  if (n_kv > 1 && cache_head_stride < (long long)capacity * kHeadDim) return STD_E_SHAPE;
+  if (!aligned16(x) || !aligned16(w) || (x_row_stride * 2) % 16 || (w_row_stride * 2) % 16) return STD_E_ALIGN;
+  static_assert((kShortMaxK / 4) / 32 <= kShortSteps, "four waves cover K in kShortSteps steps each");
+  const RopeArgs ra{static_cast<bf16_t*>(q_out), static_cast<bf16_t*>(cache_k), static_cast<bf16_t*>(cache_v),
+                    cache_head_stride, n_q, n_kv, capacity, pos_offset};
+  hipLaunchKernelGGL(gemv_qkv_rope_kernel, dim3((n_q + 2 * n_kv) * 16), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const bf16_t*>(w), w_row_stride, static_cast<const bf16_t*>(x), x_row_stride,
+                     static_cast<const bf16_t*>(bias), n_rows, K, ra, len_dev, pos_dev, inv_freq);
+  return launch_status();
 }

@@ -190,12 +190,19 @@ class RandomDecoder:
         p = self.layers[li]
         n = h.shape[1]
         hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
-        qkv = self._linear(h, p["qkv_w"], p["qkv_b"])                        # [1, n, (hq + 2hkv) d]
         controller = self.sparse_controller
         if controller is not None and controller.enabled and n != 1:
             raise RuntimeError("Sparse draft attention currently expects autoregressive q_len=1 calls.")
+        if self.fused_rows(n) and self._hip_rows(h, 1) and h.shape[-1] <= ops.QKV_ROPE_MAX_K:
+            # one bf16 row: the projection, rotary embedding and K/V append in one launch
+            q = ops.qkv_rope_append(h, p["qkv_w"], p["qkv_b"], hq, kc.data, vc.data, state[0:1], state[1:2],
+                                    self.inv_freq)
+            qkv = None
+        else:
+            qkv = self._linear(h, p["qkv_w"], p["qkv_b"])                    # [1, n, (hq + 2hkv) d]
         if self.fused_rows(n):
-            q = ops.rope_append(qkv, hq, kc.data, vc.data, state[0:1], state[1:2], self.inv_freq)
+            if qkv is not None:
+                q = ops.rope_append(qkv, hq, kc.data, vc.data, state[0:1], state[1:2], self.inv_freq)
             if self.capture_text_queries:
                 self.captured_queries[li] = q
             gather = controller.gather_for(li) if controller is not None and controller.enabled else None

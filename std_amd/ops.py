@@ -409,6 +409,49 @@ def rope_append(qkv: torch.Tensor, n_q: int, key_cache: torch.Tensor, value_cach
     return q_out
 
 
+QKV_ROPE_MAX_K = 4096          # qkv_rope_append stages up to this many activations a row in LDS
+
+
+def qkv_rope_append(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], n_q: int,
+                    key_cache: torch.Tensor, value_cache: torch.Tensor, length: torch.Tensor,
+                    position: torch.Tensor, inv_freq: torch.Tensor, pos_offset: int = 0) -> torch.Tensor:
+    """rope_append(linear(x, weight, bias), ...) in one launch for up to four
+    bf16 rows: x [1, n, K] (K <= 4096), weight [(n_q + 2 n_kv) D, K] the
+    stacked q|k|v projection, bias [(n_q + 2 n_kv) D] or None. Same outputs,
+    bit for bit, as the projection followed by rope_append: returns the
+    rotated queries [1, n_q, n, D]; rotated keys and the values go to cache
+    row length[0] + r. The length is not advanced."""
+    dev = _check_device(x, weight, key_cache, value_cache, length, position, inv_freq)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("qkv_rope_append: bf16 only")
+    if x.dim() != 3 or x.shape[0] != 1 or x.stride(2) != 1:
+        raise ValueError(f"x must be [1, n, K] with a contiguous last dim, got {tuple(x.shape)}")
+    n, K = x.shape[1], x.shape[2]
+    _check_cache_view("key_cache", key_cache)
+    _check_cache_view("value_cache", value_cache)
+    if value_cache.shape != key_cache.shape or value_cache.stride(1) != key_cache.stride(1):
+        raise ValueError("key and value caches must share shape and head stride")
+    if key_cache.dtype != x.dtype or value_cache.dtype != x.dtype:
+        raise TypeError("caches must have the x dtype")
+    n_kv = key_cache.shape[1]
+    NW = (n_q + 2 * n_kv) * HEAD_DIM
+    if n_q % n_kv or weight.shape != (NW, K) or weight.stride(1) != 1:
+        raise ValueError(f"weight must be [{NW}, {K}] for {n_q} + 2 x {n_kv} heads")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (NW,) or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous bf16 [{NW}]")
+    _check_dev_scalar("length", length)
+    _check_dev_scalar("position", position)
+    if inv_freq.dtype != torch.float32 or inv_freq.numel() != HEAD_DIM // 2 or not inv_freq.is_contiguous():
+        raise TypeError("inv_freq must be a contiguous float32 tensor of head_dim / 2 entries")
+    q_out = torch.empty(1, n_q, n, HEAD_DIM, dtype=x.dtype, device=dev)
+    _lib.call("std_qkv_rope_append", x.data_ptr(), x.stride(1), n, K, weight.data_ptr(), weight.stride(0),
+              bias.data_ptr() if bias is not None else None, n_q, n_kv, HEAD_DIM, q_out.data_ptr(),
+              key_cache.data_ptr(), value_cache.data_ptr(), key_cache.stride(1), key_cache.shape[2],
+              length.data_ptr(), position.data_ptr(), int(pos_offset), inv_freq.data_ptr(), _lib.STD_BF16,
+              _stream(dev))
+    return q_out
+
+
 def attention_devlen(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
                      length: torch.Tensor, max_kv_len: int, scale: Optional[float] = None,
                      out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -8,7 +8,7 @@ import torch
 
 from oracle import attention as ref_attn
 from oracle import rope as ref_rope
-from std_amd import ops
+from std_amd import _lib, ops
 from tests.gpu_helpers import announce, assert_close, dev
 
 pytestmark = pytest.mark.gpu
@@ -121,3 +121,43 @@ def test_attention_devlen_rejects_length_past_plan_with_nan():
         out = ops.attention_devlen(q, k, k, _scalar(bad), max_kv_len=300)
         torch.cuda.synchronize()
         assert torch.isnan(out.float()).all()
+
+
+@pytest.mark.parametrize("n,K,n_q,n_kv,length,pos,off,cap",
+                         [(1, 3584, 28, 4, 1023, 33000, 0, 1100), (1, 3584, 28, 4, 5, 131000, 7, 64),
+                          (3, 896, 7, 1, 40, 900, 2, 44), (4, 1024, 8, 2, 0, 0, 0, 8),
+                          (2, 3584, 28, 4, 63, 70, 0, 64)])
+def test_qkv_rope_append_equals_projection_then_rope_append(n, K, n_q, n_kv, length, pos, off, cap):
+    """The fused projection + rotary + append against the projection (HIP
+    GEMV with bias) followed by rope_append: queries and both caches equal
+    bit for bit, including rows at or past the capacity (not written: the
+    last case's second row)."""
+    announce(f"qkv_rope_append n={n} K={K} heads={n_q}/{n_kv} len={length} pos={pos}+{off} cap={cap}")
+    g = torch.Generator(device=dev()).manual_seed(n * 1000 + K + length)
+    NW = (n_q + 2 * n_kv) * D
+    x = (torch.randn(1, n, K, generator=g, device=dev()) * 2).to(torch.bfloat16)
+    w = (torch.randn(NW, K, generator=g, device=dev()) * 0.03).to(torch.bfloat16)
+    b = (torch.randn(NW, generator=g, device=dev()) * 0.5).to(torch.bfloat16)
+    inv = torch.from_numpy(ref_rope.inv_freq(1e6, D)).to(dev())
+    caches = [torch.full((1, n_kv, cap, D), float("nan"), dtype=torch.bfloat16, device=dev()) for _ in range(4)]
+    q = ops.qkv_rope_append(x, w, b, n_q, caches[0], caches[1], _scalar(length), _scalar(pos), inv, pos_offset=off)
+    want = ops.rope_append(ops.linear(x, w, b), n_q, caches[2], caches[3], _scalar(length), _scalar(pos), inv,
+                           pos_offset=off)
+    torch.cuda.synchronize()
+    assert q.shape == (1, n_q, n, D) and torch.equal(q, want)
+    for got, ref in ((caches[0], caches[2]), (caches[1], caches[3])):
+        assert torch.equal(got.nan_to_num(7.0), ref.nan_to_num(7.0))
+
+
+def test_qkv_rope_append_rejects_bad_arguments():
+    announce("qkv_rope_append host-side validation")
+    x = torch.zeros(1, 5, 3584, dtype=torch.bfloat16, device=dev())
+    w = torch.zeros(36 * D, 3584, dtype=torch.bfloat16, device=dev())
+    kc = torch.zeros(1, NKV, 64, D, dtype=torch.bfloat16, device=dev())
+    inv = torch.from_numpy(ref_rope.inv_freq(1e6, D)).to(dev())
+    with pytest.raises(_lib.StdHipError):            # five rows
+        ops.qkv_rope_append(x, w, None, NQ, kc, kc.clone(), _scalar(0), _scalar(0), inv)
+    with pytest.raises(ValueError):                 # weight rows do not match the heads
+        ops.qkv_rope_append(x[:, :1], w[:-D], None, NQ, kc, kc.clone(), _scalar(0), _scalar(0), inv)
+    with pytest.raises(TypeError):
+        ops.qkv_rope_append(x[:, :1].float(), w, None, NQ, kc, kc.clone(), _scalar(0), _scalar(0), inv)
