@@ -371,14 +371,17 @@ int std_gemv_ex(const void* x, long long x_row_stride, const void* w, long long 
  * at position pos_dev[0] + pos_offset + r, rotated queries to q_out
  * [n_q][n_rows][128], rotated keys and the values to cache row len_dev[0] + r
  * (not written at or past capacity). Outputs equal std_gemv_ex followed by
- * std_rope_append bit for bit. bf16 only; head_dim 128; the length is not
- * advanced.
+ * std_rope_append bit for bit. With norm_weight (not NULL; one row, K <=
+ * 3584) x is the decoder layer's input before its input_layernorm
+ * (modeling_qwen2_5_vl.py:1202) and the launch normalises it first, equal to
+ * std_rms_norm(x, norm_weight, eps) bit for bit. bf16 only; head_dim 128; the
+ * length is not advanced.
  */
 int std_qkv_rope_append(const void* x, long long x_row_stride, int n_rows, int K, const void* w,
                         long long w_row_stride, const void* bias, int n_q, int n_kv, int d, void* q_out,
                         void* cache_k, void* cache_v, long long cache_head_stride, int capacity,
                         const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
-                        const float* inv_freq, int dtype, void* stream);
+                        const float* inv_freq, const void* norm_weight, float eps, int dtype, void* stream);
 
 int std_greedy_accept(const void* logits, long long logits_row_stride, int q_rows, int vocab,
                       int dtype, const int32_t* draft, int n_draft, int has_pending,

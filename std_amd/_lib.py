@@ -65,7 +65,7 @@ SIGNATURES = {
                             c_longlong, c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "std_qkv_rope_append": (c_int, [c_void_p, c_longlong, c_int, c_int, c_void_p, c_longlong, c_void_p, c_int, c_int,
                                     c_int, c_void_p, c_void_p, c_void_p, c_longlong, c_int, c_void_p, c_void_p, c_int,
-                                    c_void_p, c_int, c_void_p]),
+                                    c_void_p, c_void_p, c_float, c_int, c_void_p]),
     "std_argmax_rows": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "std_rms_norm": (c_int, [c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_int, c_int, c_float, c_int,
                              c_void_p]),

@@ -132,15 +132,11 @@ argmax_final_kernel(const uint2* __restrict__ part, int n_blocks, long long* __r
 // this kernel's lane/wave order). No global staging, so it is safe to
 // capture in a HIP graph.
 //
-// Thread t owns elements t, t + 256, t + 512, ... and adds their squares in
-// that order. A row of up to 256 * kRmsBatch elements (3584: 14 a thread) is
-// read with every load of x and of the weights issued before the first add --
-// one memory round trip -- and kept in registers for the scaling pass; wider
-// rows are read kRmsBatch elements a thread at a time, twice. Elements past
-// the row re-read the last one and are never used: a load under a condition
-// would compile to a branch that waits for it before issuing the next.
-constexpr int kRmsBatch = 16;
-
+// The row statistic follows the order of the rms_* helpers. A row of up to
+// kRmsMaxOneBatch elements (3584: 14 a thread) is read with every load of x
+// and of the weights issued before the first add -- one memory round trip --
+// and kept in registers for the scaling pass; wider rows are read
+// kRmsBatch elements a thread at a time, twice.
 template <typename T>
 __global__ void __launch_bounds__(256)
 rms_norm_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ out, int hidden, long long x_rs,
@@ -150,51 +146,33 @@ rms_norm_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __restrict_
   const T* xr = x + (long long)r * x_rs;
   T* orow = out + (long long)r * o_rs;
   T xv[kRmsBatch], wv[kRmsBatch];
-  auto load = [&](const T* src, T* dst, int i0) {
-#pragma unroll
-    for (int j = 0; j < kRmsBatch; ++j) dst[j] = src[min(i0 + tid + 256 * j, hidden - 1)];
-  };
-  auto add_squares = [&](float ss, int i0) {
-#pragma unroll
-    for (int j = 0; j < kRmsBatch; ++j)
-      if (i0 + tid + 256 * j < hidden) {
-        const float v = to_f32<T>(xv[j]);
-        ss = __fadd_rn(ss, __fmul_rn(v, v));
-      }
-    return ss;
+  auto inv_rms = [&](float ss) {
+    ss = rms_wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    return rms_inv(red, hidden, eps);
   };
   auto scale = [&](float inv, int i0) {
 #pragma unroll
     for (int j = 0; j < kRmsBatch; ++j) {
       const int i = i0 + tid + 256 * j;
-      if (i < hidden) {
-        const float n = to_f32<T>(from_f32<T>(__fmul_rn(to_f32<T>(xv[j]), inv)));
-        orow[i] = from_f32<T>(__fmul_rn(to_f32<T>(wv[j]), n));
-      }
+      if (i < hidden) orow[i] = rms_scale<T>(xv[j], wv[j], inv);
     }
   };
-  auto inv_rms = [&](float ss) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    const float mean = ((red[0] + red[1]) + (red[2] + red[3])) * (1.0f / (float)hidden);
-    return rsqrtf(__fadd_rn(mean, eps));
-  };
-  if (hidden <= 256 * kRmsBatch) {
-    load(xr, xv, 0);
-    load(w, wv, 0);
-    scale(inv_rms(add_squares(0.f, 0)), 0);
+  if (hidden <= kRmsMaxOneBatch) {
+    rms_load<T>(xr, xv, 0, hidden, tid);
+    rms_load<T>(w, wv, 0, hidden, tid);
+    scale(inv_rms(rms_add_squares<T>(0.f, xv, 0, hidden, tid)), 0);
   } else {
     float ss = 0.f;
-    for (int i0 = 0; i0 < hidden; i0 += 256 * kRmsBatch) {
-      load(xr, xv, i0);
-      ss = add_squares(ss, i0);
+    for (int i0 = 0; i0 < hidden; i0 += kRmsMaxOneBatch) {
+      rms_load<T>(xr, xv, i0, hidden, tid);
+      ss = rms_add_squares<T>(ss, xv, i0, hidden, tid);
     }
     const float inv = inv_rms(ss);
-    for (int i0 = 0; i0 < hidden; i0 += 256 * kRmsBatch) {
-      load(xr, xv, i0);
-      load(w, wv, i0);
+    for (int i0 = 0; i0 < hidden; i0 += kRmsMaxOneBatch) {
+      rms_load<T>(xr, xv, i0, hidden, tid);
+      rms_load<T>(w, wv, i0, hidden, tid);
       scale(inv, i0);
     }
   }

@@ -42,6 +42,54 @@ template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// RMSNorm row statistic (modeling_qwen2_5_vl.py:192-197) in one fixed order,
+// shared by the norm kernel and the projection that normalises its own input:
+// over a block of 256 threads, thread t adds the squares of elements t,
+// t + 256, t + 512, ... of the row in that order (fp32, each product and sum
+// rounded), each wave adds its 64 partials by an xor butterfly, and the four
+// wave sums combine as ((w0 + w1) + (w2 + w3)).
+constexpr int kRmsBatch = 16;                  // elements a thread loads at once
+constexpr int kRmsMaxOneBatch = 256 * kRmsBatch;
+
+// This thread's kRmsBatch elements of a row of n from element i0; elements
+// past the row re-read the last one and must not be used (a load under a
+// condition would compile to a branch that waits for it before the next).
+template <typename T>
+__device__ __forceinline__ void rms_load(const T* __restrict__ src, T* dst, int i0, int n, int tid) {
+#pragma unroll
+  for (int j = 0; j < kRmsBatch; ++j) dst[j] = src[min(i0 + tid + 256 * j, n - 1)];
+}
+
+template <typename T>
+__device__ __forceinline__ float rms_add_squares(float ss, const T* v, int i0, int n, int tid) {
+#pragma unroll
+  for (int j = 0; j < kRmsBatch; ++j)
+    if (i0 + tid + 256 * j < n) {
+      const float f = to_f32<T>(v[j]);
+      ss = __fadd_rn(ss, __fmul_rn(f, f));
+    }
+  return ss;
+}
+
+__device__ __forceinline__ float rms_wave_sum(float ss) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  return ss;
+}
+
+// 1 / sqrt(mean + eps) from the four wave sums.
+__device__ __forceinline__ float rms_inv(const float* wave_sums, int n, float eps) {
+  const float mean = ((wave_sums[0] + wave_sums[1]) + (wave_sums[2] + wave_sums[3])) * (1.0f / (float)n);
+  return rsqrtf(__fadd_rn(mean, eps));
+}
+
+// dtype(weight * dtype(x * inv)), the normalised element as torch rounds it.
+template <typename T>
+__device__ __forceinline__ T rms_scale(T x, T weight, float inv) {
+  const float n = to_f32<T>(from_f32<T>(__fmul_rn(to_f32<T>(x), inv)));
+  return from_f32<T>(__fmul_rn(to_f32<T>(weight), n));
+}
+
 // Status of the most recent launch on this thread (0 or a positive hipError_t).
 inline int launch_status() {
   hipError_t e = hipGetLastError();

@@ -301,6 +301,15 @@ namespace {
 // with each product and the sum rounded. Query heads go to q_out
 // [n_q][M][128]; key heads, rotated, and value heads, as projected, go to cache
 // row len + m of their KV head (rows at or past the capacity are not written).
+//
+// NORM (one row, K <= kQkvNormMaxK): x is the layer's input before its
+// RMSNorm (weight nw): the workgroup forms the row statistic in the order of
+// the rms_* helpers and writes the normalised row -- rms_norm_kernel's output
+// bit for bit -- to LDS, where the MFMAs read it. The weight registers are
+// sized to kQkvNormMaxK / 4 / 32 steps so the kernel keeps three workgroups a CU
+// (all of a 7B q/k/v launch in one wave of workgroups).
+constexpr int kQkvNormMaxK = 3584;
+
 struct RopeArgs {
   bf16_t* q_out;
   bf16_t* ck;
@@ -309,13 +318,22 @@ struct RopeArgs {
   int n_q, n_kv, capacity, pos_offset;
 };
 
-__global__ void __launch_bounds__(256)
+template <bool NORM>
+__global__ void __launch_bounds__(256, 3)    // three waves a SIMD: a 7B q/k/v launch in one wave of workgroups
 gemv_qkv_rope_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
                      const bf16_t* __restrict__ bias, int M, int K, RopeArgs ra, const int32_t* __restrict__ len_dev,
-                     const int32_t* __restrict__ pos_dev, const float* __restrict__ inv_freq) {
-  constexpr int WK = 4, NS = kShortSteps, HALF = kHeadDim / 2;
+                     const int32_t* __restrict__ pos_dev, const float* __restrict__ inv_freq,
+                     const bf16_t* __restrict__ nw, float eps) {
+  constexpr int WK = 4, NS = NORM ? kQkvNormMaxK / 4 / 32 : kShortSteps, HALF = kHeadDim / 2;
+  static_assert(kQkvNormMaxK <= kRmsMaxOneBatch && kQkvNormMaxK % 128 == 0, "one load batch, whole steps");
   __shared__ f32x4 red[WK][64];
   __shared__ __align__(16) bf16_t xs[kShortRows * kShortMaxK];
+  __shared__ float rms_red[4];
+  bf16_t nx[NORM ? kRmsBatch : 1], ng[NORM ? kRmsBatch : 1];
+  if constexpr (NORM) {                        // issued first: the statistic's wait leaves the weights in flight
+    rms_load<bf16_t>(x, nx, 0, K, threadIdx.x);
+    rms_load<bf16_t>(nw, ng, 0, K, threadIdx.x);
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lg = lane >> 4;
   const int head = blockIdx.x / 16, p = (blockIdx.x % 16) * 4;
@@ -329,10 +347,23 @@ gemv_qkv_rope_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t*
 #pragma unroll
   for (int u = 0; u < NS; ++u)
     if (u < nsteps) a[u] = aw ? ld16(wr + 32 * u) : bf16x8_t{};
-  const int cpr = (k_end - k_begin) / 8;       // 16-byte chunks per activation row
-  for (int c = lane; c < M * cpr; c += 64) {
-    const int m = c / cpr, kk = k_begin + (c - m * cpr) * 8;
-    *reinterpret_cast<uint4*>(xs + m * K + kk) = *reinterpret_cast<const uint4*>(x + (long long)m * x_rs + kk);
+  if constexpr (NORM) {
+    const float ss = rms_wave_sum(rms_add_squares<bf16_t>(0.f, nx, 0, K, threadIdx.x));
+    if (lane == 0) rms_red[wave] = ss;
+    __syncthreads();
+    const float inv = rms_inv(rms_red, K, eps);
+#pragma unroll
+    for (int j = 0; j < kRmsBatch; ++j) {
+      const int i = threadIdx.x + 256 * j;
+      if (i < K) xs[i] = rms_scale<bf16_t>(nx[j], ng[j], inv);
+    }
+    __syncthreads();
+  } else {
+    const int cpr = (k_end - k_begin) / 8;     // 16-byte chunks per activation row
+    for (int c = lane; c < M * cpr; c += 64) {
+      const int m = c / cpr, kk = k_begin + (c - m * cpr) * 8;
+      *reinterpret_cast<uint4*>(xs + m * K + kk) = *reinterpret_cast<const uint4*>(x + (long long)m * x_rs + kk);
+    }
   }
   const bool xm = ln < M;
   const bf16_t* xl = xs + (xm ? ln : 0) * K + k_begin + 8 * lg;
@@ -466,8 +497,10 @@ extern "C" int std_qkv_rope_append(const void* x, long long x_row_stride, int n_
                                    long long w_row_stride, const void* bias, int n_q, int n_kv, int d, void* q_out,
                                    void* cache_k, void* cache_v, long long cache_head_stride, int capacity,
                                    const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
-                                   const float* inv_freq, int dtype, void* stream) {
+                                   const float* inv_freq, const void* norm_weight, float eps, int dtype,
+                                   void* stream) {
   if (!x || !w || !q_out || !cache_k || !cache_v || !len_dev || !pos_dev || !inv_freq) return STD_E_NULL;
+  if (norm_weight && (n_rows != 1 || K > kQkvNormMaxK)) return STD_E_SHAPE;
   if (dtype != STD_BF16) return STD_E_DTYPE;
   if (d != kHeadDim || n_rows < 1 || n_rows > kShortRows || n_q < 1 || n_kv < 1 || n_q % n_kv != 0 || capacity < 1)
     return STD_E_SHAPE;
@@ -477,8 +510,10 @@ extern "C" int std_qkv_rope_append(const void* x, long long x_row_stride, int n_
   static_assert((kShortMaxK / 4) / 32 <= kShortSteps, "four waves cover K in kShortSteps steps each");
   const RopeArgs ra{static_cast<bf16_t*>(q_out), static_cast<bf16_t*>(cache_k), static_cast<bf16_t*>(cache_v),
                     cache_head_stride, n_q, n_kv, capacity, pos_offset};
-  hipLaunchKernelGGL(gemv_qkv_rope_kernel, dim3((n_q + 2 * n_kv) * 16), dim3(256), 0, static_cast<hipStream_t>(stream),
+  auto kern = norm_weight ? gemv_qkv_rope_kernel<true> : gemv_qkv_rope_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3((n_q + 2 * n_kv) * 16), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const bf16_t*>(w), w_row_stride, static_cast<const bf16_t*>(x), x_row_stride,
-                     static_cast<const bf16_t*>(bias), n_rows, K, ra, len_dev, pos_dev, inv_freq);
+                     static_cast<const bf16_t*>(bias), n_rows, K, ra, len_dev, pos_dev, inv_freq,
+                     static_cast<const bf16_t*>(norm_weight), eps);
   return launch_status();
 }

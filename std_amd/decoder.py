@@ -183,23 +183,29 @@ class RandomDecoder:
         c = self.config
         return n * (c.num_attention_heads // c.num_key_value_heads) <= MAX_FUSED_ROWS
 
-    def _attention(self, li: int, h: torch.Tensor, cos, sin, kc: KVCache, vc: KVCache,
-                   state: Optional[torch.Tensor], host_lengths: bool, residual: torch.Tensor) -> torch.Tensor:
-        """residual + self-attention block output (o_proj included)."""
+    def _attention(self, li: int, x: torch.Tensor, cos, sin, kc: KVCache, vc: KVCache,
+                   state: Optional[torch.Tensor], host_lengths: bool) -> torch.Tensor:
+        """x + self-attention block output of input_layernorm(x) (o_proj included)."""
         c = self.config
         p = self.layers[li]
-        n = h.shape[1]
+        n, width = x.shape[1], x.shape[-1]
+        residual = x
         hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         controller = self.sparse_controller
         if controller is not None and controller.enabled and n != 1:
             raise RuntimeError("Sparse draft attention currently expects autoregressive q_len=1 calls.")
-        if self.fused_rows(n) and self._hip_rows(h, 1) and h.shape[-1] <= ops.QKV_ROPE_MAX_K:
-            # one bf16 row: the projection, rotary embedding and K/V append in one launch
-            q = ops.qkv_rope_append(h, p["qkv_w"], p["qkv_b"], hq, kc.data, vc.data, state[0:1], state[1:2],
-                                    self.inv_freq)
-            qkv = None
+        qkv = None
+        if self.fused_rows(n) and self._hip_rows(x, 1) and width <= ops.QKV_ROPE_NORM_MAX_K:
+            # one bf16 row: the norm, projection, rotary embedding and K/V append in one launch
+            q = ops.qkv_rope_append(x, p["qkv_w"], p["qkv_b"], hq, kc.data, vc.data, state[0:1], state[1:2],
+                                    self.inv_freq, norm_weight=p["ln1"], eps=c.rms_norm_eps)
         else:
-            qkv = self._linear(h, p["qkv_w"], p["qkv_b"])                    # [1, n, (hq + 2hkv) d]
+            h = self._rms_norm(x, p["ln1"])
+            if self.fused_rows(n) and self._hip_rows(h, 1) and width <= ops.QKV_ROPE_MAX_K:
+                q = ops.qkv_rope_append(h, p["qkv_w"], p["qkv_b"], hq, kc.data, vc.data, state[0:1], state[1:2],
+                                        self.inv_freq)
+            else:
+                qkv = self._linear(h, p["qkv_w"], p["qkv_b"])                # [1, n, (hq + 2hkv) d]
         if self.fused_rows(n):
             if qkv is not None:
                 q = ops.rope_append(qkv, hq, kc.data, vc.data, state[0:1], state[1:2], self.inv_freq)
@@ -281,8 +287,7 @@ class RandomDecoder:
             cos, sin = self._rope(position_ids)
         for li in range(self.config.num_hidden_layers):
             kc, vc = past_key_values[li]
-            x = self._attention(li, self._rms_norm(x, self.layers[li]["ln1"]), cos, sin, kc, vc, step_state,
-                                host_lengths, residual=x)
+            x = self._attention(li, x, cos, sin, kc, vc, step_state, host_lengths)
             x = self._mlp(li, self._rms_norm(x, self.layers[li]["ln2"]), residual=x)
         if not host_lengths:
             ops.len_add(step_state, n)

@@ -410,17 +410,21 @@ def rope_append(qkv: torch.Tensor, n_q: int, key_cache: torch.Tensor, value_cach
 
 
 QKV_ROPE_MAX_K = 4096          # qkv_rope_append stages up to this many activations a row in LDS
+QKV_ROPE_NORM_MAX_K = 3584     # ... and normalises rows up to this width in the same launch
 
 
 def qkv_rope_append(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], n_q: int,
                     key_cache: torch.Tensor, value_cache: torch.Tensor, length: torch.Tensor,
-                    position: torch.Tensor, inv_freq: torch.Tensor, pos_offset: int = 0) -> torch.Tensor:
+                    position: torch.Tensor, inv_freq: torch.Tensor, pos_offset: int = 0,
+                    norm_weight: Optional[torch.Tensor] = None, eps: float = 0.0) -> torch.Tensor:
     """rope_append(linear(x, weight, bias), ...) in one launch for up to four
     bf16 rows: x [1, n, K] (K <= 4096), weight [(n_q + 2 n_kv) D, K] the
     stacked q|k|v projection, bias [(n_q + 2 n_kv) D] or None. Same outputs,
     bit for bit, as the projection followed by rope_append: returns the
     rotated queries [1, n_q, n, D]; rotated keys and the values go to cache
-    row length[0] + r. The length is not advanced."""
+    row length[0] + r. The length is not advanced. With norm_weight (one row,
+    K <= 3584) x is normalised first in the same launch, exactly as
+    rms_norm(x, norm_weight, eps)."""
     dev = _check_device(x, weight, key_cache, value_cache, length, position, inv_freq)
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise TypeError("qkv_rope_append: bf16 only")
@@ -443,12 +447,16 @@ def qkv_rope_append(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.
     _check_dev_scalar("position", position)
     if inv_freq.dtype != torch.float32 or inv_freq.numel() != HEAD_DIM // 2 or not inv_freq.is_contiguous():
         raise TypeError("inv_freq must be a contiguous float32 tensor of head_dim / 2 entries")
+    if norm_weight is not None:
+        _check_device(norm_weight)
+        if norm_weight.dtype != torch.bfloat16 or norm_weight.shape != (K,) or not norm_weight.is_contiguous():
+            raise ValueError(f"norm weight must be a contiguous bf16 [{K}]")
     q_out = torch.empty(1, n_q, n, HEAD_DIM, dtype=x.dtype, device=dev)
     _lib.call("std_qkv_rope_append", x.data_ptr(), x.stride(1), n, K, weight.data_ptr(), weight.stride(0),
               bias.data_ptr() if bias is not None else None, n_q, n_kv, HEAD_DIM, q_out.data_ptr(),
               key_cache.data_ptr(), value_cache.data_ptr(), key_cache.stride(1), key_cache.shape[2],
-              length.data_ptr(), position.data_ptr(), int(pos_offset), inv_freq.data_ptr(), _lib.STD_BF16,
-              _stream(dev))
+              length.data_ptr(), position.data_ptr(), int(pos_offset), inv_freq.data_ptr(),
+              norm_weight.data_ptr() if norm_weight is not None else None, float(eps), _lib.STD_BF16, _stream(dev))
     return q_out
 
 

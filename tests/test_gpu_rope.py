@@ -161,3 +161,39 @@ def test_qkv_rope_append_rejects_bad_arguments():
         ops.qkv_rope_append(x[:, :1], w[:-D], None, NQ, kc, kc.clone(), _scalar(0), _scalar(0), inv)
     with pytest.raises(TypeError):
         ops.qkv_rope_append(x[:, :1].float(), w, None, NQ, kc, kc.clone(), _scalar(0), _scalar(0), inv)
+
+
+@pytest.mark.parametrize("K,n_q,n_kv", [(3584, 28, 4), (896, 7, 1), (1024, 8, 2)])
+def test_qkv_rope_append_with_norm_equals_rms_norm_first(K, n_q, n_kv):
+    """One row with the layer's input RMSNorm in the same launch: equal, bit
+    for bit, to rms_norm followed by the fused projection + rotary + append."""
+    announce(f"qkv_rope_append with norm K={K} heads={n_q}/{n_kv}")
+    g = torch.Generator(device=dev()).manual_seed(K + n_q)
+    NW = (n_q + 2 * n_kv) * D
+    x = (torch.randn(1, 1, K, generator=g, device=dev()) * 3).to(torch.bfloat16)
+    nw = (1 + 0.2 * torch.randn(K, generator=g, device=dev())).to(torch.bfloat16)
+    w = (torch.randn(NW, K, generator=g, device=dev()) * 0.03).to(torch.bfloat16)
+    b = (torch.randn(NW, generator=g, device=dev()) * 0.5).to(torch.bfloat16)
+    inv = torch.from_numpy(ref_rope.inv_freq(1e6, D)).to(dev())
+    caches = [torch.full((1, n_kv, 40, D), float("nan"), dtype=torch.bfloat16, device=dev()) for _ in range(4)]
+    q = ops.qkv_rope_append(x, w, b, n_q, caches[0], caches[1], _scalar(17), _scalar(5000), inv,
+                            norm_weight=nw, eps=1e-6)
+    want = ops.qkv_rope_append(ops.rms_norm(x, nw, 1e-6), w, b, n_q, caches[2], caches[3], _scalar(17),
+                               _scalar(5000), inv)
+    torch.cuda.synchronize()
+    assert torch.equal(q, want)
+    for got, ref in ((caches[0], caches[2]), (caches[1], caches[3])):
+        assert torch.equal(got.nan_to_num(7.0), ref.nan_to_num(7.0))
+
+
+def test_qkv_rope_append_norm_limits():
+    """The in-launch norm takes one row of at most 3584 elements."""
+    announce("qkv_rope_append norm: row and width limits")
+    inv = torch.from_numpy(ref_rope.inv_freq(1e6, D)).to(dev())
+    kc = torch.zeros(1, NKV, 64, D, dtype=torch.bfloat16, device=dev())
+    for n, K in ((2, 3584), (1, 4096)):
+        x = torch.zeros(1, n, K, dtype=torch.bfloat16, device=dev())
+        w = torch.zeros(36 * D, K, dtype=torch.bfloat16, device=dev())
+        with pytest.raises(_lib.StdHipError):
+            ops.qkv_rope_append(x, w, None, NQ, kc, kc.clone(), _scalar(0), _scalar(0), inv,
+                                norm_weight=torch.ones(K, dtype=torch.bfloat16, device=dev()), eps=1e-6)
