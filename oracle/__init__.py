@@ -4,8 +4,8 @@ A numpy (fp64) restatement of the reference's algorithm for each function on
 the path, written from the reference files (cited per function), never by
 importing them. Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
-checker or as the timed CPU baseline. The product path (``std_amd``) never
-imports it and has no CPU fallback.
+reference results are compared against or as the timed CPU baseline. The
+product path (``std_amd``) never imports it and has no CPU fallback.
 
 Modules:
   attention  draft GQA decode (gqa_sdpa) and offset-causal verify (math SDPA)
