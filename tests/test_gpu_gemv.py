@@ -101,3 +101,29 @@ def test_gated_linear_with_residual_and_validation():
         ops.gated_linear(x, w[:-1])                      # odd row count: not a gate/up stack
     with pytest.raises(ValueError):
         ops.linear(x, w, residual=r)                     # residual shaped like a different output
+
+
+@pytest.mark.parametrize("M,N,K,gated", [(1, 3584, 512, False), (1, 3584, 1024, False), (2, 3584, 1536, False),
+                                          (1, 3584, 2560, False), (1, 2048, 1024, True), (3, 2048, 1536, True),
+                                          (1, 1024, 768, True), (4, 3000, 2048, False)])
+def test_gemv_ring_with_few_steps_per_wave(M, N, K, gated):
+    """The register ring when a wave has fewer steps than the ring has slots
+    (1-3 steps: the prologue's clamped loads and no full ring iteration) or
+    one iteration plus a remainder (5), plain and gated, against a float32
+    reference; repeated calls are bit-identical."""
+    announce(f"gemv ring few steps M={M} N={N} K={K} gated={gated}")
+    g = torch.Generator(device=dev()).manual_seed(M + N + K + int(gated))
+    x = torch.randn(M, K, generator=g, device=dev()).to(torch.bfloat16)
+    NW = 2 * N if gated else N
+    w = (torch.randn(NW, K, generator=g, device=dev()) * 0.02).to(torch.bfloat16)
+    if gated:
+        got = ops.gated_linear(x, w)
+        ref = F.silu(F.linear(x.float(), w[:N].float())) * F.linear(x.float(), w[N:].float())
+        again = ops.gated_linear(x, w)
+    else:
+        got = ops.linear(x, w)
+        ref = F.linear(x.float(), w.float())
+        again = ops.linear(x, w)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(got.float(), ref, rtol=2e-2, atol=2e-3)
+    assert torch.equal(got, again)
