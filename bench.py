@@ -39,10 +39,11 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c4", choices=["c2", "c3", "c4", "c5", "gemv"],
+    ap.add_argument("--workload", default="c4", choices=["c2", "c3", "c4", "c5", "gemv", "stream"],
                     help="c2-c4: attention hot path at 16k/64k/128k context (default c4, the headline); "
                          "c5: end-to-end STD vs dense AR decode on a random-init Qwen2.5-VL-7B-shaped decoder; "
-                         "gemv: the decoder's weight-streaming projections at one and ten rows")
+                         "gemv: the decoder's weight-streaming projections at one and ten rows; "
+                         "stream: the HBM streaming-read ceiling in the attention kernels' access patterns")
     ap.add_argument("--new-tokens", type=int, default=128, help="c5: tokens to decode")
     ap.add_argument("--eager", action="store_true",
                     help="c5: run the decode loops eagerly (host lengths) instead of replaying captured HIP graphs")
@@ -115,6 +116,9 @@ def main():
         return
     if args.workload == "gemv":
         run_gemv(args)
+        return
+    if args.workload == "stream":
+        run_stream(args)
         return
     w = WORKLOADS[args.workload]
     if args.pmc_run:
@@ -574,6 +578,67 @@ def run_gemv(args) -> None:
                       "config": {"workload": "gemv: Qwen2.5-VL-7B projections (hidden 3584, SwiGLU 18944, vocab "
                                              "152064) at 1 and 10 rows"},
                       "results": results}))
+
+
+def run_stream(args) -> None:
+    """Streaming-read ceiling: 256 MiB reads through std_stream_read in the
+    access patterns of the attention kernels (vector loads or the LDS DMA ring;
+    one contiguous chunk per workgroup or tiles dealt round-robin) at several
+    workgroup counts. Eight distinct 256 MiB buffers (2 GiB, eight times the
+    256 MB last-level cache) are read in turn, 16 reads captured in one HIP
+    graph; the median per-read time over replays is reported (events on the
+    stream the reads run on). Prints one JSON line; `best` is the ceiling the
+    attention kernels are compared against."""
+    import torch
+
+    from std_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    nbytes = 256 << 20
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(8)]
+    sink = torch.zeros(65536, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    reads = 16
+    results = []
+    configs = [(m, n) for m in (0, 1) for n in (256, 512, 1024, 2048, 4096)]
+    configs += [(m, n) for m in (2, 3, 4, 5) for n in (256, 512)]
+    for mode, n_wg in configs:
+        def body():
+            for i in range(reads):
+                ops.stream_read(bufs[i % len(bufs)], mode, n_wg, sink)
+        body()
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            body()
+        stream.wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            body()
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(max(5, args.steps // 2)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / reads)
+        us = statistics.median(times)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        results.append({"mode": mode, "pattern": ops.STREAM_MODES[mode], "workgroups": n_wg, "us_per_256MiB": round(us, 2),
+                        "GB_s": round(gbps, 1), "pct_of_8TB_s": round(100 * gbps / HBM_PEAK_GBPS, 1)})
+        log(f"stream mode {mode} wg {n_wg}: {us:.2f} us, {gbps:.0f} GB/s")
+        del graph
+    best = max(results, key=lambda r: r["GB_s"])
+    print(json.dumps({"metric": "HBM streaming-read ceiling (256 MiB reads, graph-replayed)", "value": best["GB_s"],
+                      "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "u8", "data": "synthetic",
+                      "config": {"workload": "stream: 256 MiB reads over 8 distinct buffers"},
+                      "best": best, "results": results}))
 
 
 def cpu_baseline(w, L):

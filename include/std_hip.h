@@ -389,6 +389,21 @@ int std_greedy_accept(const void* logits, long long logits_row_stride, int q_row
                       int32_t* rollback_lens, int n_lens,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Streaming-read ceiling (measurement helper; no counterpart in the
+ * reference, which records no kernel measurement). Reads `bytes` of device
+ * memory at src once and writes at most one word per workgroup to sink
+ * (n_workgroups words; in practice never). bytes: a multiple of 32 KiB.
+ *   mode 0/1: 256-thread workgroups issuing eight 16-byte vector loads per
+ *             thread per 32 KiB tile;
+ *   mode 2/3: the verify kernel's LDS DMA ring (eight waves, two tiles in
+ *             flight), each tile 16 KiB from either half of the buffer;
+ *   mode 4/5: the decode key split's ring (four waves, three in flight).
+ * Even modes give each workgroup one contiguous chunk (the tile count must
+ * divide by n_workgroups), odd modes deal tiles round-robin.
+ * ------------------------------------------------------------------------ */
+int std_stream_read(const void* src, size_t bytes, int mode, int n_workgroups, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,7 @@ SIGNATURES = {
     "std_attn_devlen": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_int,
                                 c_longlong, c_longlong, c_float, c_int, c_void_p, c_size_t, c_void_p]),
     "std_greedy_accept_workspace_bytes": (c_size_t, [c_int, c_int]),
+    "std_stream_read": (c_int, [c_void_p, c_size_t, c_int, c_int, c_void_p, c_void_p]),
     "std_greedy_accept": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_int, c_int, c_void_p,
                                   c_void_p, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
 }

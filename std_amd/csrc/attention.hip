@@ -33,6 +33,7 @@
 #include <climits>
 
 #include "common.h"
+#include "lds_dma.h"
 
 namespace stdhip {
 namespace {
@@ -102,9 +103,15 @@ WsLayout ws_layout(int n_kv, int rows, const SplitPlan& p) {
   return l;
 }
 
-__device__ __forceinline__ int split_tile(int split, int ntiles, int n_split) {
-  return (int)((long long)split * ntiles / n_split);
+// Tiles are dealt to the splits of a head round-robin: split s streams tiles
+// s, s + n_split, s + 2 n_split, ... so that at every step the workgroups of a
+// head read neighbouring 16 KiB tiles, spread over the HBM channels. (One
+// contiguous chunk per split puts 256 workgroups 512 KiB apart at 128k context;
+// the same DMA ring then reads 10 % slower.)
+__device__ __forceinline__ int split_ntiles(int split, int ntiles_total, int n_split) {
+  return (ntiles_total - split + n_split - 1) / n_split;   // >= 0: split < n_split
 }
+__device__ __forceinline__ int tile_key0(int split, int tt, int n_split) { return (split + tt * n_split) * TK; }
 
 // Device-length launch: the cache holds *len_dev rows plus this step's q_len
 // new rows, and the grid was planned for kv_len (the launch's maximum). A
@@ -119,19 +126,21 @@ __device__ __forceinline__ void device_length(const int32_t* len_dev, int q_len,
 }
 
 // Fused append: cache rows [kv_len - n_new, kv_len) receive the n_new new
-// rows (new_*[g][r], strides in elements). Each workgroup writes the rows that
-// fall inside its own key range, before it reads that range (the caller puts a
-// barrier between the two), so no other workgroup depends on these writes.
+// rows (new_*[g][r], strides in elements). Each workgroup writes the rows of
+// the tiles it streams, before it reads them (the caller puts a barrier
+// between the two), so no other workgroup depends on these writes.
 template <typename T>
 __device__ void append_rows(T* __restrict__ kh, T* __restrict__ vh, const T* __restrict__ nk,
                             const T* __restrict__ nv, long long n_hs, long long n_rs, int g, int n_new, int kv_len,
-                            int key_begin, int key_end, int nthreads) {
+                            int split, int n_split, int nthreads) {
   constexpr int EPC = 16 / (int)sizeof(T);
   constexpr int CPR = D / EPC;
-  const int first = max(kv_len - n_new, key_begin), last = min(kv_len, key_end);
-  for (int idx = threadIdx.x; idx < (last - first) * CPR; idx += nthreads) {
+  if (kv_len < n_new) return;
+  const int first = kv_len - n_new;
+  for (int idx = threadIdx.x; idx < n_new * CPR; idx += nthreads) {
     const int row = first + idx / CPR, col = idx % CPR;
-    const long long src = (long long)g * n_hs + (long long)(row - (kv_len - n_new)) * n_rs + col * EPC;
+    if ((row / TK) % n_split != split) continue;        // another split streams this tile
+    const long long src = (long long)g * n_hs + (long long)(row - first) * n_rs + col * EPC;
     const uint4 k4 = *reinterpret_cast<const uint4*>(nk + src);
     const uint4 v4 = *reinterpret_cast<const uint4*>(nv + src);
     *reinterpret_cast<uint4*>(kh + (long long)row * D + col * EPC) = k4;
@@ -280,66 +289,6 @@ typedef short i16x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ int swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
 __device__ __forceinline__ int sw_off(int row, int chunk) { return row * ROWB + ((chunk ^ swz(row)) << 4); }
 
-// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory
-// operations of this wave are outstanding, leaving the other counters alone.
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-// One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from
-// sbase + voff (a wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane
-// byte offset, the global saddr form) to LDS byte lds_base + 16 i. Issued through inline asm on purpose:
-// the compiler's own LDS-DMA tracking cannot tell the ring stages apart and
-// would put s_waitcnt vmcnt(0) before every LDS read, draining the whole
-// prefetch each tile. Completion is instead ordered explicitly by
-// wait_vm_ahead (vmcnt) followed by a workgroup barrier before any wave
-// reads the stage; the "memory" clobber keeps the compiler from moving LDS
-// accesses across the issue. The compiler inserts no hazard wait states for
-// inline asm, so the asm carries its own: s_nop 4 (5 wait states) covers both
-// the M0 write before an LDS DMA and an SGPR operand written by a VALU
-// instruction (v_readfirstlane) shortly before a VMEM instruction reads it.
-__device__ __forceinline__ void lds_dma16_sbase(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  // readfirstlane pins the wave-uniform operands to SGPRs even where the
-  // compiler cannot prove them uniform (it folds away when they already are).
-  const uint64_t b = reinterpret_cast<uint64_t>(sbase);
-  // (readfirstlane returns int: widen through uint32_t, never sign-extend.)
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
-  const uint64_t base = static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
-  const uint32_t lds = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lds_base));
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(voff), "s"(base), "s"(lds)
-               : "memory", "m0");
-}
-
-// The same copy from a per-lane 64-bit address (gathered rows).
-__device__ __forceinline__ void lds_dma16_vaddr(const void* addr, uint32_t lds_base) {
-  const uint32_t lds = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lds_base));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(addr), "s"(lds) : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  typedef const __attribute__((address_space(3))) char* lds_cptr;
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr)(p)));
-}
-
-// Workgroup barrier without the memory fence of __syncthreads (which would
-// wait for every outstanding load); the empty asm statements keep the
-// compiler from moving LDS accesses across it.
-__device__ __forceinline__ void wg_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// Wait until the tile `ahead` tiles before the newest issued one has landed
-// (each tile is `per_tile` DMA instructions per wave).
-template <int PER_TILE>
-__device__ __forceinline__ void wait_vm_ahead(int ahead) {
-  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * PER_TILE));
-  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(PER_TILE));
-  else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-}
-
 // Four floats -> four bf16 (RNE); the two-wide conversions compile to
 // v_cvt_pk_bf16_f32.
 __device__ __forceinline__ i16x4 pack_bf16x4(float a, float b, float c, float d) {
@@ -423,20 +372,17 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     }
   }
   if (len_dev != nullptr) device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
-  const int t_begin = split_tile(split, ntiles_total, n_split);
-  const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
-  const int key_begin = t_begin * TK;
-  const int key_end = min(kv_len, key_begin + ntiles * TK);
+  const int ntiles = split_ntiles(split, ntiles_total, n_split);
   bf16_t* kh = kc + (long long)g * k_hs;
   bf16_t* vh = vc + (long long)g * v_hs;
   if (n_new > 0) {
-    append_rows<bf16_t>(kh, vh, new_k, new_v, n_hs, n_rs, g, n_new, kv_len, key_begin, key_end, C::kThreads);
+    append_rows<bf16_t>(kh, vh, new_k, new_v, n_hs, n_rs, g, n_new, kv_len, split, n_split, C::kThreads);
     __syncthreads();
   }
 
   // Each wave DMAs kSegsPerWave 1 KiB segments (4 rows) of K and of V per
   // tile. Lane l fills row 4*seg + l/16 at physical chunk l%16, i.e. logical
-  // chunk (l%16) ^ swz(row). Rows past the split's last key re-read that key
+  // chunk (l%16) ^ swz(row). Rows past the cache's last key re-read that key
   // (their scores are masked), so no read leaves the valid range.
   int dma_row[C::kSegsPerWave], dma_chunk[C::kSegsPerWave];
 #pragma unroll
@@ -446,8 +392,8 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     dma_chunk[j] = ((lane & 15) ^ swz(dma_row[j])) * 16;
   }
   auto issue = [&](int tt, char* stage) {
-    const int key0 = key_begin + tt * TK;
-    const int last = key_end - 1 - key0;               // wave-uniform
+    const int key0 = tile_key0(split, tt, n_split);
+    const int last = min(kv_len - key0, TK) - 1;       // wave-uniform
     if constexpr (GA) {
       static_assert(NT == 1, "gathered keys serve the single-row decode");
       if (key0 < ga.n_idx) {                             // wave-uniform: a tile with gathered keys
@@ -475,7 +421,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
         }
         const char* gkh = reinterpret_cast<const char*>(ga.k + g * ga.k_hs);
         const char* gvh = reinterpret_cast<const char*>(ga.v + g * ga.v_hs);
-        // Rows past the split's last key re-read that key from where it really
+        // Rows past the cache's last key re-read that key from where it really
         // lives (a gathered dense row or an own-cache row), as the compacted
         // cache would: own-cache rows below n_idx are never written.
         const int klast = key0 + last;
@@ -586,7 +532,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   // reads) and the P^T operand (the lane's own scores).
   auto softmax_pv = [&](int tt, const char* st, f32x4* s) {
     const char* Vs = st + TILEB;
-    const int tile_base = key_begin + tt * TK;
+    const int tile_base = tile_key0(split, tt, n_split);
     bf16x8 vf[2][8];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -603,13 +549,13 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[j][i] *= scale_log2;
-    if (tile_base + TK > key_end || tile_base + TK - 1 > causal_off) {   // wave-uniform
+    if (tile_base + TK > kv_len || tile_base + TK - 1 > causal_off) {   // wave-uniform
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = tile_base + 16 * j + 4 * lg + i;
-          s[j][i] = (key < key_end && key <= lim) ? s[j][i] : -INFINITY;
+          s[j][i] = (key < kv_len && key <= lim) ? s[j][i] : -INFINITY;
         }
     }
     // Per-lane max against the running max; the running max is raised
@@ -677,10 +623,11 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) sc[i] *= scale_log2;
-    const int key0 = key_begin + tt * TK + 16 * ks_sub + 4 * lg;
-    if (key_begin + tt * TK + TK > key_end || key_begin + tt * TK + TK - 1 > causal_off) {   // wave-uniform
+    const int tile_base = tile_key0(split, tt, n_split);
+    const int key0 = tile_base + 16 * ks_sub + 4 * lg;
+    if (tile_base + TK > kv_len || tile_base + TK - 1 > causal_off) {   // wave-uniform
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] = (key0 + i < key_end && key0 + i <= lim) ? sc[i] : -INFINITY;
+      for (int i = 0; i < 4; ++i) sc[i] = (key0 + i < kv_len && key0 + i <= lim) ? sc[i] : -INFINITY;
     }
     const float lm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     if (__ballot(lm > m_run + kRescaleSlack)) {
@@ -905,14 +852,11 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
     }
   }
   if (len_dev != nullptr) device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
-  const int t_begin = split_tile(split, ntiles_total, n_split);
-  const int ntiles = split_tile(split + 1, ntiles_total, n_split) - t_begin;
-  const int key_begin = t_begin * TK;
-  const int key_end = min(kv_len, key_begin + ntiles * TK);
+  const int ntiles = split_ntiles(split, ntiles_total, n_split);
   float* kh = kc + (long long)g * k_hs;
   float* vh = vc + (long long)g * v_hs;
   if (n_new > 0) {
-    append_rows<float>(kh, vh, new_k, new_v, n_hs, n_rs, g, n_new, kv_len, key_begin, key_end, NTHREADS);
+    append_rows<float>(kh, vh, new_k, new_v, n_hs, n_rs, g, n_new, kv_len, split, n_split, NTHREADS);
     __syncthreads();
   }
 
@@ -943,13 +887,13 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
 
   uint4 kreg[CPT], vreg[CPT];
   auto gload = [&](int t) {
-    const int base = key_begin + t * TK;
+    const int base = tile_key0(split, t, n_split);
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       const int c = tid + j * NTHREADS;
       const int row = c / CPR, col = c - row * CPR;
       const int key = base + row;
-      if (key < key_end) {
+      if (key < kv_len) {
         kreg[j] = *reinterpret_cast<const uint4*>(kh + (long long)key * D + col * 4);
         vreg[j] = *reinterpret_cast<const uint4*>(vh + (long long)key * D + col * 4);
       } else {
@@ -978,8 +922,8 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
     if (t + 1 < ntiles) gload(t + 1);
     const float* Kt = Ks + buf * S::kTileElems;
     const float* Vt = Vs + buf * S::kTileElems;
-    const int tile_base = key_begin + t * TK;
-    const bool need_mask = (tile_base + TK > key_end) || (tile_base + TK - 1 > causal_off);
+    const int tile_base = tile_key0(split, t, n_split);
+    const bool need_mask = (tile_base + TK > kv_len) || (tile_base + TK - 1 > causal_off);
     typename F::KFrag kf;
     typename F::VFrag vf;
     F::load_k(kf, Kt + (w * 16 + ln) * LROW, lg);
@@ -995,7 +939,7 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = key0 + i;
-          if (key >= key_end || key > lim[rt]) sv[i] = -INFINITY;
+          if (key >= kv_len || key > lim[rt]) sv[i] = -INFINITY;
         }
       }
       float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));

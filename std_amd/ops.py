@@ -710,3 +710,23 @@ def greedy_accept(logits: torch.Tensor, draft: torch.Tensor, has_pending: bool,
               n_draft, 1 if has_pending else 0, dense_next.data_ptr() if dense_next is not None else None,
               out.data_ptr(), rollback_lengths.data_ptr() if n_lens else None, n_lens, ws_ptr, ws_bytes, _stream(dev))
     return out
+
+
+STREAM_MODES = {
+    0: "vector loads, contiguous chunk per workgroup",
+    1: "vector loads, tiles round-robin",
+    2: "LDS DMA ring (verify schedule: 8 waves, 2 tiles in flight), contiguous chunk per workgroup",
+    3: "LDS DMA ring (verify schedule), tiles round-robin",
+    4: "LDS DMA ring (decode key split: 4 waves, 3 tiles in flight), contiguous chunk per workgroup",
+    5: "LDS DMA ring (decode key split), tiles round-robin",
+}
+
+
+def stream_read(buf: torch.Tensor, mode: int, n_workgroups: int, sink: torch.Tensor) -> None:
+    """Read all of buf once with the streaming-ceiling kernel (a measurement
+    helper: nothing is computed). sink: int32, at least n_workgroups words."""
+    dev = _check_device(buf, sink)
+    if not buf.is_contiguous() or not sink.is_contiguous() or sink.numel() < n_workgroups:
+        raise ValueError("buf and sink must be contiguous; sink needs n_workgroups words")
+    nbytes = buf.numel() * buf.element_size()
+    _lib.call("std_stream_read", buf.data_ptr(), nbytes, int(mode), int(n_workgroups), sink.data_ptr(), _stream(dev))
