@@ -12,7 +12,9 @@
  * memory: scratch space is a caller-owned workspace whose size is queried up
  * front with the matching *_workspace_bytes() function; its contents need no
  * initialisation, and calls that can run concurrently need distinct
- * workspaces. No call synchronizes the device. The library keeps no mutable
+ * workspaces. No call synchronizes the device. Apart from
+ * std_gqa_decode_noalloc (its own device scratch array per GPU and the
+ * lock-guarded table of those arrays' addresses) the library keeps no mutable
  * global state, so distinct streams may be driven from distinct host threads.
  *
  * Layouts (batch size 1, as in the reference):
@@ -72,6 +74,22 @@ int std_gqa_decode(const void* q, const void* k, const void* v, void* out,
                    long long k_head_stride, long long v_head_stride,
                    float scale, int dtype,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Allocation-free decode: no counterpart in the reference. For callers that
+ * cannot allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc) and cannot keep a workspace either. Same arguments,
+ * kernels and results as std_gqa_decode, bit for bit, but the split partials
+ * live in a device array of the library (2 MiB + 64 KiB per GPU, held until
+ * the process ends; looked up on the first call on each device, which must be
+ * the current device and the stream's device). Returns STD_E_WORKSPACE where
+ * std_gqa_decode_workspace_bytes() exceeds that size (bf16: never; fp32: more
+ * than 8 query heads per KV head at long kv_len). Calls that overlap on one
+ * GPU share the array and race: serialise them (one stream per GPU).
+ * Allocates nothing and keeps no other state. */
+int std_gqa_decode_noalloc(const void* q, const void* k, const void* v, void* out,
+                           int n_q, int n_kv, int kv_len, int d,
+                           long long k_head_stride, long long v_head_stride,
+                           float scale, int dtype, void* stream);
 
 /* Batched decode: n_batch independent single-query problems of the same
  * shape in one launch (plus one merge launch). Problem b reads

@@ -31,6 +31,7 @@
 // last-arriving-workgroup merge inside the split kernel was measured slower:
 // its device-scope fences write back L2 in every workgroup.)
 #include <climits>
+#include <mutex>
 
 #include "common.h"
 #include "lds_dma.h"
@@ -1126,6 +1127,48 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode (std_gqa_decode_noalloc). The split partials live in
+// this file-scope device array instead of a caller workspace; every GPU the
+// library runs on holds its own copy until the process ends. Host code never
+// passes the name `scratch` to a kernel (on the host it is only a stand-in
+// symbol): the device address of the current device's copy is looked up once
+// per device with hipGetSymbolAddress and kept in scratch_dev. The kernels
+// need no initial contents (every partial is written before it is read), so
+// nothing is cleared; calls that overlap on one GPU share the array and race.
+constexpr size_t kNoAllocScratchBytes = (2u << 20) + (64u << 10);
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kMaxDevices];
+
+// Device address of the current device's scratch array; the stream (if not
+// the null stream) must belong to that device.
+int scratch_address(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return STD_E_RANGE;
+  if (st != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess) return (int)e;
+    if (sdev != dev) return STD_E_RANGE;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return 0;
+}
+}  // namespace
 }  // namespace stdhip
 
 using namespace stdhip;
@@ -1216,4 +1259,23 @@ extern "C" int std_gqa_decode_indexed(const void* q, const void* dense_k, const 
   return attn_entry(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), out, n_q, n_kv, 1, kv_len, d,
                     k_head_stride, v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0,
                     0, stream, 1, BatchStrides{0, 0, 0, 0}, len_dev, ga);
+}
+
+extern "C" int std_gqa_decode_noalloc(const void* q, const void* k, const void* v, void* out, int n_q, int n_kv,
+                                      int kv_len, int d, long long k_head_stride, long long v_head_stride,
+                                      float scale, int dtype, void* stream) {
+  // The size check comes before any HIP call; attn_entry repeats the full validation.
+  if (!q || !k || !v || !out) return STD_E_NULL;
+  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || kv_len < 1 || n_q / n_kv > kMaxRows) return STD_E_SHAPE;
+  const size_t need = attn_workspace_bytes(n_kv, n_q / n_kv, kv_len, dtype);
+  if (need > kNoAllocScratchBytes) return STD_E_WORKSPACE;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int s = scratch_address(static_cast<hipStream_t>(stream), &ws);
+    if (s != 0) return s;
+  }
+  return attn_entry(q, const_cast<void*>(k), const_cast<void*>(v), out, n_q, n_kv, 1, kv_len, d, k_head_stride,
+                    v_head_stride, scale, dtype, ws, need > 0 ? kNoAllocScratchBytes : 0, nullptr, nullptr, 0, 0, 0,
+                    stream);
 }

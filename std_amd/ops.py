@@ -730,3 +730,30 @@ def stream_read(buf: torch.Tensor, mode: int, n_workgroups: int, sink: torch.Ten
         raise ValueError("buf and sink must be contiguous; sink needs n_workgroups words")
     nbytes = buf.numel() * buf.element_size()
     _lib.call("std_stream_read", buf.data_ptr(), nbytes, int(mode), int(n_workgroups), sink.data_ptr(), _stream(dev))
+
+
+def gqa_decode_noalloc(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                       scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gqa_decode through the allocation-free entry point: the library's own
+    per-GPU scratch array replaces the workspace (no allocation at all when
+    `out` is given). Results equal gqa_decode's bit for bit."""
+    if query.dim() != 4 or query.shape[0] != 1 or query.shape[2] != 1:
+        raise ValueError(f"Expected q_len=1 query [1, n_q, 1, D], got {tuple(query.shape)}")
+    dev = _check_device(query, key, value)
+    code = _dtype_code(query)
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise TypeError("query, key and value must share a dtype")
+    _check_cache_view("key", key)
+    _check_cache_view("value", value)
+    _check_rows_contiguous("query", query)
+    n_q, n_kv, kv_len = query.shape[1], key.shape[1], key.shape[2]
+    if value.shape != key.shape:
+        raise ValueError("key and value shapes differ")
+    if out is None:
+        out = torch.empty_like(query)
+    elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like query")
+    scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else float(scale)
+    _lib.call("std_gqa_decode_noalloc", query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), n_q, n_kv,
+              kv_len, HEAD_DIM, key.stride(1), value.stride(1), scale, code, _stream(dev))
+    return out
