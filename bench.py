@@ -100,6 +100,12 @@ def verify_bytes(n_q, n_kv, q, kv, d, es):
     return 2 * n_kv * kv * d * es + 2 * n_q * q * d * es
 
 
+def coll_extra_bytes(n_kv, q, n_vis):
+    """HBM bytes the collector adds to a verify launch: its fp32 logits written
+    and read back once, and the fp32 scores written."""
+    return 2 * n_kv * q * n_vis * 4 + n_kv * n_vis * 4
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -310,11 +316,23 @@ def main():
             times.append(e0.elapsed_time(e1) * 1e3 / per_replay)
         return statistics.median(times)
 
+    V = P - T
+    coll_scores = torch.empty(L, Hkv, V, dtype=torch.float32, device=dev)
+
+    def verify_collect_only():
+        # the verify attention with the visual-attention collector riding the same pass
+        for l in range(L):
+            ops.verify_attention_collect(q_verify[l], dense_k[l][:, :, :kv], dense_v[l][:, :, :kv], 0, V, kv_len=kv,
+                                         out=verify_out[l], scores=coll_scores[l])
+
     rep = 10
     verify_graph, _ = capture(repeated(verify_only, 2))
+    verify_collect_graph, _ = capture(repeated(verify_collect_only, 2))
     draft_graph, _ = capture(repeated(draft_only, rep))
     draft_all_graph, _ = capture(repeated(draft_all_layers, rep))
     verify_call_us = time_graph(verify_graph, 10, 2 * L)
+    verify_collect_us = time_graph(verify_collect_graph, 10, 2 * L)
+    del verify_collect_graph
     draft_call_us = time_graph(draft_graph, 20, rep * L)
     draft_all_warm_us = time_graph(draft_all_graph, 20, rep)
     draft_only()
@@ -395,6 +413,9 @@ def main():
         "verify_attn_us_per_layer": round(verify_call_us, 3),
         "verify_hbm_gbps": round(verify_gbps, 1),
         "verify_pct_peak": round(100 * verify_gbps / HBM_PEAK_GBPS, 2),
+        "verify_collect_us_per_layer": round(verify_collect_us, 3),
+        "collector_overhead_us_per_layer": round(verify_collect_us - verify_call_us, 3),
+        "collector_extra_bytes_per_layer": coll_extra_bytes(Hkv, Q, V),
         "select_compact_ms_all_layers": round(select_ms, 3),
         "select_compact_ms_first_call": round(select_ms_first, 3),
         "roofline": {

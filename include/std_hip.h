@@ -408,6 +408,37 @@ int std_greedy_accept(const void* logits, long long logits_row_stride, int q_row
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Verify attention with the visual-attention collector riding the same pass.
+ *
+ * Replaces VerificationCollectorV3._hook (src/std_repro/dynamic_selection.py:
+ *   504-519), called from the verify forward at
+ *   src/specvlm/models/modeling_qwen2_5_vl.py:1063-1067, together with the
+ *   verify attention it rides (std_verify_attn / std_verify_attn_append).
+ * out: exactly std_verify_attn's (bit for bit); with new_k / new_v (both or
+ * neither) the q_len new rows are appended first, as std_verify_attn_append.
+ * scores[g][j - vis_begin] (fp32, head stride scores_head_stride) =
+ *   sum_i softmax_j( qbar[g][i] . k[g][j] * scale ) over the visual keys
+ *   j in [vis_begin, vis_end), where qbar[g][i] is the fp32 mean of the query
+ *   rows of KV head g's query heads at position i (the hook's
+ *   q.float().reshape(...).mean(dim=2)); i < q_len. The visual keys form one
+ *   contiguous range of prompt keys (vis_end <= kv_len - q_len), as the video
+ *   tokens of a prompt do. bf16 only; (n_q / n_kv + 1) * q_len <= 80 (the
+ *   collector's q_len rows use the padding rows of the verify's last row
+ *   tile: gamma + 1 <= 10 at seven query heads per KV head).
+ * ------------------------------------------------------------------------ */
+size_t std_verify_attn_collect_workspace_bytes(int n_q, int n_kv, int q_len, int kv_len, int d,
+                                               int vis_begin, int vis_end);
+
+int std_verify_attn_collect(const void* q, void* k_cache, void* v_cache,
+                            const void* new_k, const void* new_v, void* out,
+                            int n_q, int n_kv, int q_len, int kv_len, int d,
+                            long long k_head_stride, long long v_head_stride,
+                            long long new_head_stride, long long new_row_stride,
+                            float scale, int dtype, int vis_begin, int vis_end,
+                            float* scores, long long scores_head_stride,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Streaming-read ceiling (measurement helper; no counterpart in the
  * reference, which records no kernel measurement). Reads `bytes` of device
  * memory at src once and writes at most one word per workgroup to sink

@@ -11,6 +11,8 @@ Modules:
   attention  draft GQA decode (gqa_sdpa) and offset-causal verify (math SDPA)
   selection  causal text-row softmax scores, lowest-index top-K, compaction
   accept     argmax (torch.argmax semantics), greedy prefix, rollback lengths
+  collector  the verify pass's visual-attention scores (group-mean query,
+             softmax over the visual keys, summed over the positions)
   brute      pure-Python loop versions for tiny inputs (pin the numpy code)
 
 Pinning (each function has at least one independent check in tests/):
@@ -30,4 +32,8 @@ Pinning (each function has at least one independent check in tests/):
       tests/test_verification_fallback.py:45-73.
   rollback_lengths              the closed-form length invariant
       dense_len + |pending| == prompt_len + |generated|.
+  verification_scores           brute-force loops on tiny shapes; per KV head
+      the scores sum to q_len; mean-query logits equal the mean of the
+      group's per-head logits; identical visual keys -> q_len / V each; one
+      dominant key takes q_len; keys outside the visual set change nothing.
 """

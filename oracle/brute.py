@@ -50,3 +50,26 @@ def selection_scores_loops(q_text, k, text_start) -> List[List[float]]:
             for j in range(lim + 1):
                 scores[g][j] += w[j] / tot
     return scores
+
+
+def verification_scores_loops(q, k, visual_positions) -> List[List[float]]:
+    """q [n_q][Q][D], k [n_kv][S][D] nested lists; per KV head, the group's
+    mean query per position, softmax over the visual keys, summed over the
+    positions: returns [n_kv][len(visual_positions)]."""
+    n_q, q_len, d = len(q), len(q[0]), len(q[0][0])
+    n_kv = len(k)
+    group = n_q // n_kv
+    scale = 1.0 / math.sqrt(d)
+    out = []
+    for g in range(n_kv):
+        col = [0.0] * len(visual_positions)
+        for i in range(q_len):
+            qbar = [sum(q[g * group + h][i][e] for h in range(group)) / group for e in range(d)]
+            logits = [sum(qbar[e] * k[g][j][e] for e in range(d)) * scale for j in visual_positions]
+            mx = max(logits)
+            w = [math.exp(x - mx) for x in logits]
+            tot = sum(w)
+            for c in range(len(w)):
+                col[c] += w[c] / tot
+        out.append(col)
+    return out

@@ -32,6 +32,7 @@
 // its device-scope fences write back L2 in every workgroup.)
 #include <climits>
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "lds_dma.h"
@@ -89,6 +90,23 @@ struct GatherArgs {
   const bf16_t* v;
   long long k_hs, v_hs;
 };
+
+// Visual-attention collector riding the verify pass (COLL): the group-mean
+// query of each verify position, a softmax over the visual keys only, summed
+// over the positions. logits: [n_kv][n_vtiles][q_len][64] log2-domain scaled
+// logits of the 64-key tiles that hold visual keys (tile vt = key / 64 -
+// vis_begin / 64; -inf at non-visual keys), so that a split writes one
+// contiguous block per tile; stats: [n_kv][n_split][q_len] per-split (max, sum
+// of exp2(logit - max)).
+struct CollArgs {
+  float* logits;
+  float2* stats;
+  int n_vtiles;
+  int vis_begin, vis_end;
+};
+
+template <bool COLL>
+using AuxArgs = typename std::conditional<COLL, CollArgs, GatherArgs>::type;
 
 struct WsLayout {
   size_t o_off, ml_off, total;
@@ -187,13 +205,13 @@ constexpr int kMergeThreads = kMergeGroups * (D / 4);
 constexpr int kMergePrefetch = 8;
 
 template <typename T>
-__global__ void __launch_bounds__(kMergeThreads)
-attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
-                  int n_split, int q_len, int group, long long out_bs, int n_kv) {
+__device__ __forceinline__ void merge_row(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml,
+                                          T* __restrict__ out, int n_split, int q_len, int group, long long out_bs,
+                                          int n_kv, int r, int g) {
   __shared__ float wts[kMaxSplit];
   __shared__ float red[2][kMergeThreads / 64];
   __shared__ f32x4 part[kMergeGroups][D / 4];
-  const int r = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int d4 = tid & (D / 4 - 1), sg = tid / (D / 4);
   const int R = group * q_len;
   out += blockIdx.z * out_bs;
@@ -272,6 +290,95 @@ attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_
   }
 }
 
+template <typename T>
+__global__ void __launch_bounds__(kMergeThreads)
+attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
+                  int n_split, int q_len, int group, long long out_bs, int n_kv) {
+  merge_row<T>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y);
+}
+
+// Collector finish (the column sums of VerificationCollectorV3._hook,
+// dynamic_selection.py:504-519), one 256-thread block per 16 visual tiles
+// (1024 keys) of a KV head: thread t's four keys are columns 4 (t % 16) .. +3
+// of visual tile 16 cb + t / 16. Every load is issued first: the thread's logits, then
+// the split statistics of the rows its wave reduces (wave w: rows w, w + 4,
+// ...; lane s: splits s, s + 64, ...). Each row's log-sum-exp is formed by a
+// fixed butterfly, then the thread sums exp2(logit - lse) over the rows in
+// row order.
+__device__ __forceinline__ void coll_finish(const float* __restrict__ logits, const float2* __restrict__ stats,
+                                            float* __restrict__ scores, long long score_hs, int q_len, int n_split,
+                                            int n_vtiles, int vis_begin, int vis_end, int cb, int g) {
+  __shared__ float lse[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int vt = min(16 * cb + tid / 16, n_vtiles - 1), c = 4 * (tid % 16);
+  const float* src = logits + ((long long)g * n_vtiles + vt) * q_len * TK + c;
+  f32x4 z[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (i < q_len) z[i] = *reinterpret_cast<const f32x4*>(src + i * TK);
+  float2 st[4][2];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = wv + 4 * r, sp = lane + 64 * h;
+      st[r][h] = (i < q_len && sp < n_split) ? stats[((long long)g * n_split + sp) * q_len + i]
+                                             : make_float2(-1e30f, 0.f);
+    }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = wv + 4 * r;
+    float m = fmaxf(st[r][0].x, st[r][1].x);
+    float l = st[r][0].y * fast_exp2(st[r][0].x - m) + st[r][1].y * fast_exp2(st[r][1].x - m);
+    for (int sp = lane + 128; sp < n_split; sp += 64) {       // more than 128 splits (fewer than 2 KV heads)
+      const float2 v = stats[((long long)g * n_split + sp) * q_len + min(i, q_len - 1)];
+      const float mm = fmaxf(m, v.x);
+      l = l * fast_exp2(m - mm) + v.y * fast_exp2(v.x - mm);
+      m = mm;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float mo = __shfl_xor(m, off), lo = __shfl_xor(l, off);
+      const float mm = fmaxf(m, mo);
+      l = l * fast_exp2(m - mm) + lo * fast_exp2(mo - mm);
+      m = mm;
+    }
+    if (lane == 0 && i < q_len) lse[i] = m + __log2f(l);
+  }
+  __syncthreads();
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (i < q_len) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += fast_exp2(z[i][e] - lse[i]);
+    }
+  if (16 * cb + tid / 16 >= n_vtiles) return;
+  float* dst = scores + (long long)g * score_hs;
+  const int key0 = (vis_begin / TK + vt) * TK + c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int key = key0 + e;
+    if (key >= vis_begin && key < vis_end) dst[key - vis_begin] = acc[e];
+  }
+}
+
+// The verify merge and the collector finish in one launch: grid
+// (n_rows + n_col_blocks, n_kv); blocks x < n_rows merge attention row x (none
+// when the verify ran as one split), the others finish 1024 visual keys each.
+__global__ void __launch_bounds__(kMergeThreads)
+merge_coll_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, bf16_t* __restrict__ out,
+                  int n_split, int q_len, int group, int n_rows, const float* __restrict__ logits,
+                  const float2* __restrict__ stats, float* __restrict__ scores, int n_vtiles, long long score_hs,
+                  int vis_begin, int vis_end) {
+  static_assert(kMergeThreads == 256, "the collector finish runs 256 threads");
+  if ((int)blockIdx.x < n_rows)
+    merge_row<bf16_t>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
+  else
+    coll_finish(logits, stats, scores, score_hs, q_len, n_split, n_vtiles, vis_begin, vis_end, blockIdx.x - n_rows,
+                blockIdx.y);
+}
+
 // ===========================================================================
 // bf16 kernel: DMA ring + swizzled LDS + MFMA.
 constexpr int NSTAGE = 4;
@@ -333,14 +440,14 @@ struct Bf16Cfg {
   static constexpr int kLoadsPerTile = 2 * kSegsPerWave;
 };
 
-template <int NT, bool KS, bool GA>
+template <int NT, bool KS, bool GA, bool COLL = false>
 __global__ void __launch_bounds__(NT == 1 ? 256 : 512)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
                  bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                  int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
                  long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev,
-                 GatherArgs ga, const int32_t* __restrict__ gidx) {
+                 AuxArgs<COLL> ga, const int32_t* __restrict__ gidx) {
   using C = Bf16Cfg<NT>;
   __shared__ __align__(16) char ring[NSTAGE * STAGEB];
 
@@ -354,6 +461,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   // 0-3 and waves 4-7, one per SIMD, share row tile 4 by keys as in the key
   // split, so that no SIMD carries two row tiles.
   static_assert(!KS || NT == 1, "the key split serves one row tile");
+  static_assert(!COLL || (NT == 5 && !KS && !GA), "the collector rides the five-row-tile verify layout");
   constexpr bool HYB = NT == 5 && !KS;
   constexpr int kOwners = HYB ? 4 : NT;
   const bool computes = !KS && w < kOwners;     // row owner (wave-uniform)
@@ -381,29 +489,38 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     __syncthreads();
   }
 
-  // Each wave DMAs kSegsPerWave 1 KiB segments (4 rows) of K and of V per
+  // Each issuing wave DMAs kSegs 1 KiB segments (4 rows) of K and of V per
   // tile. Lane l fills row 4*seg + l/16 at physical chunk l%16, i.e. logical
   // chunk (l%16) ^ swz(row). Rows past the cache's last key re-read that key
   // (their scores are masked), so no read leaves the valid range.
-  int dma_row[C::kSegsPerWave], dma_chunk[C::kSegsPerWave];
+  // With the collector, only waves 0-3 issue the ring (four segments each):
+  // the key-split waves then keep no loads of the ring in flight, so their
+  // logit stores never enter a ring wait count, and they need no ring wait at
+  // all (the barrier that follows the issuing waves' waits orders each tile).
+  constexpr int kDmaWaves = COLL ? 4 : C::kWaves;
+  constexpr int kSegs = 16 / kDmaWaves;
+  constexpr int kLoads = 2 * kSegs;
+  const bool dma_wave = w < kDmaWaves;
+  int dma_row[kSegs], dma_chunk[kSegs];
 #pragma unroll
-  for (int j = 0; j < C::kSegsPerWave; ++j) {
-    const int seg = w * C::kSegsPerWave + j;
+  for (int j = 0; j < kSegs; ++j) {
+    const int seg = w * kSegs + j;
     dma_row[j] = seg * 4 + (lane >> 4);
     dma_chunk[j] = ((lane & 15) ^ swz(dma_row[j])) * 16;
   }
   auto issue = [&](int tt, char* stage) {
+    if (!dma_wave) return;
     const int key0 = tile_key0(split, tt, n_split);
     const int last = min(kv_len - key0, TK) - 1;       // wave-uniform
     if constexpr (GA) {
       static_assert(NT == 1, "gathered keys serve the single-row decode");
       if (key0 < ga.n_idx) {                             // wave-uniform: a tile with gathered keys
-        // This wave's DMA rows are 4 kSegsPerWave consecutive rows from wrow0;
+        // This wave's DMA rows are 4 kSegs consecutive rows from wrow0;
         // their indices come through scalar loads (gidx is read-only and not
         // aliased, so the compiler can use them; they are counted apart from
         // the ring's vector-memory count), then each lane copies from its row's
         // own address: gathered dense row or own-cache row.
-        constexpr int kRows = 4 * C::kSegsPerWave;
+        constexpr int kRows = 4 * kSegs;
         const int wrow0 = w * kRows;
         int sidx[kRows];
         if (key0 + wrow0 < ga.n_idx) {
@@ -437,7 +554,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
         }
         const int sel = lane >> 4;
 #pragma unroll
-        for (int j = 0; j < C::kSegsPerWave; ++j) {
+        for (int j = 0; j < kSegs; ++j) {
           const int r = dma_row[j];
           const int key = key0 + r;
           int ix = sel == 0 ? sidx[4 * j] : sel == 1 ? sidx[4 * j + 1] : sel == 2 ? sidx[4 * j + 2] : sidx[4 * j + 3];
@@ -453,7 +570,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
             ka = reinterpret_cast<const char*>(kh + (long long)key * D);
             va = reinterpret_cast<const char*>(vh + (long long)key * D);
           }
-          const uint32_t dst = lds_addr(stage) + (w * C::kSegsPerWave + j) * 1024;
+          const uint32_t dst = lds_addr(stage) + (w * kSegs + j) * 1024;
           lds_dma16_vaddr(ka + dma_chunk[j], dst);
           lds_dma16_vaddr(va + dma_chunk[j], dst + TILEB);
         }
@@ -463,9 +580,9 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     const bf16_t* kt = kh + (long long)key0 * D;
     const bf16_t* vt = vh + (long long)key0 * D;
 #pragma unroll
-    for (int j = 0; j < C::kSegsPerWave; ++j) {
+    for (int j = 0; j < kSegs; ++j) {
       const uint32_t off = (uint32_t)(min(dma_row[j], last) * ROWB + dma_chunk[j]);
-      const uint32_t dst = lds_addr(stage) + (w * C::kSegsPerWave + j) * 1024;
+      const uint32_t dst = lds_addr(stage) + (w * kSegs + j) * 1024;
       lds_dma16_sbase(kt, off, dst);
       lds_dma16_sbase(vt, off, dst + TILEB);
     }
@@ -492,6 +609,47 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
 #pragma unroll
     for (int c = 0; c < 4; ++c) qf[c] = bf16x8{};
   }
+  // Collector rows: lanes q_off .. 15 of the key-split waves (the padding rows
+  // of the last row tile, R + q_len <= 80) carry position i = ln - q_off's
+  // group-mean query, the fp32 mean of the group's bf16 query rows
+  // (modeling_qwen2_5_vl.py hook -> dynamic_selection.py:509-512), split into
+  // a bf16 head qf and a bf16 remainder qlo, so that K.qf + K.qlo carries the
+  // fp32 mean's precision through bf16 MFMAs.
+  const int q_off = 16 - q_len;
+  bf16x8 qlo[4];
+  if constexpr (COLL) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qlo[c] = bf16x8{};
+    if (ksw && ln >= q_off) {
+      const int i = ln - q_off;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float m8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int hl = 0; hl < group; ++hl) {
+          const uint4 v4 =
+              *reinterpret_cast<const uint4*>(q + ((long long)(g * group + hl) * q_len + i) * D + 32 * c + 8 * lg);
+          const uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            m8[2 * e] += bf16_to_f32(w4[e] & 0xffffu);
+            m8[2 * e + 1] += bf16_to_f32(w4[e] >> 16);
+          }
+        }
+        const float inv = 1.f / (float)group;
+        i16x8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float mean = m8[e] * inv;
+          const uint32_t h = f32_to_bf16(mean);
+          hi[e] = (short)h;
+          lo[e] = (short)f32_to_bf16(mean - bf16_to_f32(h));
+        }
+        qf[c] = __builtin_bit_cast(bf16x8, hi);
+        qlo[c] = __builtin_bit_cast(bf16x8, lo);
+      }
+    }
+  }
+  float m_c = -1e30f, l_c = 0.f;       // collector row statistics of this lane's keys (log2 domain)
   // Retire the query loads (and with them the two ring tiles issued before
   // them) here: the compiler counts only its own loads, and a wait for them
   // placed inside the loop would drain the ring there.
@@ -607,11 +765,38 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   typedef short s16x4 __attribute__((ext_vector_type(4)));
   const s16x4 ones4 = {0x3f80, 0x3f80, 0x3f80, 0x3f80};
   auto ks_tile = [&](int tt, const char* st) {
-    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + sw_off(16 * ks_sub + ln, 4 * c + lg));
       sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], sc, 0, 0, 0);
+      if constexpr (COLL) sl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qlo[c], sl, 0, 0, 0);
+    }
+    if constexpr (COLL) {
+      // Collector lanes: logits of this wave's four keys of the tile, over
+      // the visual keys only; stored, and folded into the lane's (max, sum).
+      if (ln >= q_off) {
+        const int kb = tile_key0(split, tt, n_split);
+        const int key0 = kb + 16 * ks_sub + 4 * lg;
+        float z[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool vis = key0 + i >= ga.vis_begin && key0 + i < ga.vis_end;
+          z[i] = vis ? (sc[i] + sl[i]) * scale_log2 : -INFINITY;
+        }
+        const int vt = kb / TK - ga.vis_begin / TK;           // wave-uniform
+        if (vt >= 0 && vt < ga.n_vtiles) {
+          float* dst = ga.logits + (((long long)g * ga.n_vtiles + vt) * q_len + (ln - q_off)) * TK + 16 * ks_sub +
+                       4 * lg;
+          *reinterpret_cast<f32x4*>(dst) = f32x4{z[0], z[1], z[2], z[3]};
+        }
+        const float mx = fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
+        if (mx > m_c) {
+          l_c *= fast_exp2(m_c - mx);
+          m_c = mx;
+        }
+        l_c += (fast_exp2(z[0] - m_c) + fast_exp2(z[1] - m_c)) + (fast_exp2(z[2] - m_c) + fast_exp2(z[3] - m_c));
+      }
     }
     const char* Vs = st + TILEB;
     const int rv = 16 * ks_sub + 4 * lg + (ln >> 2);
@@ -706,7 +891,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   f32x4 sA[4], sB[4];
   auto step = [&](int u, const char* cur, const char* prev, char* ahead2, f32x4* s_new, f32x4* s_old) {
     if (u > ntiles) return;
-    if (u < ntiles) wait_vm_ahead<C::kLoadsPerTile>(u + 1 < ntiles ? 1 : 0);
+    if (u < ntiles && dma_wave) wait_vm_ahead<kLoads>(u + 1 < ntiles ? 1 : 0);
     wg_barrier();
     if (u + 2 < ntiles) issue(u + 2, ahead2);
     if (computes) {
@@ -723,7 +908,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     // complete; after the barrier (every wave is done with tile u-1) tile u+3
     // goes into tile u-1's stage, then tile u is scored and accumulated.
     for (int u = 0; u < ntiles; ++u) {
-      wait_vm_ahead<C::kLoadsPerTile>(min(2, ntiles - 1 - u));
+      wait_vm_ahead<kLoads>(min(2, ntiles - 1 - u));
       wg_barrier();
       if (u + 3 < ntiles) issue(u + 3, stage(u + 3));
       ks_tile(u, stage(u));
@@ -738,16 +923,40 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       step(u + 1, stage(u + 1), stage(u), stage(u + 3), sB, sA);
     }
   }
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  if (dma_wave) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   if constexpr (HYB) {
     // The row owners may still read the last tile's stage (their final PV);
     // the key-split waves merge through two other stages, then write the last
     // row tile while the owners write theirs.
     const int sl = (ntiles - 1) & (NSTAGE - 1);
     char* region = ring + (sl <= 1 ? (sl + 1) * STAGEB : 0);
+    // Collector: each key-split wave's (max, sum) per row over its four lane
+    // groups, then (after the barrier) the four waves in wave order.
+    float2* cst = reinterpret_cast<float2*>(region + 1024 + 4 * 16 * OROW * 4);
+    if constexpr (COLL) {
+      static_assert(1024 + 4 * 16 * OROW * 4 + 4 * 16 * 8 <= 2 * STAGEB, "collector statistics exceed the region");
+      if (ksw) {
+        const float M = xor32_max(xor16_max(m_c));
+        const float L = xor32_sum(xor16_sum(l_c * fast_exp2(m_c - M)));
+        if (lg == 0) cst[ks_sub * 16 + ln] = make_float2(M, L);
+      }
+    }
     if (ksw) ks_store(region);
     __syncthreads();
     if (ksw) {
+      if constexpr (COLL) {
+        const int t = tid - 64 * kOwners;
+        if (t < q_len) {
+          float2 w[4];
+#pragma unroll
+          for (int ww = 0; ww < 4; ++ww) w[ww] = cst[ww * 16 + q_off + t];
+          const float M = fmaxf(fmaxf(w[0].x, w[1].x), fmaxf(w[2].x, w[3].x));
+          float L = 0.f;
+#pragma unroll
+          for (int ww = 0; ww < 4; ++ww) L += w[ww].y * fast_exp2(w[ww].x - M);
+          ga.stats[((long long)g * n_split + split) * q_len + t] = make_float2(M, L);
+        }
+      }
       ks_merge_rows(region, 16 * kOwners, C::kThreads - 64 * kOwners, tid - 64 * kOwners);
       return;
     }
@@ -1126,6 +1335,71 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
                      n_new, n_batch, bs, len_dev, ga, static_cast<hipStream_t>(stream));
 }
 
+// Verify + collector workspace: the verify attention's (split partials), then
+// the collector logits [n_kv][q_len][logit_rs] and statistics
+// [n_kv][n_split][q_len].
+struct CollLayout {
+  size_t attn, logits_off, stats_off, total;
+  int n_vtiles, n_split;
+};
+
+CollLayout coll_layout(int n_kv, int group, int q_len, int kv_len, int vis_begin, int vis_end) {
+  CollLayout c{};
+  const SplitPlan p = plan_splits(n_kv, group * q_len, kv_len, STD_BF16);
+  c.n_split = p.n_split;
+  c.attn = round_up(ws_layout(n_kv, group * q_len, p).total, 256);
+  c.n_vtiles = (vis_end - 1) / TK - vis_begin / TK + 1;
+  c.logits_off = c.attn;
+  c.stats_off = round_up(c.logits_off + (size_t)n_kv * c.n_vtiles * q_len * TK * sizeof(float), 256);
+  c.total = round_up(c.stats_off + (size_t)n_kv * p.n_split * q_len * sizeof(float2), 256);
+  return c;
+}
+
+int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, int q_len, int kv_len,
+                         int d, long long k_hs, long long v_hs, float scale, int dtype, const void* nk,
+                         const void* nv, long long n_hs, long long n_rs, int vis_begin, int vis_end, float* scores,
+                         long long score_hs, void* ws, size_t ws_bytes, void* stream) {
+  if (!q || !k || !v || !out || !scores) return STD_E_NULL;
+  if ((nk == nullptr) != (nv == nullptr)) return STD_E_NULL;
+  if (dtype != STD_BF16) return STD_E_DTYPE;
+  if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len) return STD_E_SHAPE;
+  const int group = n_q / n_kv;
+  // the collector rows fill the padding lanes of the five-row-tile layout's last row tile
+  if (q_len > 16 || (long long)group * q_len + q_len > 80) return STD_E_SHAPE;
+  if (vis_begin < 0 || vis_end <= vis_begin || vis_end > kv_len - q_len) return STD_E_SHAPE;
+  if (n_kv > 1 && (k_hs < (long long)kv_len * D || v_hs < (long long)kv_len * D)) return STD_E_SHAPE;
+  if (n_kv > 1 && score_hs < vis_end - vis_begin) return STD_E_SHAPE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return STD_E_ALIGN;
+  if ((k_hs * 2) % 16 != 0 || (v_hs * 2) % 16 != 0) return STD_E_ALIGN;
+  if (nk && (!aligned16(nk) || !aligned16(nv) || (n_hs * 2) % 16 != 0 || (n_rs * 2) % 16 != 0)) return STD_E_ALIGN;
+  const CollLayout cl = coll_layout(n_kv, group, q_len, kv_len, vis_begin, vis_end);
+  if (ws == nullptr || ws_bytes < cl.total) return STD_E_WORKSPACE;
+  if (!aligned16(ws)) return STD_E_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int R = group * q_len;
+  const SplitPlan p = plan_splits(n_kv, R, kv_len, STD_BF16);
+  const WsLayout wl = ws_layout(n_kv, R, p);
+  char* base = static_cast<char*>(ws);
+  float* ws_o = p.n_split > 1 ? reinterpret_cast<float*>(base + wl.o_off) : nullptr;
+  float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
+  const CollArgs ca{reinterpret_cast<float*>(base + cl.logits_off), reinterpret_cast<float2*>(base + cl.stats_off),
+                    cl.n_vtiles, vis_begin, vis_end};
+  const int n_new = nk ? q_len : 0;
+  hipLaunchKernelGGL((attn_bf16_kernel<5, false, false, true>), dim3(p.n_split, n_kv, 1), dim3(Bf16Cfg<5>::kThreads),
+                     0, st, static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
+                     static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs,
+                     scale * 1.4426950408889634f, p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
+                     static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, BatchStrides{0, 0, 0, 0, 0}, nullptr, ca,
+                     nullptr);
+  int s = launch_status();
+  if (s != 0) return s;
+  const int n_rows = p.n_split > 1 ? R : 0;
+  hipLaunchKernelGGL(merge_coll_kernel, dim3(n_rows + (cl.n_vtiles + 15) / 16, n_kv), dim3(kMergeThreads), 0, st,
+                     ws_o, ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len, group, n_rows, ca.logits, ca.stats,
+                     scores, cl.n_vtiles, n_kv > 1 ? score_hs : 0LL, vis_begin, vis_end);
+  return launch_status();
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1278,4 +1552,22 @@ extern "C" int std_gqa_decode_noalloc(const void* q, const void* k, const void* 
   return attn_entry(q, const_cast<void*>(k), const_cast<void*>(v), out, n_q, n_kv, 1, kv_len, d, k_head_stride,
                     v_head_stride, scale, dtype, ws, need > 0 ? kNoAllocScratchBytes : 0, nullptr, nullptr, 0, 0, 0,
                     stream);
+}
+
+extern "C" size_t std_verify_attn_collect_workspace_bytes(int n_q, int n_kv, int q_len, int kv_len, int d,
+                                                          int vis_begin, int vis_end) {
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len || d != D) return 0;
+  if (vis_begin < 0 || vis_end <= vis_begin || vis_end > kv_len) return 0;
+  return coll_layout(n_kv, n_q / n_kv, q_len, kv_len, vis_begin, vis_end).total;
+}
+
+extern "C" int std_verify_attn_collect(const void* q, void* k_cache, void* v_cache, const void* new_k,
+                                       const void* new_v, void* out, int n_q, int n_kv, int q_len, int kv_len,
+                                       int d, long long k_head_stride, long long v_head_stride,
+                                       long long new_head_stride, long long new_row_stride, float scale, int dtype,
+                                       int vis_begin, int vis_end, float* scores, long long scores_head_stride,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  return verify_collect_entry(q, k_cache, v_cache, out, n_q, n_kv, q_len, kv_len, d, k_head_stride, v_head_stride,
+                              scale, dtype, new_k, new_v, new_head_stride, new_row_stride, vis_begin, vis_end, scores,
+                              scores_head_stride, workspace, workspace_bytes, stream);
 }

@@ -757,3 +757,73 @@ def gqa_decode_noalloc(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
     _lib.call("std_gqa_decode_noalloc", query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), n_q, n_kv,
               kv_len, HEAD_DIM, key.stride(1), value.stride(1), scale, code, _stream(dev))
     return out
+
+
+def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                             vis_begin: int, vis_end: int, new_key: Optional[torch.Tensor] = None,
+                             new_value: Optional[torch.Tensor] = None, kv_len: Optional[int] = None,
+                             scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                             scores: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Dense verify attention plus the visual-attention collector in one pass
+    (VerificationCollectorV3._hook, dynamic_selection.py:504-519, riding the
+    verify forward at modeling_qwen2_5_vl.py:1063-1067).
+
+    query [1, n_q, q_len, D] bf16; key_cache / value_cache [1, n_kv, S, D]
+    cache views (read in place). Without new_key/new_value the caches hold
+    kv_len (default S) keys including this step's q_len rows; with them
+    ([1, n_kv, q_len, D]) those rows are appended at kv_len - q_len first.
+    Returns (out [1, n_q, q_len, D], scores [n_kv, vis_end - vis_begin] fp32):
+    out is verify_attention's result bit for bit; scores[g, j] sums, over the
+    q_len positions, the softmax over the visual keys [vis_begin, vis_end) of
+    the group-mean query of KV head g."""
+    dev = _check_device(query, key_cache, value_cache)
+    if query.dtype != torch.bfloat16:
+        raise TypeError("the collector path is bf16")
+    if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
+        raise TypeError("query and caches must share a dtype")
+    _check_cache_view("key_cache", key_cache)
+    _check_cache_view("value_cache", value_cache)
+    _check_rows_contiguous("query", query)
+    if query.dim() != 4 or query.shape[0] != 1:
+        raise ValueError(f"Expected query [1, n_q, q_len, D], got {tuple(query.shape)}")
+    _, n_q, q_len, d = query.shape
+    n_kv = key_cache.shape[1]
+    if kv_len is None:
+        kv_len = key_cache.shape[2]
+    if not (q_len <= kv_len <= key_cache.shape[2]):
+        raise ValueError(f"kv_len={kv_len} must be in [q_len, cache capacity {key_cache.shape[2]}]")
+    appending = new_key is not None
+    if appending != (new_value is not None):
+        raise ValueError("new_key and new_value go together")
+    if appending:
+        for name, t in (("new_key", new_key), ("new_value", new_value)):
+            if t.dim() != 4 or tuple(t.shape) != (1, n_kv, q_len, HEAD_DIM) or t.stride(3) != 1:
+                raise ValueError(f"{name} must be [1, n_kv, {q_len}, {HEAD_DIM}] with contiguous rows")
+            if t.dtype != query.dtype or t.device != query.device:
+                raise TypeError(f"{name} must match the query dtype and device")
+        if not same_layout(new_key, new_value):
+            raise ValueError("new_key and new_value must share strides")
+    if not (0 <= vis_begin < vis_end <= kv_len - q_len):
+        raise ValueError(f"visual keys [{vis_begin}, {vis_end}) must be prompt keys below {kv_len - q_len}")
+    if out is None:
+        out = torch.empty_like(query)
+    elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like query")
+    n_vis = vis_end - vis_begin
+    if scores is None:
+        scores = torch.empty(n_kv, n_vis, dtype=torch.float32, device=dev)
+    elif scores.dtype != torch.float32 or scores.dim() != 2 or tuple(scores.shape) != (n_kv, n_vis) or \
+            scores.stride(1) != 1:
+        raise ValueError(f"scores must be float32 [{n_kv}, {n_vis}] with contiguous rows")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    lib = _lib.load_library()
+    ws_bytes = lib.std_verify_attn_collect_workspace_bytes(n_q, n_kv, q_len, kv_len, d, vis_begin, vis_end)
+    ws_ptr = _attn_workspace(ws_bytes, dev)
+    _lib.call("std_verify_attn_collect", query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+              new_key.data_ptr() if appending else None, new_value.data_ptr() if appending else None,
+              out.data_ptr(), n_q, n_kv, q_len, int(kv_len), d, key_cache.stride(1), value_cache.stride(1),
+              new_key.stride(1) if appending else 0, new_key.stride(2) if appending else 0, float(scale),
+              _lib.STD_BF16, int(vis_begin), int(vis_end), scores.data_ptr(), scores.stride(0), ws_ptr, ws_bytes,
+              _stream(dev))
+    return out, scores

@@ -110,6 +110,27 @@ def test_verify_validation():
     assert lib.std_verify_attn(16, 16, 16, 16, 28, 4, 11, 10, 128, hs, hs, 1.0, 1, NULL, 0, NULL) == -3   # q > kv
 
 
+def test_verify_collect_validation():
+    lib = _lib.load_library()
+    hs = 4106 * 128
+    args = dict(q=16, k=16, v=16, nk=NULL, nv=NULL, out=16, nq=28, nkv=4, ql=10, kv=4106, d=128, khs=hs, vhs=hs,
+                nhs=0, nrs=0, scale=0.088, dt=1, vb=0, ve=3968, sc=16, schs=3968, ws=16, wsb=1 << 30, st=NULL)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.std_verify_attn_collect(*a.values())
+    assert lib.std_verify_attn_collect_workspace_bytes(28, 4, 10, 4106, 128, 0, 3968) > 0
+    assert call(dt=0) == -2                     # bf16 only
+    assert call(sc=NULL) == -1
+    assert call(nk=16) == -1                    # new_k without new_v
+    assert call(ql=11) == -3                    # (7 + 1) * 11 > 80 rows
+    assert call(nq=4, ql=17) == -3              # more than 16 collector rows
+    assert call(ve=4100) == -3                  # visual keys must be prompt keys
+    assert call(vb=3968) == -3                  # empty visual range
+    assert call(schs=100) == -3                 # score rows overlap
+    assert call(wsb=10) == -4
+
+
 def test_select_validation():
     lib = _lib.load_library()
     hs = 4096 * 128

@@ -1,0 +1,80 @@
+"""GPU parity of the visual-attention collector that rides the verify pass
+(std_verify_attn_collect) against the oracle restatement of
+VerificationCollectorV3._hook (src/std_repro/dynamic_selection.py:504-519),
+and bit-equality of its attention output with the plain verify launch."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import collector as ref_coll
+from std_amd import ops
+from std_amd.workloads import WORKLOADS, make_layer
+from tests.gpu_helpers import announce, cache_buffer, dev
+
+pytestmark = pytest.mark.gpu
+
+# Scores: fp32 sums of exp2 of fp32 logits whose queries carry the fp32 mean
+# (bf16 head + bf16 remainder), against fp64: relative 2e-4.
+RTOL, ATOL = 2e-4, 1e-9
+
+
+def _layer(wname, layer, prompt_len=None, q_len=None):
+    w = WORKLOADS[wname]
+    x = make_layer(w, layer, prompt_len=prompt_len)
+    if q_len is not None and q_len != x["q_verify"].shape[2]:
+        x = dict(x, q_verify=x["q_verify"][:, :, :q_len].contiguous(), new_k=x["new_k"][:, :, :q_len].contiguous(),
+                 new_v=x["new_v"][:, :, :q_len].contiguous())
+    k = torch.cat([x["k"], x["new_k"]], 2)
+    v = torch.cat([x["v"], x["new_v"]], 2)
+    return w, x, k, v
+
+
+def _check(wname, layer, vis_begin, vis_end, prompt_len=None, q_len=None, append=False):
+    w, x, k, v = _layer(wname, layer, prompt_len, q_len)
+    q = x["q_verify"]
+    Q, kv_len = q.shape[2], k.shape[2]
+    announce(f"collector {wname} layer={layer} kv_len={kv_len} q_len={Q} visual=[{vis_begin},{vis_end}) "
+             f"append={append}")
+    kb = cache_buffer(k, kv_len + 29)
+    vb = cache_buffer(v, kv_len + 29)
+    qd = q.to(dev())
+    want_out = ops.verify_attention(qd, kb[:, :, :kv_len], vb[:, :, :kv_len])
+    if append:
+        kb2 = cache_buffer(x["k"], kv_len + 29)
+        vb2 = cache_buffer(x["v"], kv_len + 29)
+        out, scores = ops.verify_attention_collect(qd, kb2, vb2, vis_begin, vis_end, new_key=x["new_k"].to(dev()),
+                                                   new_value=x["new_v"].to(dev()), kv_len=kv_len)
+        torch.cuda.synchronize()
+        assert torch.equal(kb2[:, :, :kv_len], kb[:, :, :kv_len]) and torch.equal(vb2[:, :, :kv_len],
+                                                                                    vb[:, :, :kv_len])
+    else:
+        out, scores = ops.verify_attention_collect(qd, kb, vb, vis_begin, vis_end, kv_len=kv_len)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want_out), "collector launch changed the verify output"
+    want = ref_coll.verification_scores(q, k, np.arange(vis_begin, vis_end))
+    got = scores.double().cpu().numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(got.sum(axis=1), Q, rtol=1e-4)
+
+
+def test_collector_c2():
+    w = WORKLOADS["c2"]
+    _check("c2", 0, 0, w.prompt_len - w.text_len)
+
+
+def test_collector_c2_append_first_round_rows():
+    """Nine verify rows (the first round, no pending token) and the fused append."""
+    w = WORKLOADS["c2"]
+    _check("c2", 1, 0, w.prompt_len - w.text_len, q_len=9, append=True)
+
+
+def test_collector_unaligned_visual_range():
+    """Visual keys not starting at 0 nor on a 4-key boundary (a system prompt before the video)."""
+    _check("c2", 2, 13, 3003, prompt_len=4096)
+
+
+def test_collector_c4_full_context_lognormal_keys():
+    """131082 keys with heavy-tailed key norms, the 128k-context verify."""
+    w = WORKLOADS["c4"]
+    _check("c4", 0, 0, w.prompt_len - w.text_len, append=True)

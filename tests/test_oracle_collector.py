@@ -1,0 +1,71 @@
+"""Pins oracle.collector.verification_scores (the restatement of
+VerificationCollectorV3._hook, src/std_repro/dynamic_selection.py:504-519)
+with checks that share no code with it."""
+import numpy as np
+import pytest
+
+from oracle import brute
+from oracle.collector import verification_scores
+
+
+def _case(seed, n_q=6, n_kv=2, q_len=3, kv_len=14, d=8):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((1, n_q, q_len, d))
+    k = rng.standard_normal((1, n_kv, kv_len, d))
+    return q, k
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_matches_brute_force_loops(seed):
+    q, k = _case(seed)
+    vis = list(range(3, 11))
+    got = verification_scores(q, k, vis)
+    want = brute.verification_scores_loops(q[0].tolist(), k[0].tolist(), vis)
+    np.testing.assert_allclose(got, np.array(want), rtol=1e-12, atol=1e-14)
+
+
+def test_each_position_contributes_a_distribution():
+    q, k = _case(5, q_len=4)
+    s = verification_scores(q, k, range(0, 12))
+    assert (s >= 0).all()
+    np.testing.assert_allclose(s.sum(axis=1), 4.0, rtol=1e-12)
+
+
+def test_mean_query_logits_equal_mean_of_head_logits():
+    """The collector's logits are linear in the query: q_bar . k equals the
+    mean over the group's heads of q_h . k, computed here per head."""
+    q, k = _case(7, n_q=8, n_kv=2, q_len=2, d=16)
+    vis = np.arange(2, 13)
+    d = q.shape[-1]
+    s = np.zeros((2, vis.size))
+    for g in range(2):
+        for i in range(2):
+            per_head = [q[0, g * 4 + h, i] @ k[0, g, vis].T for h in range(4)]
+            logits = np.mean(per_head, axis=0) / np.sqrt(d)
+            w = np.exp(logits - logits.max())
+            s[g] += w / w.sum()
+    np.testing.assert_allclose(verification_scores(q, k, vis), s, rtol=1e-12)
+
+
+def test_identical_visual_keys_share_the_mass_evenly():
+    q, k = _case(9, q_len=5)
+    k[0, :, 2:10] = k[0, :, 2:3]
+    s = verification_scores(q, k, range(2, 10))
+    np.testing.assert_allclose(s, 5.0 / 8, rtol=1e-12)
+
+
+def test_one_dominant_key_takes_every_position():
+    q, k = _case(11, n_q=4, n_kv=1, q_len=3)
+    qbar = q[0].reshape(1, 4, 3, -1).mean(axis=1)[0]          # [3, D]
+    k[0, 0, 6] = 500.0 * np.linalg.pinv(qbar) @ np.ones(3)   # qbar_i . k_6 = 500 for every position i
+    s = verification_scores(q, k, range(0, 12))
+    assert s[0, 6] > 3.0 - 1e-6
+
+
+def test_keys_outside_the_visual_set_change_nothing():
+    q, k = _case(13)
+    vis = range(4, 9)
+    a = verification_scores(q, k, vis)
+    k[0, :, :4] += 100.0
+    k[0, :, 9:] -= 100.0
+    np.testing.assert_allclose(verification_scores(q, k, vis), a, rtol=1e-13)
