@@ -108,6 +108,7 @@ class RandomDecoder:
         inv = 1.0 / (c.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
         self.inv_freq = inv.to(torch.float32).to(self.device)
         self.sparse_controller = None     # set by SparseDraftController.install()
+        self.verify_collector = None      # set by VerificationCollectorV3.install()
         self.capture_text_queries = False
         self.captured_queries: List[Optional[torch.Tensor]] = [None] * c.num_hidden_layers
 
@@ -212,7 +213,15 @@ class RandomDecoder:
             if self.capture_text_queries:
                 self.captured_queries[li] = q
             gather = controller.gather_for(li) if controller is not None and controller.enabled else None
-            if gather is not None:        # index-addressed sparse cache: prompt keys read from the dense cache
+            collector = self.verify_collector
+            if collector is not None and collector.active and n > 1:
+                # the verify forward with the visual-attention collector riding its attention pass
+                if not host_lengths:
+                    raise RuntimeError("the verification collector runs in eager (host-length) verify steps")
+                out, scores = ops.verify_attention_collect(q, kc.data, vc.data, collector.vis_begin,
+                                                           collector.vis_end, kv_len=kc.length + n)
+                collector.record(li, scores)
+            elif gather is not None:      # index-addressed sparse cache: prompt keys read from the dense cache
                 dk, dv, index, n_index = gather
                 out = ops.gqa_decode_indexed(q, dk, dv, index, n_index, kc.data, vc.data, length=state[0:1],
                                              max_kv_len=kc.capacity)

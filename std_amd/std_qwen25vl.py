@@ -264,6 +264,68 @@ class SparseDraftController:
         self.enabled = enabled
 
 
+class VerificationCollectorV3:
+    """Per-round visual relevance from the dense verify forward, with the
+    interface of the reference's VerificationCollectorV3
+    (src/std_repro/dynamic_selection.py:447-519): install / uninstall,
+    begin_verification / end_verification around a verify forward, and
+    ``rounds`` / ``latest_scores()`` holding fp32 [num_layers, kv_heads,
+    visual_len] on the CPU (one readback per round).
+
+    Where the reference's hook recomputes the group-mean queries against the
+    gathered visual keys in separate GEMMs, each layer's scores here come out
+    of the verify attention launch itself (``ops.verify_attention_collect``):
+    the collector's query rows ride the verify kernel's padding rows, so the
+    visual keys are read once. The visual positions must form one contiguous
+    range (the video tokens of a prompt do); verify steps must run eagerly
+    (host lengths)."""
+
+    def __init__(self, model, visual_positions: torch.Tensor):
+        pos = visual_positions.to(torch.long).cpu().reshape(-1)
+        if pos.numel() == 0:
+            raise ValueError("no visual positions")
+        self.vis_begin, self.vis_end = int(pos[0]), int(pos[-1]) + 1
+        if not torch.equal(pos, torch.arange(self.vis_begin, self.vis_end)):
+            raise ValueError("the HIP collector serves one contiguous, ascending range of visual positions")
+        self.model = model
+        self.visual_positions = pos
+        self.visual_len = int(pos.numel())
+        self.num_kv_heads = model.config.num_key_value_heads
+        self.rounds: List[torch.Tensor] = []
+        self.active = False
+        self._layer_scores: Dict[int, torch.Tensor] = {}
+        self.collect_time = 0.0
+
+    def install(self) -> None:
+        self.model.verify_collector = self
+
+    def uninstall(self) -> None:
+        if getattr(self.model, "verify_collector", None) is self:
+            self.model.verify_collector = None
+
+    def begin_verification(self, round_id: int) -> None:
+        self.active = True
+        self._layer_scores = {}
+
+    def record(self, layer_idx: int, scores: torch.Tensor) -> None:
+        """Called by the verify forward with one layer's device scores [kv_heads, visual_len]."""
+        self._layer_scores[layer_idx] = scores
+
+    def end_verification(self) -> None:
+        self.active = False
+        if not self._layer_scores:
+            return
+        t0 = time.perf_counter()
+        order = sorted(self._layer_scores)
+        stacked = torch.stack([self._layer_scores[i] for i in order], dim=0).cpu()  # single sync
+        self.collect_time += time.perf_counter() - t0
+        self.rounds.append(stacked)
+        self._layer_scores = {}
+
+    def latest_scores(self) -> Optional[torch.Tensor]:
+        return self.rounds[-1] if self.rounds else None
+
+
 def _token_argmax(logits: torch.Tensor) -> torch.Tensor:
     """[1, 1] int64 next token of the last row (graph-capture safe argmax)."""
     return ops.argmax_rows(logits[0, -1:, :]).view(1, 1)

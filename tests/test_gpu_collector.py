@@ -78,3 +78,49 @@ def test_collector_c4_full_context_lognormal_keys():
     """131082 keys with heavy-tailed key norms, the 128k-context verify."""
     w = WORKLOADS["c4"]
     _check("c4", 0, 0, w.prompt_len - w.text_len, append=True)
+
+
+def test_collector_class_on_a_decoder_verify_forward():
+    """VerificationCollectorV3 (the reference's interface) around a bf16 verify
+    forward of a two-layer decoder: per-layer scores equal the oracle on that
+    forward's rotated queries and cached keys, and the verify logits are the
+    same with and without the collector."""
+    from std_amd.decoder import DecoderConfig, RandomDecoder
+    from std_amd.kv_cache import initialize_past_key_values
+    from std_amd.std_qwen25vl import VerificationCollectorV3, prefill_prompt
+
+    announce("collector class on a tiny bf16 decoder verify forward")
+    cfg = DecoderConfig.tiny(layers=2)
+    model = RandomDecoder(cfg, dev(), torch.bfloat16, seed=5003)
+    gen = torch.Generator().manual_seed(17)
+    n_vis, n_text, Q = 1000, 24, 10
+    ids = torch.cat([torch.full((n_vis,), cfg.video_token_id),
+                     torch.randint(0, cfg.vocab_size - 2, (n_text,), generator=gen)]).view(1, -1).to(dev())
+    vis = torch.randn(n_vis, cfg.hidden_size, generator=gen).to(dev(), torch.bfloat16)
+    P = n_vis + n_text
+    step = torch.randint(0, cfg.vocab_size - 2, (1, Q), generator=gen).to(dev())
+    results = []
+    for with_collector in (False, True):
+        pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.bfloat16, P + 32)
+        prefill_prompt(model, {"input_ids": ids, "visual_embeds": vis}, pkv, cfg.video_token_id)
+        coll = None
+        if with_collector:
+            coll = VerificationCollectorV3(model, torch.arange(n_vis))
+            coll.install()
+            coll.begin_verification(0)
+        model.capture_text_queries = True
+        logits = model(step, pkv, all_logits=True)
+        model.capture_text_queries = False
+        if coll is not None:
+            coll.end_verification()
+            coll.uninstall()
+        torch.cuda.synchronize()
+        results.append((logits, coll, [q.clone() for q in model.captured_queries], pkv))
+    assert torch.equal(results[0][0], results[1][0]), "the collector changed the verify logits"
+    _, coll, queries, pkv = results[1]
+    scores = coll.latest_scores()
+    assert scores.shape == (cfg.num_hidden_layers, cfg.num_key_value_heads, n_vis)
+    for li in range(cfg.num_hidden_layers):
+        keys = pkv[li][0].data[:, :, :P + Q]
+        want = ref_coll.verification_scores(queries[li], keys, np.arange(n_vis))
+        np.testing.assert_allclose(scores[li].double().numpy(), want, rtol=RTOL, atol=ATOL)
