@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 /* element types */
-enum { STD_F32 = 0, STD_BF16 = 1 };
+enum { STD_F32 = 0, STD_BF16 = 1, STD_F16 = 2 };   /* STD_F16: selection probabilities only */
 
 /* validation errors (negative) */
 enum {
@@ -185,6 +185,25 @@ int std_select_topk(const void* q_text, const void* k,
                     const int32_t* visual_pos, int n_visual, int k_select,
                     int32_t* topk_out, double* scores_out,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Selection from materialised attention probabilities: the reference's own
+ * input. Replaces build_sparse_selection(attentions, ...) per layer
+ * (src/std_repro/std_qwen25vl.py:175-231): probs [n_q][text_len][prompt_len]
+ * (one layer's [1, n_q, T, P] probabilities of the text suffix's rows,
+ * head stride and row stride in elements, columns contiguous; STD_F16, the
+ * reference's dtype, STD_BF16 or STD_F32), summed over the query heads of
+ * each KV head and the text rows, then the top k_select of the visual
+ * columns visual_pos[n_visual] per KV head -> topk_out int32
+ * [n_kv][k_select], ascending; ties go to the lowest position. The sums are
+ * fp64 (exact for fp16 probabilities); scores_out (optional, fp64
+ * [n_kv][prompt_len]) receives them. Rows and the base 4-element aligned. */
+size_t std_select_topk_probs_workspace_bytes(int n_q, int n_kv, int text_len, int prompt_len, int n_visual);
+
+int std_select_topk_probs(const void* probs, long long head_stride, long long row_stride, int dtype,
+                          int n_q, int n_kv, int text_len, int prompt_len,
+                          const int32_t* visual_pos, int n_visual, int k_select,
+                          int32_t* topk_out, double* scores_out,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Compact-index construction: per KV head, the sorted union of the

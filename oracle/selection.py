@@ -108,6 +108,27 @@ def selection_scores(q_text, key, text_start: int, scale: Optional[float] = None
     return scores
 
 
+def scores_from_probs(probs, n_kv: int) -> np.ndarray:
+    """The reference's selection scores from materialised probabilities
+    (std_qwen25vl.py:203-215): one layer's [1, n_q, T, P] attention of the
+    text rows, summed over the query heads of each KV head and over the text
+    rows (fp64 here; exact for fp16 inputs) -> [n_kv, P]."""
+    a = probs
+    if hasattr(a, "detach"):
+        a = a.detach().cpu()
+        if str(a.dtype) in ("torch.bfloat16", "torch.float16"):
+            a = a.float()
+        a = a.numpy()
+    a = np.asarray(a)[0]
+    n_q, t_len, p_len = a.shape
+    out = np.zeros((n_kv, p_len))
+    group = n_q // n_kv
+    for g in range(n_kv):
+        for h in range(g * group, (g + 1) * group):
+            out[g] += a[h].astype(np.float64).sum(axis=0)
+    return out
+
+
 def topk_positions(scores: np.ndarray, visual_positions: Sequence[int], k: int) -> np.ndarray:
     """Per KV head, the k visual positions with the largest score, ties to the
     lowest position, returned sorted ascending (std_qwen25vl.py:219-222 with a

@@ -15,6 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libstdhip.so"
 
 STD_F32 = 0
 STD_BF16 = 1
+STD_F16 = 2
 
 STATUS_NAMES = {
     -1: "STD_E_NULL",
@@ -54,6 +55,9 @@ SIGNATURES = {
     "std_select_topk_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "std_select_topk": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_longlong, c_int,
                                 c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "std_select_topk_probs_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "std_select_topk_probs": (c_int, [c_void_p, c_longlong, c_longlong, c_int, c_int, c_int, c_int, c_int, c_void_p,
+                                      c_int, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "std_build_compact_index": (c_int, [c_void_p, c_int, c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "std_compact_kv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                c_longlong, c_int, c_longlong, c_int, c_int, c_void_p]),

@@ -624,6 +624,135 @@ bool select_shape_ok(int n_q, int n_kv, int text_len, int prompt_len, int text_s
   return true;
 }
 
+// From column partials colpart[rg][g][prompt_len] (fp64, n_rg row groups):
+// the u64 keys of the visual columns, the radix passes, counts and the
+// ordered emission of the k_sel selected positions per KV head.
+int launch_topk(const double* colpart, int n_rg, int n_kv, int prompt_len, const int32_t* vis, int n_vis, int k_sel,
+                int32_t* topk_out, double* scores_out, unsigned long long* keys, unsigned* hist, int2* counts,
+                hipStream_t st) {
+  const int n_cols = n_vis > prompt_len ? n_vis : prompt_len;
+  hipLaunchKernelGGL(sel_keys_kernel, dim3((n_cols + 255) / 256, n_kv), dim3(256), 0, st, colpart, n_rg, n_kv,
+                     prompt_len, vis, n_vis, keys, scores_out, hist);
+  int s = launch_status();
+  if (s) return s;
+  const dim3 tgrid(topk_blocks(n_vis), n_kv);
+  for (int pass = 0; pass < TOPK_PASSES; ++pass) {
+    hipLaunchKernelGGL(sel_topk_hist_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, pass);
+    if ((s = launch_status())) return s;
+  }
+  hipLaunchKernelGGL(sel_topk_count_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, counts,
+                     (int)tgrid.x);
+  if ((s = launch_status())) return s;
+  hipLaunchKernelGGL(sel_topk_emit_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, vis, n_vis, k_sel, n_kv, hist,
+                     counts, topk_out, (int)tgrid.x);
+  return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// Selection from materialised attention probabilities, the reference's input
+// (std_qwen25vl.py:175-231: per layer [1, n_q, T, P] probabilities of the text
+// suffix's rows over the prompt, summed over the query heads of each KV head
+// and the text rows, then top-k over the visual columns). colpart[rg][g][j] =
+// the fp64 sum of column j over row group rg's probability rows (row r = head
+// r / T of the group, text row r % T), rows in order; the keys stage adds the
+// row groups in order. fp64 holds any sum of fp16 probabilities exactly, so
+// the scores and the selected positions do not depend on the summation order.
+// grid (ceil(P / 1024), n_kv, n_rg), block 256: thread t sums columns
+// 4 (blockIdx.x * 256 + t) .. +3.
+template <typename T>
+__device__ __forceinline__ double prob_to_f64(T x);
+template <> __device__ __forceinline__ double prob_to_f64<float>(float x) { return (double)x; }
+template <> __device__ __forceinline__ double prob_to_f64<bf16_t>(bf16_t x) { return (double)bf16_to_f32(x); }
+struct f16_bits {
+  uint16_t v;
+};
+template <> __device__ __forceinline__ double prob_to_f64<f16_bits>(f16_bits x) {
+  return (double)(float)__builtin_bit_cast(_Float16, x.v);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+probs_colsum_kernel(const T* __restrict__ probs, long long head_stride, long long row_stride, int group, int text_len,
+                    int prompt_len, int rows_per_rg, double* __restrict__ colpart, int n_kv) {
+  const int g = blockIdx.y, rg = blockIdx.z;
+  const int j0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (j0 >= prompt_len) return;
+  const int R = group * text_len;
+  const int r0 = rg * rows_per_rg, r1 = min(R, r0 + rows_per_rg);
+  const bool full = j0 + 4 <= prompt_len;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 8
+  for (int r = r0; r < r1; ++r) {
+    const int hl = r / text_len, t = r - hl * text_len;
+    const T* row = probs + (long long)(g * group + hl) * head_stride + (long long)t * row_stride + j0;
+    T x[4];
+    if (full) {
+      if constexpr (sizeof(T) == 2) {
+        const uint2 u = *reinterpret_cast<const uint2*>(row);
+        x[0] = __builtin_bit_cast(T, (uint16_t)(u.x & 0xffffu));
+        x[1] = __builtin_bit_cast(T, (uint16_t)(u.x >> 16));
+        x[2] = __builtin_bit_cast(T, (uint16_t)(u.y & 0xffffu));
+        x[3] = __builtin_bit_cast(T, (uint16_t)(u.y >> 16));
+      } else {
+        const float4 u = *reinterpret_cast<const float4*>(row);
+        x[0] = __builtin_bit_cast(T, u.x);
+        x[1] = __builtin_bit_cast(T, u.y);
+        x[2] = __builtin_bit_cast(T, u.z);
+        x[3] = __builtin_bit_cast(T, u.w);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = row[min(e, prompt_len - 1 - j0)];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += prob_to_f64<T>(x[e]);
+  }
+  double* dst = colpart + ((long long)rg * n_kv + g) * prompt_len + j0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (j0 + e < prompt_len) dst[e] = acc[e];
+}
+
+struct ProbsPlan {
+  int n_rg, rows_per_rg, n_tb;
+  size_t off_col, off_keys, off_hist, off_cnt, total;
+};
+
+ProbsPlan plan_probs(int n_q, int n_kv, int text_len, int prompt_len, int n_vis) {
+  ProbsPlan p;
+  const int R = (n_q / n_kv) * text_len;
+  const int n_cb = (prompt_len + 1023) / 1024;
+  int n_rg = 2048 / (n_cb * n_kv);                      // about 2048 workgroups (8 per CU)
+  n_rg = n_rg < 1 ? 1 : n_rg > 64 ? 64 : n_rg;
+  n_rg = n_rg > R ? R : n_rg;
+  p.rows_per_rg = (R + n_rg - 1) / n_rg;
+  p.n_rg = (R + p.rows_per_rg - 1) / p.rows_per_rg;
+  p.n_tb = topk_blocks(n_vis);
+  p.off_col = 0;
+  p.off_keys = round_up((size_t)p.n_rg * n_kv * prompt_len * sizeof(double), 256);
+  p.off_hist = round_up(p.off_keys + (size_t)n_kv * n_vis * sizeof(unsigned long long), 256);
+  p.off_cnt = round_up(p.off_hist + (size_t)TOPK_PASSES * n_kv * 256 * sizeof(unsigned), 256);
+  p.total = round_up(p.off_cnt + (size_t)n_kv * p.n_tb * sizeof(int2), 256);
+  return p;
+}
+
+template <typename T>
+int launch_select_probs(const void* probs, long long head_stride, long long row_stride, int n_q, int n_kv,
+                        int text_len, int prompt_len, const int32_t* vis, int n_vis, int k_sel, int32_t* topk_out,
+                        double* scores_out, void* ws, hipStream_t st) {
+  const ProbsPlan p = plan_probs(n_q, n_kv, text_len, prompt_len, n_vis);
+  char* base = static_cast<char*>(ws);
+  double* colpart = reinterpret_cast<double*>(base + p.off_col);
+  hipLaunchKernelGGL((probs_colsum_kernel<T>), dim3((prompt_len + 1023) / 1024, n_kv, p.n_rg), dim3(256), 0, st,
+                     static_cast<const T*>(probs), head_stride, row_stride, n_q / n_kv, text_len, prompt_len,
+                     p.rows_per_rg, colpart, n_kv);
+  const int s = launch_status();
+  if (s) return s;
+  return launch_topk(colpart, p.n_rg, n_kv, prompt_len, vis, n_vis, k_sel, topk_out, scores_out,
+                     reinterpret_cast<unsigned long long*>(base + p.off_keys),
+                     reinterpret_cast<unsigned*>(base + p.off_hist), reinterpret_cast<int2*>(base + p.off_cnt), st);
+}
+
 template <typename T>
 int launch_select(const void* q_text, const void* k, int n_q, int n_kv, int text_len, int prompt_len, int text_start,
                   long long k_hs, const int32_t* vis, int n_vis, int k_sel, int32_t* topk_out, double* scores_out,
@@ -649,21 +778,8 @@ int launch_select(const void* q_text, const void* k, int n_q, int n_kv, int text
   hipLaunchKernelGGL((sel_colsum_kernel<T>), dim3(p.n_kb2, n_kv, p.n_rg2), dim3(P2_THREADS), 0, st, qt, kk, lse, colpart,
                      group, text_len, prompt_len, text_start, k_hs, scale, p.kpb2, n_kv);
   if ((s = launch_status())) return s;
-  const int n_cols = n_vis > prompt_len ? n_vis : prompt_len;
-  hipLaunchKernelGGL(sel_keys_kernel, dim3((n_cols + 255) / 256, n_kv), dim3(256), 0, st, colpart, p.n_rg2, n_kv,
-                     prompt_len, vis, n_vis, keys, scores_out, hist);
-  if ((s = launch_status())) return s;
-  const dim3 tgrid(p.n_tb, n_kv);
-  for (int pass = 0; pass < TOPK_PASSES; ++pass) {
-    hipLaunchKernelGGL(sel_topk_hist_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, pass);
-    if ((s = launch_status())) return s;
-  }
-  hipLaunchKernelGGL(sel_topk_count_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, n_vis, k_sel, n_kv, hist, counts,
-                     (int)tgrid.x);
-  if ((s = launch_status())) return s;
-  hipLaunchKernelGGL(sel_topk_emit_kernel, tgrid, dim3(TOPK_THREADS), 0, st, keys, vis, n_vis, k_sel, n_kv, hist,
-                     counts, topk_out, (int)tgrid.x);
-  return launch_status();
+  return launch_topk(colpart, p.n_rg2, n_kv, prompt_len, vis, n_vis, k_sel, topk_out, scores_out, keys, hist, counts,
+                     st);
 }
 
 }  // namespace
@@ -726,4 +842,36 @@ extern "C" int std_compact_kv(const void* dense_k, const void* dense_v, void* sp
                      idx, compact_len, row_bytes, dense_head_stride * es, dense_rows, sparse_head_stride * es,
                      sparse_rows);
   return launch_status();
+}
+
+extern "C" size_t std_select_topk_probs_workspace_bytes(int n_q, int n_kv, int text_len, int prompt_len,
+                                                        int n_visual) {
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || text_len < 1 || prompt_len < 1 || n_visual < 1) return 0;
+  return plan_probs(n_q, n_kv, text_len, prompt_len, n_visual).total;
+}
+
+extern "C" int std_select_topk_probs(const void* probs, long long head_stride, long long row_stride, int dtype,
+                                     int n_q, int n_kv, int text_len, int prompt_len, const int32_t* visual_pos,
+                                     int n_visual, int k_select, int32_t* topk_out, double* scores_out,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (!probs || !visual_pos || !topk_out || !workspace) return STD_E_NULL;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || text_len < 1 || prompt_len < 1) return STD_E_SHAPE;
+  if (n_visual < 1 || n_visual > prompt_len || k_select < 1 || k_select > n_visual) return STD_E_SHAPE;
+  if (row_stride < prompt_len || head_stride < row_stride * text_len) return STD_E_SHAPE;
+  if (workspace_bytes < plan_probs(n_q, n_kv, text_len, prompt_len, n_visual).total) return STD_E_WORKSPACE;
+  // four-column loads: 8-byte (16-bit types) or 16-byte (fp32) aligned rows
+  const int es = dtype == STD_F32 ? 4 : 2;
+  if (!aligned16(workspace) || ((uintptr_t)probs % (4 * es)) != 0 || (row_stride * es) % (4 * es) != 0 ||
+      (head_stride * es) % (4 * es) != 0)
+    return STD_E_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == STD_F16)
+    return launch_select_probs<f16_bits>(probs, head_stride, row_stride, n_q, n_kv, text_len, prompt_len, visual_pos,
+                                         n_visual, k_select, topk_out, scores_out, workspace, st);
+  if (dtype == STD_BF16)
+    return launch_select_probs<bf16_t>(probs, head_stride, row_stride, n_q, n_kv, text_len, prompt_len, visual_pos,
+                                       n_visual, k_select, topk_out, scores_out, workspace, st);
+  return launch_select_probs<float>(probs, head_stride, row_stride, n_q, n_kv, text_len, prompt_len, visual_pos,
+                                    n_visual, k_select, topk_out, scores_out, workspace, st);
 }

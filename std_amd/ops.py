@@ -294,6 +294,42 @@ def select_topk(q_text: torch.Tensor, key: torch.Tensor, text_start: int, visual
     return (topk, scores) if return_scores else topk
 
 
+def select_topk_probs(probs: torch.Tensor, visual_positions: torch.Tensor, k: int, num_key_value_heads: int,
+                      return_scores: bool = False):
+    """Per-KV-head top-k visual positions from one layer's materialised
+    attention probabilities, the reference's selection input
+    (build_sparse_selection, std_qwen25vl.py:175-231).
+
+    probs [1, n_q, T, P] (fp16 as the reference produces them, bf16 or fp32;
+    columns contiguous, any head/row strides); visual_positions int32
+    [n_visual] ascending. Returns int32 [n_kv, k] ascending (and the fp64
+    group sums [n_kv, P] if requested); ties go to the lowest position."""
+    dev = _check_device(probs, visual_positions)
+    codes = {torch.float16: _lib.STD_F16, torch.bfloat16: _lib.STD_BF16, torch.float32: _lib.STD_F32}
+    if probs.dtype not in codes:
+        raise TypeError(f"unsupported probability dtype {probs.dtype}")
+    if probs.dim() != 4 or probs.shape[0] != 1 or probs.stride(3) != 1:
+        raise ValueError(f"probs must be [1, n_q, T, P] with contiguous columns, got {tuple(probs.shape)}")
+    if visual_positions.dtype != torch.int32 or visual_positions.dim() != 1:
+        raise TypeError("visual_positions must be a 1-D int32 tensor")
+    visual_positions = visual_positions.contiguous()
+    _, n_q, text_len, prompt_len = probs.shape
+    if n_q % num_key_value_heads:
+        raise ValueError(f"Query heads ({n_q}) must be divisible by KV heads ({num_key_value_heads}).")
+    n_vis = visual_positions.numel()
+    if not (1 <= k <= n_vis):
+        raise ValueError(f"k={k} must be in [1, n_visual={n_vis}]")
+    lib = _lib.load_library()
+    ws_bytes = lib.std_select_topk_probs_workspace_bytes(n_q, num_key_value_heads, text_len, prompt_len, n_vis)
+    ws_ptr, ws = _workspace(ws_bytes, dev)
+    topk = torch.empty(num_key_value_heads, k, dtype=torch.int32, device=dev)
+    scores = torch.empty(num_key_value_heads, prompt_len, dtype=torch.float64, device=dev) if return_scores else None
+    _lib.call("std_select_topk_probs", probs.data_ptr(), probs.stride(1), probs.stride(2), codes[probs.dtype], n_q,
+              num_key_value_heads, text_len, prompt_len, visual_positions.data_ptr(), n_vis, int(k), topk.data_ptr(),
+              scores.data_ptr() if scores is not None else None, ws_ptr, ws_bytes, _stream(dev))
+    return (topk, scores) if return_scores else topk
+
+
 def build_compact_index(non_visual: torch.Tensor, topk: torch.Tensor) -> torch.Tensor:
     """Sorted union of the non-visual positions and each head's top-k
     (std_qwen25vl.py:286-291). Returns int32 [n_kv, n_nonvisual + k]."""

@@ -33,7 +33,9 @@ import torch
 from . import ops
 from .kv_cache import KVCache, fill_cache_length, initialize_past_key_values
 
-SPARSE_ATTN_MODES = {"hip"}
+# "hip" and the reference's three mode names (std_qwen25vl.py:239-240), which
+# all compute the same draft attention: each runs the HIP decode kernel here.
+SPARSE_ATTN_MODES = {"hip", "gqa_sdpa", "triton_gqa", "repeat_sdpa"}
 # "compact": the selected prompt rows are copied into the sparse cache
 # (compact_sparse_prompt_cache, std_qwen25vl.py:265-298); "indexed": the draft
 # reads them from the dense cache through the per-head index lists (no copy;
@@ -159,10 +161,44 @@ def prefill_prompt(model, inputs: Dict[str, torch.Tensor], past_key_values, vide
 # ---------------------------------------------------------------------------
 # Selection and compaction.
 
-def build_sparse_selection(text_queries, key_caches, full_input_ids: torch.Tensor, video_token_id: int,
-                           text_start: int, target_k_plus_text: int = 1024, explicit_k: Optional[int] = None,
+def build_sparse_selection(attentions, full_input_ids: torch.Tensor, video_token_id: int, text_start: int,
+                           target_k_plus_text: int = 1024, explicit_k: Optional[int] = None,
                            num_key_value_heads: int = 4) -> SparseSelection:
-    """Top-k visual positions per (layer, KV head) (std_qwen25vl.py:175-231).
+    """Top-k visual positions per (layer, KV head) from the prefill's
+    materialised attention probabilities: the reference's signature and input
+    (std_qwen25vl.py:175-231). attentions[l]: [1, Hq, T, P] probabilities of
+    the text suffix's rows over the prompt (fp16 as the reference's attention
+    returns them, bf16 or fp32), on the device. Each layer's group and
+    text-row sums (fp64) and the top-k run on the device; ties go to the
+    lowest position. build_sparse_selection_from_queries is the fast path that
+    never materialises the probabilities."""
+    prompt_ids = full_input_ids[0]
+    if len(attentions) == 0:
+        raise ValueError("no attention layers")
+    dev = attentions[0].device
+    visual = torch.nonzero(prompt_ids == video_token_id, as_tuple=False).flatten()
+    if visual.numel() == 0:
+        raise ValueError("Cannot build sparse selection without visual/video token positions.")
+    non_visual = torch.nonzero(prompt_ids != video_token_id, as_tuple=False).flatten()
+    prompt_len = int(prompt_ids.numel())
+    text_len, k = selection_k(prompt_len, text_start, visual.numel(), target_k_plus_text, explicit_k)
+    visual_i32 = visual.to(dev, torch.int32)
+    layers = []
+    for layer_attn in attentions:
+        attn = layer_attn.detach()
+        if attn.shape[-1] != prompt_len:
+            raise ValueError(f"attention columns {attn.shape[-1]} != prompt length {prompt_len}")
+        layers.append(ops.select_topk_probs(attn, visual_i32, k, num_key_value_heads))
+    return SparseSelection(topk_device=torch.stack(layers), non_visual_positions=non_visual.to("cpu", torch.int64),
+                           prompt_len=prompt_len, visual_len=int(visual.numel()), text_len=text_len, k=k)
+
+
+def build_sparse_selection_from_queries(text_queries, key_caches, full_input_ids: torch.Tensor, video_token_id: int,
+                                        text_start: int, target_k_plus_text: int = 1024,
+                                        explicit_k: Optional[int] = None,
+                                        num_key_value_heads: int = 4) -> SparseSelection:
+    """Top-k visual positions per (layer, KV head) (std_qwen25vl.py:175-231)
+    without materialising the probabilities.
 
     text_queries[l]: [1, Hq, T, D] text-suffix queries of layer l (RoPE
     applied); key_caches[l]: [1, Hkv, >= P, D] cache view of layer l. The
@@ -531,9 +567,10 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     stage = _profile_mark(profile_prefill)
     queries = model.captured_queries
     model.captured_queries = [None] * model.config.num_hidden_layers
-    selection = build_sparse_selection(queries, [layer[0].data for layer in dense_pkv], prompt_ids, video_token_id,
-                                       text_start, target_k_plus_text=target_k_plus_text, explicit_k=explicit_k,
-                                       num_key_value_heads=model.config.num_key_value_heads)
+    selection = build_sparse_selection_from_queries(queries, [layer[0].data for layer in dense_pkv], prompt_ids,
+                                                    video_token_id, text_start, target_k_plus_text=target_k_plus_text,
+                                                    explicit_k=explicit_k,
+                                                    num_key_value_heads=model.config.num_key_value_heads)
     del queries
     selection_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
     controller = SparseDraftController(model, selection, sparse_attn_mode=sparse_attn_mode, use_compile=use_compile)

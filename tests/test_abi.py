@@ -131,6 +131,26 @@ def test_verify_collect_validation():
     assert call(wsb=10) == -4
 
 
+def test_select_probs_validation():
+    lib = _lib.load_library()
+    P, T = 4096, 128
+    assert lib.std_select_topk_probs_workspace_bytes(28, 4, T, P, P - T) > 0
+    ok = dict(p=16, hs=T * P, rs=P, dt=2, nq=28, nkv=4, t=T, pl=P, vis=16, nv=P - T, k=896, out=16, sc=NULL, ws=16,
+              wsb=1 << 30, st=NULL)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return lib.std_select_topk_probs(*a.values())
+    assert call(dt=5) == -2
+    assert call(vis=NULL) == -1
+    assert call(k=P) == -3                      # k above the visual count
+    assert call(rs=P - 1) == -3                 # rows overlap
+    assert call(nkv=5) == -3                    # 28 % 5
+    assert call(p=18) == -5                     # fp16 rows read four columns (8 bytes) at a time
+    assert call(rs=P + 2, hs=T * (P + 2)) == -5
+    assert call(wsb=100) == -4
+
+
 def test_select_validation():
     lib = _lib.load_library()
     hs = 4096 * 128

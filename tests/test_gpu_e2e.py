@@ -8,8 +8,9 @@ import torch
 from oracle import selection as ref_sel
 from std_amd.decoder import DecoderConfig, RandomDecoder
 from std_amd.kv_cache import initialize_past_key_values
-from std_amd.std_qwen25vl import (ar_generate_qwen25vl, build_sparse_selection, compact_sparse_prompt_cache,
-                                  first_divergence, prefill_prompt, std_generate_qwen25vl)
+from std_amd.std_qwen25vl import (ar_generate_qwen25vl, build_sparse_selection_from_queries,
+                                  compact_sparse_prompt_cache, first_divergence, prefill_prompt,
+                                  std_generate_qwen25vl)
 from tests.gpu_helpers import announce, dev
 
 pytestmark = pytest.mark.gpu
@@ -42,8 +43,9 @@ def test_selection_and_compaction_from_prefill(tiny32):
     prompt_ids, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
     queries = list(model.captured_queries)
     assert text_start == N_VISUAL and queries[0].shape == (1, 7, N_TEXT, 128)
-    sel = build_sparse_selection(queries, [layer[0].data for layer in pkv], prompt_ids, cfg.video_token_id,
-                                 text_start, target_k_plus_text=TARGET, num_key_value_heads=1)
+    sel = build_sparse_selection_from_queries(queries, [layer[0].data for layer in pkv], prompt_ids,
+                                              cfg.video_token_id, text_start, target_k_plus_text=TARGET,
+                                              num_key_value_heads=1)
     want = ref_sel.build_sparse_selection([q.cpu() for q in queries], [layer[0].data[:, :, :P].cpu() for layer in pkv],
                                           prompt_ids[0].cpu().tolist(), cfg.video_token_id, target_k_plus_text=TARGET)
     assert (sel.k, sel.text_len, sel.visual_len, sel.prompt_len) == (want["k"], want["text_len"],

@@ -81,16 +81,19 @@ def test_sparse_selection_host_mirror():
 
 
 def test_controller_validates_mode():
-    """std_qwen25vl.py:239-240 raises ValueError on an unknown mode."""
+    """std_qwen25vl.py:239-240 raises ValueError on an unknown mode; the
+    reference's three mode names are accepted (each runs the HIP kernel) as
+    well as "hip", and the reference's default needs no argument change."""
     class Model:
         sparse_controller = None
     sel = SparseSelection(torch.zeros(1, 1, 1, dtype=torch.int32), torch.tensor([0]), 2, 1, 1, 1)
     with pytest.raises(ValueError, match="sparse_attn_mode"):
-        SparseDraftController(Model(), sel, sparse_attn_mode="triton_gqa")
-    m = Model()
-    c = SparseDraftController(m, sel, sparse_attn_mode="hip")
-    c.install()
-    assert m.sparse_controller is c and not c.enabled
+        SparseDraftController(Model(), sel, sparse_attn_mode="flash")
+    for mode in ("hip", "gqa_sdpa", "triton_gqa", "repeat_sdpa"):
+        m = Model()
+        c = SparseDraftController(m, sel, sparse_attn_mode=mode)
+        c.install()
+        assert m.sparse_controller is c and not c.enabled
     c.set_enabled(True)
     assert c.enabled
 

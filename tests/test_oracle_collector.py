@@ -69,3 +69,37 @@ def test_keys_outside_the_visual_set_change_nothing():
     k[0, :, :4] += 100.0
     k[0, :, 9:] -= 100.0
     np.testing.assert_allclose(verification_scores(q, k, vis), a, rtol=1e-13)
+
+
+def test_probability_scores_equal_the_exact_score_path():
+    """scores_from_probs on the causal text-row probabilities (built here from
+    q and k) equals selection_scores, which never materialises them."""
+    from oracle.selection import scores_from_probs, selection_scores
+    rng = np.random.default_rng(3)
+    n_q, n_kv, T, P, d = 6, 2, 5, 19, 8
+    q = rng.standard_normal((1, n_q, T, d))
+    k = rng.standard_normal((1, n_kv, P, d))
+    text_start = P - T
+    probs = np.zeros((1, n_q, T, P))
+    for h in range(n_q):
+        g = h // (n_q // n_kv)
+        for t in range(T):
+            lim = text_start + t
+            z = q[0, h, t] @ k[0, g, :lim + 1].T / np.sqrt(d)
+            w = np.exp(z - z.max())
+            probs[0, h, t, :lim + 1] = w / w.sum()
+    np.testing.assert_allclose(scores_from_probs(probs, n_kv), selection_scores(q, k, text_start), rtol=1e-12,
+                               atol=1e-15)
+
+
+def test_probability_scores_are_exact_sums_of_fp16_values():
+    """fp16 probabilities: the fp64 group sum is exact, so any summation order
+    gives the same bits (the device sums in another order)."""
+    import torch
+    from oracle.selection import scores_from_probs
+    g = torch.Generator().manual_seed(5)
+    probs = torch.rand(1, 7, 33, 101, generator=g).to(torch.float16)
+    s = scores_from_probs(probs, 1)
+    a = probs.double().numpy()[0]
+    rev = a[::-1, ::-1].sum(axis=(0, 1))           # the rows in reverse order
+    assert np.array_equal(s[0], rev)
