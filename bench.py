@@ -346,6 +346,23 @@ def main():
     dense_decode_graph, _ = capture(dense_decode_only)
     dense_decode_us = time_graph(dense_decode_graph, 5, L)
     del dense_decode_graph
+    # Streaming-read ceiling on this device, in the same process: 256 MiB reads
+    # over 8 distinct buffers in the two fastest patterns of the stream
+    # workload (LDS DMA ring with three tiles in flight and vector loads, both
+    # dealing tiles round-robin); the attention kernels are also reported as a
+    # fraction of it.
+    sbufs = [torch.ones((256 << 20) // 4, dtype=torch.int32, device=dev) for _ in range(8)]
+    ssink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    ceiling = {}
+    for mode, n_wg in ((5, 256), (1, 1024)):
+        def reads(mode=mode, n_wg=n_wg):
+            for b in sbufs:
+                ops.stream_read(b, mode, n_wg, ssink)
+        g_s, _ = capture(reads)
+        ceiling[f"mode{mode}_wg{n_wg}"] = (256 << 20) / (time_graph(g_s, 10, 8) * 1e-6) / 1e9
+        del g_s
+    del sbufs
+    stream_ceiling = max(ceiling.values())
     # Cold: each copy follows a 1 GiB write that evicts the caches; the time of
     # the writes alone (same graph shape) is subtracted.
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -413,6 +430,13 @@ def main():
         "verify_attn_us_per_layer": round(verify_call_us, 3),
         "verify_hbm_gbps": round(verify_gbps, 1),
         "verify_pct_peak": round(100 * verify_gbps / HBM_PEAK_GBPS, 2),
+        "stream_ceiling_gbps": round(stream_ceiling, 1),
+        "stream_ceiling_by_pattern_gbps": {k_: round(v_, 1) for k_, v_ in ceiling.items()},
+        "verify_pct_ceiling": round(100 * verify_gbps / stream_ceiling, 2),
+        "dense_decode_pct_ceiling": round(100 * draft_bytes(Hq, Hkv, P, D, es) / (dense_decode_us * 1e-6) / 1e9
+                                          / stream_ceiling, 2),
+        "draft_one_launch_pct_ceiling_cold": round(100 * L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9
+                                                   / stream_ceiling, 2),
         "verify_collect_us_per_layer": round(verify_collect_us, 3),
         "collector_overhead_us_per_layer": round(verify_collect_us - verify_call_us, 3),
         "collector_extra_bytes_per_layer": coll_extra_bytes(Hkv, Q, V),
@@ -662,67 +686,118 @@ def run_stream(args) -> None:
                       "best": best, "results": results}))
 
 
-def cpu_baseline(w, L):
-    """The oracle (fp32 numpy/BLAS restatement of the reference operators) on
-    the host cores over the whole round, twice: every layer's verify attention
-    at the full context and gamma draft decode steps over the compact cache
-    (each layer timed over `reps` repetitions, mean taken), plus one accept."""
-    import numpy as np
-    import torch
-
-    from oracle import accept as ref_accept
-    from oracle import attention as ref_attn
-    from std_amd.workloads import make_layer, make_logits
+def _cpu_model() -> str:
+    """The host CPU's model name as lscpu reports it (else /proc/cpuinfo)."""
+    import subprocess
 
     try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    sample_layers, reps = L, 3
-    t_verify = t_draft = 0.0
-    for l in range(sample_layers):
-        x = make_layer(w, l)
-        kf = torch.cat([x["k"], x["new_k"]], 2).float().numpy()
-        vf = torch.cat([x["v"], x["new_v"]], 2).float().numpy()
-        qv = x["q_verify"].float().numpy()
-        qd = x["q_draft"].float().numpy()
-        ks, vs = kf[:, :, :w.compact_len], vf[:, :, :w.compact_len]
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            ref_attn.verify_attention(qv, kf, vf, dtype=np.float32)
-            t_verify += (time.perf_counter() - t0) / reps
-            t0 = time.perf_counter()
-            for _ in range(w.gamma):
-                ref_attn.gqa_sdpa(qd, ks, vs, dtype=np.float32)
-            t_draft += (time.perf_counter() - t0) / reps
-    logits = make_logits(w, w.gamma + 1, seed=1).float().numpy()
-    t0 = time.perf_counter()
-    preds = ref_accept.verify_predictions(logits, True)
-    ref_accept.greedy_prefix(preds[:w.gamma], preds)
-    t_accept = time.perf_counter() - t0
-    round_s = (t_verify + t_draft) * L / sample_layers + t_accept
-    cpu_name = platform.processor() or ""
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu_name = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(w, L):
+    """The reference's own torch operators on the host CPU in fp32 (the
+    oracle's torch_cpu restatements: F.scaled_dot_product_attention with
+    enable_gqa for the draft, math SDPA with the offset-causal mask for the
+    verify, argmax + prefix for the accept), timed on one layer's inputs of
+    the workload (bf16 values upcast): 3 warm-ups then the median of 10 calls
+    with torch's thread count, and 1 warm-up then the median of 3 with one
+    thread; one round = L x (verify + gamma draft steps) + one accept."""
+    import torch
+
+    from oracle import torch_cpu
+    from std_amd.workloads import make_layer, make_logits
+
+    x = make_layer(w, 0)
+    Q = w.gamma + 1
+    kv_len = w.prompt_len + Q
+    # The verify is timed over a bounded sample of the keys (the first prompt
+    # keys and the Q new rows, which carry the offset-causal part) and scaled
+    # by kv_len / kv_sample: its cost is linear in the key count.
+    kv_sample = min(kv_len, 16384 + Q)
+    n_prompt = kv_sample - Q
+    kf = torch.cat([x["k"][:, :, :n_prompt], x["new_k"]], 2).float()
+    vf = torch.cat([x["v"][:, :, :n_prompt], x["new_v"]], 2).float()
+    verify_scale = kv_len / kv_sample
+    qv = x["q_verify"].float()
+    qd = x["q_draft"].float()
+    ks = x["k"][:, :, :w.compact_len].float().contiguous()
+    vs = x["v"][:, :, :w.compact_len].float().contiguous()
+    logits = make_logits(w, w.gamma + 1, seed=1).float()
+    preds = torch.argmax(logits, dim=-1).tolist()
+    draft = preds[:w.gamma]
+
+    counts = {}
+
+    def median_time(name, fn, warm, reps, budget_s):
+        """warm warm-ups and the median of reps calls, both cut down (to at
+        least one warm-up and three calls) when one call would overrun
+        budget_s; the counts used are recorded."""
+        t0 = time.perf_counter()
+        fn()
+        first = time.perf_counter() - t0
+        warm = max(1, min(warm, int(budget_s / 4 / max(first, 1e-9))))
+        reps = max(3, min(reps, int(budget_s / max(first, 1e-9))))
+        for _ in range(warm - 1):
+            fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        counts[name] = (warm, reps)
+        return statistics.median(ts)
+
+    def round_seconds(tag, warm, reps, budget_s):
+        t_v = verify_scale * median_time("verify" + tag, lambda: torch_cpu.verify_attention(qv, kf, vf), warm, reps,
+                                         budget_s)
+        t_d = median_time("draft" + tag, lambda: torch_cpu.gqa_sdpa(qd, ks, vs), warm, reps, budget_s)
+        t_a = median_time("accept" + tag, lambda: torch_cpu.greedy_accept(logits, draft, True), warm, reps, budget_s)
+        return L * (t_v + w.gamma * t_d) + t_a, t_v, t_d, t_a
+
+    threads = torch.get_num_threads()
+    t0 = time.perf_counter()
+    r_all, v_all, d_all, a_all = round_seconds("", 3, 10, 8.0)
+    torch.set_num_threads(1)
+    try:
+        r_one, v_one, d_one, _ = round_seconds("_1_thread", 1, 3, 4.0)
+    finally:
+        torch.set_num_threads(threads)
+    sample_s = time.perf_counter() - t0
     return {
-        "value": round(w.gamma / round_s, 3),
+        "value": round(w.gamma / r_all, 3),
         "unit": "draft tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{sample_layers} of {L} layers (verify q={w.gamma + 1} over {w.prompt_len + w.gamma + 1} keys, "
-                  f"{w.gamma} draft steps over {w.compact_len} keys), each timed {reps}x (mean), + 1 accept over "
-                  f"{w.vocab} x {w.gamma + 1}, fp32 numpy oracle, scaled x{L / sample_layers:g}; host CPU: {cpu_name}",
-        "sample_seconds": round((t_verify + t_draft) * reps + t_accept, 2),
-        "verify_ms_per_layer": round(t_verify * 1e3 / sample_layers, 2),
-        "draft_ms_per_layer_step": round(t_draft * 1e3 / (sample_layers * w.gamma), 3),
+        "sample": f"one layer of the workload (verify q={Q} over {kv_len} keys, timed over {kv_sample} of them and "
+                  f"scaled x{verify_scale:.3f}; one draft step over {w.compact_len} keys; one accept over {Q} x "
+                  f"{w.vocab} logits), torch "
+                  f"fp32 on the CPU, 3 warm-ups + median of 10 ({threads} threads) and 1 + median of 3 (1 thread), "
+                  f"fewer where one call would overrun the leg's time budget (see warmups_reps); "
+                  f"round = {L} x (verify + {w.gamma} draft steps) + accept",
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "threads": threads,
+        "value_1_thread": round(w.gamma / r_one, 3),
+        "verify_ms_per_layer": round(v_all * 1e3, 3),
+        "draft_ms_per_layer_step": round(d_all * 1e3, 4),
+        "accept_ms": round(a_all * 1e3, 3),
+        "verify_ms_per_layer_1_thread": round(v_one * 1e3, 3),
+        "draft_ms_per_layer_step_1_thread": round(d_one * 1e3, 4),
+        "warmups_reps": {name: list(c) for name, c in counts.items()},
+        "sample_seconds": round(sample_s, 2),
     }
 
 

@@ -103,3 +103,27 @@ def test_probability_scores_are_exact_sums_of_fp16_values():
     a = probs.double().numpy()[0]
     rev = a[::-1, ::-1].sum(axis=(0, 1))           # the rows in reverse order
     assert np.array_equal(s[0], rev)
+
+
+def test_torch_cpu_restatements_match_the_numpy_oracle():
+    """The torch-CPU operators timed as the CPU baseline agree with the fp64
+    numpy oracle (fp32 tolerance) on decode, offset-causal verify and accept."""
+    import torch
+    from oracle import accept as np_accept
+    from oracle import attention as np_attn
+    from oracle import torch_cpu
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(1, 28, 1, 128, generator=g)
+    k = torch.randn(1, 4, 300, 128, generator=g)
+    v = torch.randn(1, 4, 300, 128, generator=g)
+    np.testing.assert_allclose(torch_cpu.gqa_sdpa(q, k, v).double().numpy(), np_attn.gqa_sdpa(q, k, v),
+                               rtol=1e-5, atol=1e-6)
+    qv = torch.randn(1, 28, 10, 128, generator=g)
+    np.testing.assert_allclose(torch_cpu.verify_attention(qv, k, v).double().numpy(),
+                               np_attn.verify_attention(qv, k, v), rtol=1e-5, atol=1e-6)
+    logits = torch.randn(10, 1000, generator=g)
+    preds = np_accept.verify_predictions(logits.numpy(), True)
+    draft = preds[:3] + [(preds[3] + 1) % 1000] + preds[4:9]
+    assert torch_cpu.greedy_accept(logits, draft, True) == (3, preds[3])
+    a, bonus, _ = np_accept.verify_accept(logits.numpy(), draft, True)
+    assert (a, bonus) == (3, preds[3])
