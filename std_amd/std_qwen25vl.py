@@ -519,7 +519,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
                           copy_sparse_prefill: bool = True, profile_prefill: bool = False,
                           verify_attn_backend: str = "math", verify_margin_threshold: Optional[float] = None,
                           use_compile: bool = False, ignore_eos: bool = False, use_graphs: bool = False,
-                          sparse_kv: str = "compact") -> Tuple[GenerateResult, SparseSelection]:
+                          sparse_kv: str = "compact", round_hook=None) -> Tuple[GenerateResult, SparseSelection]:
     """Sparse-to-Dense greedy decoding (std_qwen25vl.py:609-978).
 
     use_graphs: keep both caches' lengths and positions on the device (the
@@ -531,7 +531,15 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
 
     sparse_kv: "compact" gathers the selected prompt rows into the sparse
     cache; "indexed" (bf16) has the draft read them from the dense cache
-    through the per-head index lists instead (same keys, same results)."""
+    through the per-head index lists instead (same keys, same results).
+
+    round_hook (a test probe; None adds nothing): called once per round after
+    the rollback with a dict holding that round's verify logits [Q, vocab]
+    (device; with graphs the captured graph's own buffer), draft, has_pending,
+    dense_next, the kernel's accept_len and bonus, the pre-round lengths
+    (dense_cached_len, n_pending, sparse_prev_len) and the rolled-back
+    (dense, sparse) lengths: the device lengths with graphs, else the host
+    lengths."""
     if sparse_kv not in SPARSE_KV_MODES:
         raise ValueError(f"Unsupported sparse_kv={sparse_kv!r}; choose one of {sorted(SPARSE_KV_MODES)}.")
     if sparse_kv == "indexed" and model.dtype != torch.bfloat16:
@@ -606,6 +614,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     # rolled back together by the acceptance kernel.
     st4 = tok_s = pending = None
     graphs = None
+    last_logits = [None]                    # the latest verify logits (round_hook)
     if use_graphs:
         st4 = torch.tensor([prompt_len, prompt_len, sparse_prompt_len, prompt_len], dtype=torch.int32).to(dev)
         tok_s = sparse_next.reshape(1, 1).clone()
@@ -625,6 +634,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     def verify_phase(draft: torch.Tensor, has_pending: bool) -> torch.Tensor:
         ids = torch.cat([pending, draft]) if has_pending else draft
         logits = model(ids.reshape(1, -1), dense_pkv, step_state=st4[0:2], all_logits=True)
+        last_logits[0] = logits[0]
         return ops.greedy_accept(logits[0], draft.to(torch.int32), has_pending=has_pending,
                                  dense_next=None if has_pending else dense_next_i32, rollback_lengths=st4)
 
@@ -660,7 +670,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
 
         caps = _warm_and_capture(run_all, restore, [(draft_static, ()), (verify_static, (True,)),
                                                     (lambda: bonus_phase(holder["res"]), ())])
-        return caps, holder["draft"], holder["res"]
+        return caps, holder["draft"], holder["res"], last_logits[0]     # the verify graph's logits buffer
 
     torch.cuda.synchronize()
     decode_start = time.time()
@@ -694,6 +704,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         if replay:
             graphs[0][1][0].replay()
             res = graphs[2]
+            last_logits[0] = graphs[3]
         elif use_graphs:
             res = verify_phase(draft_dev, bool(dense_pending))
         else:
@@ -703,6 +714,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
             else:
                 verify_ids = draft_dev.reshape(1, -1)
             logits = model(verify_ids, dense_pkv, all_logits=True)
+            last_logits[0] = logits[0]
             res = ops.greedy_accept(logits[0], draft_dev.to(torch.int32), has_pending=bool(dense_pending),
                                     dense_next=None if dense_pending else dense_next_i32)
         host = torch.cat([res[:2], draft_dev.to(torch.int32)]).tolist()     # the round's one readback
@@ -738,6 +750,13 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         fill_cache_length(dense_lengths, dense_cached_len + len(dense_pending) + accept_len)
         fill_cache_length(sparse_lengths, sparse_prev_len + accept_len)
         cache_adjust_time += _profile_mark(profile_decode) - stage
+        if round_hook is not None:
+            lengths = ((int(st4[0]), int(st4[2])) if use_graphs
+                       else (int(dense_lengths[0]), int(sparse_lengths[0])))
+            round_hook(dict(round=decode_rounds, logits=last_logits[0], draft=draft, has_pending=bool(dense_pending),
+                            dense_next=int(dense_next.reshape(-1)[0]), accept_len=accept_len, bonus=bonus_token,
+                            dense_cached_len=dense_cached_len, n_pending=len(dense_pending),
+                            sparse_prev_len=sparse_prev_len, lengths=lengths, replayed=replay))
 
         dense_pending = [bonus_token]
         stage = _profile_mark(profile_decode)
