@@ -408,7 +408,10 @@ int std_gemv_ex(const void* x, long long x_row_stride, const void* w, long long 
  * at position pos_dev[0] + pos_offset + r, rotated queries to q_out
  * [n_q][n_rows][128], rotated keys and the values to cache row len_dev[0] + r
  * (not written at or past capacity). Outputs equal std_gemv_ex followed by
- * std_rope_append bit for bit. With norm_weight (not NULL; one row, K <=
+ * std_rope_append bit for bit when the projection has at least 256 16-column
+ * blocks (n_q + 2 n_kv >= 32 heads, as at 7B): std_gemv then splits K over
+ * four waves like this launch; for narrower projections it splits K over two
+ * waves and elements may differ by one bf16 rounding. With norm_weight (not NULL; one row, K <=
  * 3584) x is the decoder layer's input before its input_layernorm
  * (modeling_qwen2_5_vl.py:1202) and the launch normalises it first, equal to
  * std_rms_norm(x, norm_weight, eps) bit for bit. bf16 only; head_dim 128; the

@@ -81,9 +81,11 @@ def test_graph_replays_equal_eager_round():
 
 def test_decoder_step_graph_replays_equal_eager_at_7b_shapes():
     """A 2-layer decoder with the 7B layer and vocabulary shapes: captured AR
-    and verify steps (device lengths, HIP rope/append + attention, HIP RMSNorm
-    and argmax, torch GEMMs) replay bit-identically to the eager steps, three
-    times, with unrelated eager work between replays."""
+    and verify steps replay bit-identically to the eager steps, three times,
+    with unrelated eager work between replays. Both read their lengths on the
+    device. The AR step is HIP launches only (norm + q/k/v + RoPE + append,
+    attention, o/MLP/lm_head GEMVs, argmax); the verify step's q/k/v and
+    lm_head projections of several rows are torch GEMMs, the rest HIP."""
     from std_amd.decoder import DecoderConfig, RandomDecoder
     from std_amd.kv_cache import initialize_past_key_values
     from std_amd.std_qwen25vl import _token_argmax, _warm_and_capture

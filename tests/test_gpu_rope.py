@@ -129,9 +129,11 @@ def test_attention_devlen_rejects_length_past_plan_with_nan():
                           (2, 3584, 28, 4, 63, 70, 0, 64)])
 def test_qkv_rope_append_equals_projection_then_rope_append(n, K, n_q, n_kv, length, pos, off, cap):
     """The fused projection + rotary + append against the projection (HIP
-    GEMV with bias) followed by rope_append: queries and both caches equal
-    bit for bit, including rows at or past the capacity (not written: the
-    last case's second row)."""
+    GEMV with bias) followed by rope_append, including rows at or past the
+    capacity (not written: the last case's second row). At 256 or more
+    16-column blocks (the 7B shape) both split K over four waves and the
+    results are equal bit for bit; below, the GEMV splits K over two waves, so
+    the sums associate differently and elements may differ by one bf16 ulp."""
     announce(f"qkv_rope_append n={n} K={K} heads={n_q}/{n_kv} len={length} pos={pos}+{off} cap={cap}")
     g = torch.Generator(device=dev()).manual_seed(n * 1000 + K + length)
     NW = (n_q + 2 * n_kv) * D
@@ -144,9 +146,23 @@ def test_qkv_rope_append_equals_projection_then_rope_append(n, K, n_q, n_kv, len
     want = ops.rope_append(ops.linear(x, w, b), n_q, caches[2], caches[3], _scalar(length), _scalar(pos), inv,
                            pos_offset=off)
     torch.cuda.synchronize()
-    assert q.shape == (1, n_q, n, D) and torch.equal(q, want)
-    for got, ref in ((caches[0], caches[2]), (caches[1], caches[3])):
-        assert torch.equal(got.nan_to_num(7.0), ref.nan_to_num(7.0))
+    assert q.shape == (1, n_q, n, D)
+    same_split = NW // 16 >= 256
+    pairs = [(q, want), (caches[0].nan_to_num(7.0), caches[2].nan_to_num(7.0)),
+             (caches[1].nan_to_num(7.0), caches[3].nan_to_num(7.0))]
+    for got, ref in pairs:
+        if same_split:
+            assert torch.equal(got, ref)
+        else:
+            _assert_within_one_bf16_ulp(got, ref)
+
+
+def _assert_within_one_bf16_ulp(a: torch.Tensor, b: torch.Tensor) -> None:
+    """|a - b| <= one bf16 ulp of the larger magnitude, elementwise."""
+    a32, b32 = a.float(), b.float()
+    mag = torch.maximum(a32.abs(), b32.abs()).clamp_min(torch.finfo(torch.bfloat16).tiny)
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)
+    assert ((a32 - b32).abs() <= ulp).all()
 
 
 def test_qkv_rope_append_rejects_bad_arguments():
