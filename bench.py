@@ -85,7 +85,16 @@ def pmc_run(w) -> None:
     for _ in range(5):
         ops.gqa_decode(qd, k[:, :, :S], v[:, :, :S])
     torch.cuda.synchronize()
-    log(f"pmc run done: 5 verify launches (kv={P + Q}), 5 decode launches (kv={S})")
+    V = P - w.text_len
+    scores = torch.empty(Hkv, V, dtype=torch.float32, device=dev)
+    for _ in range(5):
+        ops.verify_attention_collect(qv, k, v, 0, V, kv_len=P + Q, scores=scores)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        ops.gqa_decode(qd, k[:, :, :P], v[:, :, :P])
+    torch.cuda.synchronize()
+    log(f"pmc run done: 5 verify launches (kv={P + Q}), 5 decode launches (kv={S}), 5 verify launches with the "
+        f"collector (visual keys 0..{V}), 5 dense decode launches (kv={P})")
 
 
 def log(msg: str) -> None:
@@ -347,14 +356,14 @@ def main():
     dense_decode_us = time_graph(dense_decode_graph, 5, L)
     del dense_decode_graph
     # Streaming-read ceiling on this device, in the same process: 256 MiB reads
-    # over 8 distinct buffers in the two fastest patterns of the stream
-    # workload (LDS DMA ring with three tiles in flight and vector loads, both
-    # dealing tiles round-robin); the attention kernels are also reported as a
-    # fraction of it.
+    # over 8 distinct buffers in the fastest patterns of the stream workload
+    # (the verify kernel's LDS DMA ring, the decode key split's, and vector
+    # loads, all dealing tiles round-robin); the attention kernels are also
+    # reported as a fraction of it.
     sbufs = [torch.ones((256 << 20) // 4, dtype=torch.int32, device=dev) for _ in range(8)]
     ssink = torch.zeros(4096, dtype=torch.int32, device=dev)
     ceiling = {}
-    for mode, n_wg in ((5, 256), (1, 1024)):
+    for mode, n_wg in ((3, 256), (5, 256), (1, 1024)):
         def reads(mode=mode, n_wg=n_wg):
             for b in sbufs:
                 ops.stream_read(b, mode, n_wg, ssink)

@@ -47,7 +47,7 @@ stream_lds_kernel(const char* __restrict__ ha, const char* __restrict__ hb, int 
   constexpr int kStages = 4;
   constexpr int kHalf = kTileBytes / 2;
   constexpr int kSegs = 16 / WAVES;          // 1 KiB segments of each half per wave per tile
-  static_assert(AHEAD >= 2 && AHEAD <= 3, "two or three tiles in flight");
+  static_assert(AHEAD >= 2 && AHEAD <= kStages, "one to three tiles in flight beside the one being read");
   __shared__ __align__(16) char ring[kStages * kTileBytes];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int b = blockIdx.x;
@@ -75,8 +75,8 @@ stream_lds_kernel(const char* __restrict__ ha, const char* __restrict__ hb, int 
     // tiles issued so far: 0 .. min(u + AHEAD - 2, n - 1); tile u must have landed
     wait_vm_ahead<2 * kSegs>(min(AHEAD - 2, n - 1 - u));
     wg_barrier();
-    // the stage of tile u + AHEAD - 1 last held tile u - 1 (AHEAD 3) or u - 2
-    // (AHEAD 2), which every wave finished before this barrier
+    // the stage of tile u + AHEAD - 1 last held tile u + AHEAD - 5 (<= u - 1),
+    // which every wave finished before this barrier
     if (u + AHEAD - 1 < n) issue(u + AHEAD - 1);
     acc ^= *reinterpret_cast<const uint32_t*>(stage(u) + threadIdx.x * 16);
   }
@@ -115,19 +115,19 @@ extern "C" int std_stream_read(const void* src, size_t bytes, int mode, int n_wo
                          per, n_workgroups, sink);
       break;
     case 2:
-      hipLaunchKernelGGL((stream_lds_kernel<8, 2, false>), grid, dim3(512), 0, st, a, b, ntiles, per, n_workgroups,
+      hipLaunchKernelGGL((stream_lds_kernel<8, 3, false>), grid, dim3(512), 0, st, a, b, ntiles, per, n_workgroups,
                          sink);
       break;
     case 3:
-      hipLaunchKernelGGL((stream_lds_kernel<8, 2, true>), grid, dim3(512), 0, st, a, b, ntiles, per, n_workgroups,
+      hipLaunchKernelGGL((stream_lds_kernel<8, 3, true>), grid, dim3(512), 0, st, a, b, ntiles, per, n_workgroups,
                          sink);
       break;
     case 4:
-      hipLaunchKernelGGL((stream_lds_kernel<4, 3, false>), grid, dim3(256), 0, st, a, b, ntiles, per, n_workgroups,
+      hipLaunchKernelGGL((stream_lds_kernel<4, 4, false>), grid, dim3(256), 0, st, a, b, ntiles, per, n_workgroups,
                          sink);
       break;
     default:
-      hipLaunchKernelGGL((stream_lds_kernel<4, 3, true>), grid, dim3(256), 0, st, a, b, ntiles, per, n_workgroups,
+      hipLaunchKernelGGL((stream_lds_kernel<4, 4, true>), grid, dim3(256), 0, st, a, b, ntiles, per, n_workgroups,
                          sink);
       break;
   }
