@@ -53,8 +53,8 @@ def parse_args():
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cold-iters", type=int, default=10)
     ap.add_argument("--pmc-run", action="store_true",
-                    help="short run for rocprofv3 counter passes: a 1 GiB copy (calibration), then 5 verify and "
-                         "5 draft-decode launches at the workload's shapes")
+                    help="short run for rocprofv3 counter passes: a 1 GiB copy (calibration), then 5 launches each "
+                         "of verify, draft decode, verify with the collector and dense decode at the workload's shapes")
     return ap.parse_args()
 
 
