@@ -112,12 +112,15 @@ struct WsLayout {
   size_t o_off, ml_off, total;
 };
 
-WsLayout ws_layout(int n_kv, int rows, const SplitPlan& p) {
+// part_bytes: 2 for scaled fp16 partials, 4 for fp32 (part_bytes_of).
+int part_bytes_of(int dtype, int rows) { return dtype == STD_BF16 && rows > 16 ? 2 : 4; }
+
+WsLayout ws_layout(int n_kv, int rows, const SplitPlan& p, int part_bytes) {
   WsLayout l{0, 0, 0};
   if (p.n_split <= 1) return l;
   const size_t n = (size_t)n_kv * p.n_split * rows;
   l.o_off = 0;
-  l.ml_off = round_up(l.o_off + n * D * sizeof(float), 256);
+  l.ml_off = round_up(l.o_off + n * D * part_bytes, 256);
   l.total = round_up(l.ml_off + n * sizeof(float2), 256);
   return l;
 }
@@ -194,6 +197,29 @@ __device__ void finish_split(OLoad load_o, const float2* ml_f, T* __restrict__ o
   }
 }
 
+// Scaled fp16 partials (the bf16 kernels with several row tiles, i.e. verify):
+// a split stores its unnormalised row O as P = O 2^-k in fp16, k chosen so
+// that max|P| lies in [2^14, 2^15) (full fp16 precision, no overflow whatever
+// the values), and (m, l) as (m + k, l 2^-k): weighted by 2^(m + k - M'), P
+// contributes exactly what O contributes at 2^(m - M'), so the merge's
+// arithmetic is the same as for fp32 partials, at half the bytes written and
+// read back (128k verify: 9.3 -> 4.7 MB, 0.5 us less per layer). The decodes
+// keep fp32 partials: their few partial bytes save nothing, and the row-max
+// reduction lengthened the latency-bound launches (draft +0.35 us).
+typedef _Float16 half_t;
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int part_exp(float amax) {
+  const int e = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;   // floor(log2 amax) for a normal amax
+  return amax > 0.f ? min(max(e - 14, -100), 100) : 0;
+}
+__device__ __forceinline__ float exp2i(int k) { return __uint_as_float((uint32_t)(127 + k) << 23); }   // |k| <= 126
+
+__device__ __forceinline__ f32x4 load_part(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ f32x4 load_part(const half_t* p) {
+  return __builtin_convertvector(*reinterpret_cast<const half4_t*>(p), f32x4);
+}
+
 // Standalone merge: grid (R, n_kv), block kMergeThreads = 8 split groups x
 // 32 float4 lanes of the head dim. Every load is issued up front (a thread's
 // first kMergePrefetch partials together with the (m, l) statistics), so the
@@ -204,8 +230,8 @@ constexpr int kMergeGroups = 8;
 constexpr int kMergeThreads = kMergeGroups * (D / 4);
 constexpr int kMergePrefetch = 8;
 
-template <typename T>
-__device__ __forceinline__ void merge_row(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml,
+template <typename T, typename PT>
+__device__ __forceinline__ void merge_row(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
                                           T* __restrict__ out, int n_split, int q_len, int group, long long out_bs,
                                           int n_kv, int r, int g) {
   __shared__ float wts[kMaxSplit];
@@ -216,14 +242,14 @@ __device__ __forceinline__ void merge_row(const float* __restrict__ ws_o, const 
   const int R = group * q_len;
   out += blockIdx.z * out_bs;
   const long long base = ((long long)blockIdx.z * n_kv + g) * n_split * R + r;
-  const f32x4* col = reinterpret_cast<const f32x4*>(ws_o + base * D) + d4;
-  const long long step = (long long)R * (D / 4);
+  const PT* col = ws_o + base * D + 4 * d4;
+  const long long step = (long long)R * D;
   // Every load below is issued before the first use: splits past n_split
   // re-read the last one and are masked after the load (a load under a
   // condition would compile to a branch that waits for it).
   f32x4 pre[kMergePrefetch];
 #pragma unroll
-  for (int j = 0; j < kMergePrefetch; ++j) pre[j] = col[min(sg + j * kMergeGroups, n_split - 1) * step];
+  for (int j = 0; j < kMergePrefetch; ++j) pre[j] = load_part(col + min(sg + j * kMergeGroups, n_split - 1) * step);
   constexpr int kMlPerThread = kMaxSplit / kMergeThreads;
   float2 mls[kMlPerThread];
 #pragma unroll
@@ -266,7 +292,7 @@ __device__ __forceinline__ void merge_row(const float* __restrict__ ws_o, const 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int sp = s0 + sg + j * kMergeGroups;
-      v[j] = sp < n_split ? col[sp * step] : f32x4{0.f, 0.f, 0.f, 0.f};
+      v[j] = sp < n_split ? load_part(col + sp * step) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -290,11 +316,11 @@ __device__ __forceinline__ void merge_row(const float* __restrict__ ws_o, const 
   }
 }
 
-template <typename T>
+template <typename T, typename PT>
 __global__ void __launch_bounds__(kMergeThreads)
-attn_merge_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
+attn_merge_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
                   int n_split, int q_len, int group, long long out_bs, int n_kv) {
-  merge_row<T>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y);
+  merge_row<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y);
 }
 
 // Collector finish (the column sums of VerificationCollectorV3._hook,
@@ -367,13 +393,13 @@ __device__ __forceinline__ void coll_finish(const float* __restrict__ logits, co
 // (n_rows + n_col_blocks, n_kv); blocks x < n_rows merge attention row x (none
 // when the verify ran as one split), the others finish 1024 visual keys each.
 __global__ void __launch_bounds__(kMergeThreads)
-merge_coll_kernel(const float* __restrict__ ws_o, const float2* __restrict__ ws_ml, bf16_t* __restrict__ out,
+merge_coll_kernel(const half_t* __restrict__ ws_o, const float2* __restrict__ ws_ml, bf16_t* __restrict__ out,
                   int n_split, int q_len, int group, int n_rows, const float* __restrict__ logits,
                   const float2* __restrict__ stats, float* __restrict__ scores, int n_vtiles, long long score_hs,
                   int vis_begin, int vis_end) {
   static_assert(kMergeThreads == 256, "the collector finish runs 256 threads");
   if ((int)blockIdx.x < n_rows)
-    merge_row<bf16_t>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
+    merge_row<bf16_t, half_t>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
   else
     coll_finish(logits, stats, scores, score_hs, q_len, n_split, n_vtiles, vis_begin, vis_end, blockIdx.x - n_rows,
                 blockIdx.y);
@@ -440,10 +466,13 @@ struct Bf16Cfg {
   static constexpr int kLoadsPerTile = 2 * kSegsPerWave;
 };
 
+template <int NT>
+using PartT = typename std::conditional<(NT > 1), half_t, float>::type;
+
 template <int NT, bool KS, bool GA, bool COLL = false>
 __global__ void __launch_bounds__(NT == 1 ? 256 : 512)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
-                 bf16_t* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
+                 bf16_t* __restrict__ out, PartT<NT>* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                  int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
                  long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev,
@@ -875,9 +904,11 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   auto ks_merge_rows = [&](const char* region, int r0, int nthr, int t0) {
     const float2* mlw = reinterpret_cast<const float2*>(region);
     const float* Ow = reinterpret_cast<const float*>(region + 1024);
+    // Items are row-major and every thread runs the same number of them (nthr
+    // divides 16 * D / 4), so the 32 items of a row sit in 32 consecutive lanes
+    // of one wave: the row's max |O| is a five-step butterfly over them.
     for (int item = t0; item < 16 * (D / 4); item += nthr) {
       const int rl = item / (D / 4), d4 = item % (D / 4), r = r0 + rl;
-      if (r >= R) break;                         // items are row-major: the rest are padding rows
       float2 ml[4];
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) ml[ww] = mlw[ww * 16 + rl];
@@ -892,10 +923,23 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       }
       const int hl = r / q_len, i = r - hl * q_len;
       if (n_split == 1) {
-        bf16_t* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
-        const f32x4 on = o / Lr;
-        *reinterpret_cast<i16x4*>(dst) = pack_bf16x4(on[0], on[1], on[2], on[3]);
-      } else {
+        if (r < R) {
+          bf16_t* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
+          const f32x4 on = o / Lr;
+          *reinterpret_cast<i16x4*>(dst) = pack_bf16x4(on[0], on[1], on[2], on[3]);
+        }
+      } else if constexpr (NT > 1) {
+        float amax = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        if (r < R) {
+          const int kx = part_exp(amax);
+          const float sx = exp2i(-kx);
+          const long long prow = (long long)g * n_split * R + (long long)split * R + r;
+          *reinterpret_cast<half4_t*>(ws_o + prow * D + 4 * d4) = __builtin_convertvector(o * sx, half4_t);
+          if (d4 == 0) ws_ml[prow] = make_float2(Mr + (float)kx, Lr * sx);
+        }
+      } else if (r < R) {
         const long long prow = (long long)g * n_split * R + (long long)split * R + r;
         *reinterpret_cast<f32x4*>(ws_o + prow * D + 4 * d4) = o;
         if (d4 == 0) ws_ml[prow] = make_float2(Mr, Lr);
@@ -999,11 +1043,25 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       const f32x4 o = acc[t] / l_row;
       *reinterpret_cast<i16x4*>(dst + 16 * t) = pack_bf16x4(o[0], o[1], o[2], o[3]);
     }
-  } else {
+  } else if constexpr (NT == 1) {
     const long long prow = (long long)g * n_split * R + (long long)split * R + row;
 #pragma unroll
     for (int t = 0; t < 8; ++t) *reinterpret_cast<f32x4*>(ws_o + prow * D + 16 * t + 4 * lg) = acc[t];
     if (lg == 0) ws_ml[prow] = make_float2(m_run, l_row);
+  } else {
+    // The row's 128 columns are spread over its four lanes (lg).
+    float amax = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(acc[t][0]), fabsf(acc[t][1])), fmaxf(fabsf(acc[t][2]), fabsf(acc[t][3]))));
+    amax = xor32_max(xor16_max(amax));
+    const int kx = part_exp(amax);
+    const float sx = exp2i(-kx);
+    const long long prow = (long long)g * n_split * R + (long long)split * R + row;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      *reinterpret_cast<half4_t*>(ws_o + prow * D + 16 * t + 4 * lg) = __builtin_convertvector(acc[t] * sx, half4_t);
+    if (lg == 0) ws_ml[prow] = make_float2(m_run + (float)kx, l_row * sx);
   }
 }
 
@@ -1252,9 +1310,9 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
               GatherArgs ga, hipStream_t st) {
   const int R = group * q_len;
   const SplitPlan p = plan_splits(n_kv * n_batch, R, kv_len, dtype);
-  const WsLayout wl = ws_layout(n_kv * n_batch, R, p);
+  const WsLayout wl = ws_layout(n_kv * n_batch, R, p, part_bytes_of(dtype, R));
   char* base = static_cast<char*>(ws);
-  float* ws_o = p.n_split > 1 ? reinterpret_cast<float*>(base + wl.o_off) : nullptr;
+  void* ws_o = p.n_split > 1 ? static_cast<void*>(base + wl.o_off) : nullptr;
   float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
   const float scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(p.n_split, n_kv, n_batch);
@@ -1270,23 +1328,26 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
                                                    : attn_bf16_kernel<NT, false, false>);
     hipLaunchKernelGGL(kern, grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
                        static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
-                       static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs, scale_log2,
-                       p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
+                       static_cast<bf16_t*>(out), static_cast<PartT<NT>*>(ws_o), ws_ml, q_len, kv_len, group, k_hs,
+                       v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
                        static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev, ga, ga.idx);
   } else {
     hipLaunchKernelGGL((attn_f32_kernel<NT>), grid, dim3(NTHREADS), 0, st, static_cast<const float*>(q),
-                       static_cast<float*>(k), static_cast<float*>(v), static_cast<float*>(out), ws_o, ws_ml, q_len,
+                       static_cast<float*>(k), static_cast<float*>(v), static_cast<float*>(out),
+                       static_cast<float*>(ws_o), ws_ml, q_len,
                        kv_len, group, k_hs, v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len,
                        static_cast<const float*>(nk), static_cast<const float*>(nv), n_hs, n_rs, n_new, bs, len_dev);
   }
   int s = launch_status();
   if (s != 0 || p.n_split == 1) return s;
   if (dtype == STD_BF16)
-    hipLaunchKernelGGL((attn_merge_kernel<bf16_t>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st, ws_o,
-                       ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len, group, bs.o, n_kv);
+    hipLaunchKernelGGL((attn_merge_kernel<bf16_t, PartT<NT>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
+                       static_cast<const PartT<NT>*>(ws_o), ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len,
+                       group, bs.o, n_kv);
   else
-    hipLaunchKernelGGL((attn_merge_kernel<float>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st, ws_o,
-                       ws_ml, static_cast<float*>(out), p.n_split, q_len, group, bs.o, n_kv);
+    hipLaunchKernelGGL((attn_merge_kernel<float, float>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
+                       static_cast<const float*>(ws_o), ws_ml, static_cast<float*>(out), p.n_split, q_len, group,
+                       bs.o, n_kv);
   return launch_status();
 }
 
@@ -1310,7 +1371,7 @@ int launch_attn(const void* q, void* k, void* v, void* out, int n_kv, int q_len,
 }
 
 size_t attn_workspace_bytes(int n_kv, int rows, int kv_len, int dtype) {
-  return ws_layout(n_kv, rows, plan_splits(n_kv, rows, kv_len, dtype)).total;
+  return ws_layout(n_kv, rows, plan_splits(n_kv, rows, kv_len, dtype), part_bytes_of(dtype, rows)).total;
 }
 
 int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, int q_len, int kv_len, int d,
@@ -1373,7 +1434,7 @@ CollLayout coll_layout(int n_kv, int group, int q_len, int kv_len, int vis_begin
   CollLayout c{};
   const SplitPlan p = plan_splits(n_kv, group * q_len, kv_len, STD_BF16);
   c.n_split = p.n_split;
-  c.attn = round_up(ws_layout(n_kv, group * q_len, p).total, 256);
+  c.attn = round_up(ws_layout(n_kv, group * q_len, p, part_bytes_of(STD_BF16, group * q_len)).total, 256);
   c.n_vtiles = (vis_end - 1) / TK - vis_begin / TK + 1;
   c.logits_off = c.attn;
   c.stats_off = round_up(c.logits_off + (size_t)n_kv * c.n_vtiles * q_len * TK * sizeof(float), 256);
@@ -1404,9 +1465,9 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int R = group * q_len;
   const SplitPlan p = plan_splits(n_kv, R, kv_len, STD_BF16);
-  const WsLayout wl = ws_layout(n_kv, R, p);
+  const WsLayout wl = ws_layout(n_kv, R, p, part_bytes_of(STD_BF16, R));
   char* base = static_cast<char*>(ws);
-  float* ws_o = p.n_split > 1 ? reinterpret_cast<float*>(base + wl.o_off) : nullptr;
+  half_t* ws_o = p.n_split > 1 ? reinterpret_cast<half_t*>(base + wl.o_off) : nullptr;      // R > 16: fp16
   float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
   const CollArgs ca{reinterpret_cast<float*>(base + cl.logits_off), reinterpret_cast<float2*>(base + cl.stats_off),
                     cl.n_vtiles, vis_begin, vis_end};
