@@ -84,6 +84,29 @@ def test_verify_matches_oracle(wname, q_len):
     assert_close(out, ref.verify_attention(q, k, v), w.dtype)
 
 
+@pytest.mark.parametrize("v_exp", [24, -30, 0])
+def test_verify_partials_keep_precision_at_any_value_scale(v_exp):
+    """The verify splits store their partials as fp16 scaled per row by a power
+    of two: values far beyond fp16's range (|V| ~ 2^24) or far below its normal
+    range (2^-30) merge to the same relative accuracy as unit values. bf16
+    scales exactly by powers of two, so the expected output is the oracle's on
+    unit values times 2^v_exp."""
+    w = WORKLOADS["c2"]
+    x = make_layer(w, 2)
+    k = torch.cat([x["k"], x["new_k"]], 2)
+    v = torch.cat([x["v"], x["new_v"]], 2)
+    kv_len = k.shape[2]
+    s = 2.0 ** v_exp
+    announce(f"verify c2 kv_len={kv_len}, values scaled by 2^{v_exp}")
+    kb = cache_buffer(k, kv_len + 64)
+    vb = cache_buffer(v * s, kv_len + 64)
+    out = ops.verify_attention(x["q_verify"].to(dev()), kb[:, :, :kv_len], vb[:, :, :kv_len])
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().astype(np.float64) / s
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ref.verify_attention(x["q_verify"], k, v), rtol=2e-2, atol=2e-3)
+
+
 def test_verify_131082_one_layer():
     """V unit at 128k: Q=10 over 131072 + 10 keys."""
     w = WORKLOADS["c4"]
