@@ -422,6 +422,11 @@ def main():
         "draft_attn_us_per_layer": round(draft_call_us, 3),
         "draft_hbm_gbps_warm": round(d_bytes / (draft_call_us * 1e-6) / 1e9, 1),
         "draft_attn_us_per_step_cold": round(draft_step_cold_us, 2),
+        # In a model's decode the layers' weights stream between two draft steps
+        # and evict the compact cache from the Infinity Cache: the round's rate
+        # with each of its draft steps at the measured cold step time instead.
+        "value_with_cold_draft_steps": round(G / ((ms_per_step + G * (draft_step_cold_us - draft_call_us * L) / 1e3)
+                                                  * 1e-3), 2),
         "draft_hbm_gbps_cold_step": round(draft_step_cold_gbps, 1),
         "draft_pct_peak_cold_step": round(100 * draft_step_cold_gbps / HBM_PEAK_GBPS, 2),
         "draft_attn_us_per_step_one_launch_cold": round(draft_all_cold_us, 2),
