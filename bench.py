@@ -163,6 +163,23 @@ def main():
         dense_k[l, :, :, :P] = k.to(w.dtype)
         dense_v[l, :, :, :P] = randn(1, Hkv, P, D)
     q_text = randn(L, 1, Hq, T, D)
+    salient = []
+    if w.keys in ("salient", "salient_runs"):
+        # c2/c3: a fraction of the visual keys leans +3 along the unit mean of
+        # its KV head's text queries (single positions, or runs of 64 for c3)
+        V_ = P - T
+        n_sal = max(1, int(round(w.salient_frac * V_)))
+        for l in range(L):
+            u = q_text[l, 0].float().reshape(Hkv, (Hq // Hkv) * T, D).mean(dim=1)
+            u = u / u.norm(dim=-1, keepdim=True)
+            if w.keys == "salient":
+                pos = torch.randperm(V_, generator=gen, device=dev)[:n_sal]
+            else:
+                starts = torch.randperm(V_ // 64, generator=gen, device=dev)[:max(1, n_sal // 64)] * 64
+                pos = (starts[:, None] + torch.arange(64, device=dev)[None, :]).reshape(-1)
+            kk = dense_k[l, 0, :, pos].float() + 3.0 * u[:, None, :]
+            dense_k[l, 0, :, pos] = kk.to(w.dtype)
+            salient.append(pos)
     q_draft = randn(L, 1, Hq, 1, D)
     new_k_draft = randn(L, 1, Hkv, 1, D)
     new_v_draft = randn(L, 1, Hkv, 1, D)
@@ -192,13 +209,24 @@ def main():
     select_ms_first = (time.perf_counter() - t0) * 1e3
     t0 = time.perf_counter()
     indices = []
+    topks = []
     for l in range(L):
         topk = ops.select_topk(q_text[l], dense_k[l, :, :, :P], P - T, vis, w.k)
         idx = ops.build_compact_index(nonvis, topk)
         ops.compact_kv(dense_k[l], dense_v[l], sparse_k[l], sparse_v[l], idx)
         indices.append(idx)
+        topks.append(topk)
     torch.cuda.synchronize()
     select_ms = (time.perf_counter() - t0) * 1e3
+    salient_frac_selected = None
+    if salient:
+        # diagnostic: the share of the salient positions that the selection kept
+        hit = [float(torch.isin(salient[l], topks[l][h].long()).float().mean()) for l in range(L) for h in range(Hkv)]
+        salient_frac_selected = round(statistics.mean(hit), 4)
+
+    def compaction_only():
+        for l in range(L):
+            ops.compact_kv(dense_k[l], dense_v[l], sparse_k[l], sparse_v[l], ops.build_compact_index(nonvis, topks[l]))
     indices = [ops.pad_index(i) for i in indices]     # index-addressed draft: the same key lists
 
     S0 = w.compact_len
@@ -355,6 +383,15 @@ def main():
     dense_decode_graph, _ = capture(dense_decode_only)
     dense_decode_us = time_graph(dense_decode_graph, 5, L)
     del dense_decode_graph
+    # Compaction of one layer's compact cache (index build + gather) and the
+    # acceptance alone, each graph-replayed.
+    compaction_graph, _ = capture(compaction_only)
+    compact_us = time_graph(compaction_graph, 10, L)
+    del compaction_graph
+    accept_graph, _ = capture(lambda: ops.greedy_accept(logits, draft, True, rollback_lengths=lengths))
+    accept_us = time_graph(accept_graph, 10, 1)
+    del accept_graph
+
     # Streaming-read ceiling on this device, in the same process: 256 MiB reads
     # over 8 distinct buffers in the fastest patterns of the stream workload
     # (the verify kernel's LDS DMA ring, the decode key split's, and vector
@@ -455,9 +492,12 @@ def main():
         "collector_overhead_us_per_layer": round(verify_collect_us - verify_call_us, 3),
         "collector_extra_bytes_per_layer": coll_extra_bytes(Hkv, Q, V),
         "select_compact_ms_all_layers": round(select_ms, 3),
+        "compact_us_per_layer": round(compact_us, 2),
+        "accept_us": round(accept_us, 2),
+        "salient_selected_frac": salient_frac_selected,
         "select_compact_ms_first_call": round(select_ms_first, 3),
         "roofline": {
-            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false> + attn_merge_kernel<bf16>)",
+            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false> + attn_merge_kernel<bf16, fp16 partials>)",
             "bound": "hbm",
             "achieved": round(verify_gbps, 1),
             "peak": HBM_PEAK_GBPS,
@@ -784,6 +824,16 @@ def cpu_baseline(w, L):
     threads = torch.get_num_threads()
     t0 = time.perf_counter()
     r_all, v_all, d_all, a_all = round_seconds("", 3, 10, 8.0)
+    # Selection (once per prompt, outside the round): one layer's text rows over
+    # the first visual keys and the text keys of a bounded prompt, scaled to the
+    # full prompt (the work is linear in the key count).
+    p_sel = min(w.prompt_len, 16384)
+    k_sel = torch.cat([x["k"][:, :, :p_sel - w.text_len], x["k"][:, :, w.prompt_len - w.text_len:w.prompt_len]],
+                      2).float()
+    qt = x["q_text"].float()
+    t_sel = (w.prompt_len / p_sel) * median_time(
+        "select", lambda: torch_cpu.select_topk(qt, k_sel, p_sel - w.text_len, min(w.k, p_sel - w.text_len)),
+        3, 10, 8.0)
     torch.set_num_threads(1)
     try:
         r_one, v_one, d_one, _ = round_seconds("_1_thread", 1, 3, 4.0)
@@ -808,6 +858,8 @@ def cpu_baseline(w, L):
         "verify_ms_per_layer": round(v_all * 1e3, 3),
         "draft_ms_per_layer_step": round(d_all * 1e3, 4),
         "accept_ms": round(a_all * 1e3, 3),
+        "select_ms_per_layer": round(t_sel * 1e3, 2),
+        "select_sample": f"{p_sel} of {w.prompt_len} keys, scaled x{w.prompt_len / p_sel:.3f}; all threads only",
         "verify_ms_per_layer_1_thread": round(v_one * 1e3, 3),
         "draft_ms_per_layer_step_1_thread": round(d_one * 1e3, 4),
         "warmups_reps": {name: list(c) for name, c in counts.items()},

@@ -127,3 +127,24 @@ def test_torch_cpu_restatements_match_the_numpy_oracle():
     assert torch_cpu.greedy_accept(logits, draft, True) == (3, preds[3])
     a, bonus, _ = np_accept.verify_accept(logits.numpy(), draft, True)
     assert (a, bonus) == (3, preds[3])
+
+
+def test_torch_cpu_selection_matches_the_numpy_oracle():
+    """The CPU baseline's selection restatement (causal text-row softmax,
+    group and row sums, top-k over the visual positions) picks the oracle's
+    positions; 16 keys per head are boosted along the group's mean query so
+    that the top-k is far from any tie at fp32 precision."""
+    import torch
+    from oracle import selection as np_sel
+    from oracle import torch_cpu
+    g = torch.Generator().manual_seed(12)
+    T, V, k = 20, 280, 16
+    q = torch.randn(1, 28, T, 128, generator=g)
+    key = torch.randn(1, 4, V + T, 128, generator=g)
+    for h in range(4):
+        u = q[0, 7 * h:7 * h + 7].reshape(-1, 128).mean(0)
+        pos = torch.randperm(V, generator=g)[:k]
+        key[0, h, pos] += 3.0 * u / u.norm()
+    want = np_sel.topk_positions(np_sel.selection_scores(q, key, V), range(V), k)
+    got = torch_cpu.select_topk(q, key, V, k).numpy()
+    np.testing.assert_array_equal(got, want)
