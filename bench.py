@@ -410,19 +410,32 @@ def main():
     del sbufs
     stream_ceiling = max(ceiling.values())
     # Cold: each copy follows a 1 GiB write that evicts the caches; the time of
-    # the writes alone (same graph shape) is subtracted.
+    # the writes alone (same graph shape) is subtracted. The write leaves the
+    # caches full of dirty lines, so the copy also pays for their write-back;
+    # a decode's weight stream evicts with clean lines, which the second form,
+    # a 1 GiB read before each copy, reproduces.
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    rflush = flush.view(torch.int32)
+    rsink = torch.zeros(1024, dtype=torch.int32, device=dev)
 
     def write_flush():
         flush.fill_(1)
 
-    flush_graph, _ = capture(repeated(write_flush, rep))
-    step_cold_graph, _ = capture(repeated(lambda: (write_flush(), draft_only()), rep))
-    all_cold_graph, _ = capture(repeated(lambda: (write_flush(), draft_all_layers()), rep))
-    flush_us = time_graph(flush_graph, args.cold_iters, rep)
-    draft_step_cold_us = time_graph(step_cold_graph, args.cold_iters, rep) - flush_us
-    draft_all_cold_us = time_graph(all_cold_graph, args.cold_iters, rep) - flush_us
-    del flush, flush_graph, step_cold_graph, all_cold_graph
+    def read_flush():
+        ops.stream_read(rflush, 1, 1024, rsink)
+
+    cold = {}
+    for kind, evict in (("write", write_flush), ("read", read_flush)):
+        flush_graph, _ = capture(repeated(evict, rep))
+        step_cold_graph, _ = capture(repeated(lambda: (evict(), draft_only()), rep))
+        all_cold_graph, _ = capture(repeated(lambda: (evict(), draft_all_layers()), rep))
+        flush_us = time_graph(flush_graph, args.cold_iters, rep)
+        cold[kind] = (time_graph(step_cold_graph, args.cold_iters, rep) - flush_us,
+                      time_graph(all_cold_graph, args.cold_iters, rep) - flush_us)
+        del flush_graph, step_cold_graph, all_cold_graph
+    del flush, rflush, rsink
+    draft_step_cold_us, draft_all_cold_us = cold["write"]
+    draft_step_rcold_us, draft_all_rcold_us = cold["read"]
     d_bytes = draft_bytes(Hq, Hkv, S0, D, es)
     v_bytes = verify_bytes(Hq, Hkv, Q, P + Q, D, es)
     verify_gbps = v_bytes / (verify_call_us * 1e-6) / 1e9
@@ -471,6 +484,13 @@ def main():
         "draft_one_launch_hbm_gbps_cold": round(L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9, 1),
         "draft_one_launch_pct_peak_cold": round(100 * L * d_bytes / (draft_all_cold_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
                                                 2),
+        # The same cold figures with the caches evicted by a 1 GiB read (clean lines).
+        "draft_attn_us_per_step_cold_read_evicted": round(draft_step_rcold_us, 2),
+        "value_with_cold_draft_steps_read_evicted": round(
+            G / ((ms_per_step + G * (draft_step_rcold_us - draft_call_us * L) / 1e3) * 1e-3), 2),
+        "draft_attn_us_per_step_one_launch_cold_read_evicted": round(draft_all_rcold_us, 2),
+        "draft_one_launch_pct_peak_cold_read_evicted": round(
+            100 * L * d_bytes / (draft_all_rcold_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2),
         "draft_indexed_us_per_layer": round(draft_indexed_us, 3),
         "draft_indexed_equals_compacted": indexed_equal,
         "dense_decode_us_per_layer": round(dense_decode_us, 3),
