@@ -92,10 +92,14 @@ int std_gqa_decode_noalloc(const void* q, const void* k, const void* v, void* ou
                            float scale, int dtype, void* stream);
 
 /* Batched decode: n_batch independent single-query problems of the same
- * shape in one launch (plus one merge launch). Problem b reads
+ * shape in one launch (plus one merge launch when the problems are split).
+ * Problem b reads
  * q + b*q_batch_stride, k + b*k_batch_stride, v + b*v_batch_stride and
  * writes out + b*out_batch_stride (strides in elements; q/out strides
- * >= n_q*d, 16-byte multiples). Each problem is exactly std_gqa_decode.
+ * >= n_q*d, 16-byte multiples). Each problem equals std_gqa_decode of that
+ * problem to fp32 rounding, bit for bit when both get the same split count
+ * (with many problems a launch may stream each unsplit; n_batch = 1 always
+ * matches).
  * Serves several sequences' draft steps at once (the reference decodes one
  * sequence per call, triton_attention.py:83-112); the same call over the
  * 28 layers of one draft step is the all-layer roofline unit of the draft

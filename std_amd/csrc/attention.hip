@@ -30,6 +30,7 @@
 // merge kernel combines in split order, so results are deterministic. (A
 // last-arriving-workgroup merge inside the split kernel was measured slower:
 // its device-scope fences write back L2 in every workgroup.)
+#include <algorithm>
 #include <climits>
 #include <mutex>
 #include <type_traits>
@@ -58,6 +59,16 @@ struct SplitPlan {
   int n_split;
 };
 
+// Split-count model of the one-row-tile bf16 decode (measured on MI355X with
+// the key-split kernel, graph-replayed): a workgroup takes a 32 KiB tile step
+// in 32 KiB / min(kCuGBs, kHbmGBs / workgroups) -- one CU alone pulls about
+// 50 GB/s, and about 6.3 TB/s is shared by all -- and more than one split adds
+// the merge launch with its partial round trip, kMergeUs.
+constexpr double kCuGBs = 50.0;
+constexpr double kHbmGBs = 6300.0;
+constexpr double kMergeUs = 3.5;
+
+// n_kv counts the launch's independent problems (KV heads x batch).
 SplitPlan plan_splits(int n_kv, int rows, int kv_len, int dtype) {
   SplitPlan p;
   p.ntiles = (kv_len + TK - 1) / TK;
@@ -65,7 +76,16 @@ SplitPlan plan_splits(int n_kv, int rows, int kv_len, int dtype) {
   int per_head = target_wg / n_kv;
   if (per_head < 1) per_head = 1;
   p.n_split = p.ntiles < per_head ? p.ntiles : per_head;
-  (void)rows;
+  // A decode over many problems (e.g. the 28 layers of one draft step in one
+  // launch, 112 problems) or over few tiles streams each problem in one
+  // workgroup when splitting saves less time than the merge costs.
+  if (dtype == STD_BF16 && rows <= 16 && p.n_split > 1) {
+    auto est_us = [&](int n) {
+      const double rate = std::min(kCuGBs, kHbmGBs / ((double)n * n_kv));   // bytes per ns
+      return (double)((p.ntiles + n - 1) / n) * (2.0 * TK * D * 2) / rate * 1e-3 + (n > 1 ? kMergeUs : 0.0);
+    };
+    if (est_us(1) <= est_us(p.n_split)) p.n_split = 1;
+  }
   return p;
 }
 

@@ -111,7 +111,9 @@ def gqa_decode_batched(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
 
     query [B, 1, n_q, 1, D] (or [B, n_q, 1, D]); key, value [B, 1, n_kv, S, D]
     with any batch and head strides (e.g. one draft step's 28 layer caches).
-    Each problem b is exactly gqa_decode(query[b], key[b], value[b])."""
+    Each problem b equals gqa_decode(query[b], key[b], value[b]) to fp32
+    rounding, bit for bit when both get the same split count (always for a
+    batch of one; many problems may each stream unsplit)."""
     squeeze = query.dim() == 4
     if squeeze:
         query = query.unsqueeze(1)
