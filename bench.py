@@ -388,9 +388,12 @@ def main():
     compaction_graph, _ = capture(compaction_only)
     compact_us = time_graph(compaction_graph, 10, L)
     del compaction_graph
-    accept_graph, _ = capture(lambda: ops.greedy_accept(logits, draft, True, rollback_lengths=lengths))
-    accept_us = time_graph(accept_graph, 10, 1)
+    # (rep copies per graph, as for the other phases; each copy rolls the
+    # lengths back again, which changes no shape)
+    accept_graph, _ = capture(repeated(lambda: ops.greedy_accept(logits, draft, True, rollback_lengths=lengths), rep))
+    accept_us = time_graph(accept_graph, 10, rep)
     del accept_graph
+    lengths.copy_(lengths0)
 
     # Streaming-read ceiling on this device, in the same process: 256 MiB reads
     # over 8 distinct buffers in the fastest patterns of the stream workload
@@ -422,7 +425,7 @@ def main():
         flush.fill_(1)
 
     def read_flush():
-        ops.stream_read(rflush, 1, 1024, rsink)
+        ops.stream_read(rflush, 0, 1024, rsink)
 
     cold = {}
     for kind, evict in (("write", write_flush), ("read", read_flush)):
