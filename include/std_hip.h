@@ -69,6 +69,13 @@ int std_version(void);
  * ------------------------------------------------------------------------ */
 size_t std_gqa_decode_workspace_bytes(int n_q, int n_kv, int kv_len, int d);
 
+/* Planning query (host only, no counterpart in the reference): the number of
+ * key-range splits per problem that an attention launch over n_problems
+ * independent (KV head x batch) problems of `rows` query rows each
+ * ((n_q / n_kv) * q_len, 1..96) and kv_len keys uses; one split means no
+ * merge launch and no workspace. STD_E_SHAPE / STD_E_DTYPE on bad input. */
+int std_attn_split_count(int n_problems, int rows, int kv_len, int dtype);
+
 int std_gqa_decode(const void* q, const void* k, const void* v, void* out,
                    int n_q, int n_kv, int kv_len, int d,
                    long long k_head_stride, long long v_head_stride,

@@ -31,6 +31,7 @@ SIGNATURES = {
     "std_status_string": (ctypes.c_char_p, [c_int]),
     "std_version": (c_int, []),
     "std_gqa_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "std_attn_split_count": (c_int, [c_int, c_int, c_int, c_int]),
     "std_gqa_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                c_longlong, c_longlong, c_float, c_int, c_void_p, c_size_t, c_void_p]),
     "std_gqa_decode_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,

@@ -1554,6 +1554,12 @@ int scratch_address(hipStream_t st, void** out) {
 
 using namespace stdhip;
 
+extern "C" int std_attn_split_count(int n_problems, int rows, int kv_len, int dtype) {
+  if (dtype != STD_BF16 && dtype != STD_F32) return STD_E_DTYPE;
+  if (n_problems < 1 || rows < 1 || rows > kMaxRows || kv_len < 1) return STD_E_SHAPE;
+  return plan_splits(n_problems, rows, kv_len, dtype).n_split;
+}
+
 extern "C" size_t std_gqa_decode_workspace_bytes(int n_q, int n_kv, int kv_len, int d) {
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || kv_len < 1 || d != D) return 0;
   // the larger of the two dtype plans, so one query serves both

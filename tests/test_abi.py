@@ -84,6 +84,28 @@ def test_noalloc_decode_validation():
     assert lib.std_gqa_decode_workspace_bytes(64, 4, 1 << 20, 128) > 0
 
 
+def test_split_plan():
+    """The planner's split counts at the shapes they were measured on: the
+    per-layer draft (4 KV heads, 1034 keys) keeps one tile per split, dense
+    decode and verify at 128k keep 64 splits per head, the 28-layer draft
+    launch (112 problems) and decodes of at most five tiles stream unsplit,
+    and 32 / 64 problems keep their 256-workgroup plans."""
+    lib = _lib.load_library()
+    bf16, f32 = 1, 0
+    for n_prob, rows, kv_len, want in [(4, 7, 1034, 17), (4, 7, 1043, 17), (4, 7, 131072, 64), (4, 70, 131082, 64),
+                                        (112, 7, 1034, 1), (112, 7, 2048, 1), (64, 7, 1034, 4), (64, 7, 2048, 4),
+                                        (32, 7, 1034, 8), (224, 7, 1034, 1), (4, 7, 320, 1), (4, 7, 400, 7),
+                                        (4, 7, 64, 1), (4, 7, 1, 1), (4, 70, 4106, 64)]:
+        assert lib.std_attn_split_count(n_prob, rows, kv_len, bf16) == want, (n_prob, rows, kv_len)
+    # fp32 and multi-row-tile launches split to fill the GPU whatever the merge costs
+    assert lib.std_attn_split_count(4, 7, 320, f32) == 5
+    assert lib.std_attn_split_count(112, 70, 1034, bf16) == 2
+    assert lib.std_attn_split_count(4, 7, 1034, 5) == -2
+    assert lib.std_attn_split_count(0, 7, 1034, bf16) == -3
+    assert lib.std_attn_split_count(4, 97, 1034, bf16) == -3
+    assert lib.std_attn_split_count(4, 7, 0, bf16) == -3
+
+
 def test_batched_decode_validation():
     """Every call here fails validation before any launch."""
     lib = _lib.load_library()
