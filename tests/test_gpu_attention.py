@@ -27,6 +27,7 @@ def _decode_case(wname, layer, kv_len, capacity_extra=37):
 @pytest.mark.parametrize("wname,kv_len", [
     ("c1", 1024), ("c1", 1), ("c1", 63), ("c1", 64), ("c1", 65), ("c1", 4096),
     ("c2", 1024), ("c2", 1033), ("c2", 2600), ("c2", 16384),
+    ("c2", 320), ("c2", 321),                  # the last unsplit bf16 decode (five tiles) and the first split one
     ("c3", 4096),
 ])
 def test_decode_matches_oracle(wname, kv_len):
