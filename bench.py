@@ -403,7 +403,7 @@ def main():
     sbufs = [torch.ones((256 << 20) // 4, dtype=torch.int32, device=dev) for _ in range(8)]
     ssink = torch.zeros(4096, dtype=torch.int32, device=dev)
     ceiling = {}
-    for mode, n_wg in ((3, 256), (5, 256), (1, 1024)):
+    for mode, n_wg in ((3, 256), (3, 208), (5, 256), (5, 192), (1, 1024)):
         def reads(mode=mode, n_wg=n_wg):
             for b in sbufs:
                 ops.stream_read(b, mode, n_wg, ssink)
@@ -724,7 +724,10 @@ def run_stream(args) -> None:
     reads = 16
     results = []
     configs = [(m, n) for m in (0, 1) for n in (256, 512, 1024, 2048, 4096)]
-    configs += [(m, n) for m in (2, 3, 4, 5) for n in (256, 512)]
+    configs += [(m, n) for m in (2, 4) for n in (256, 512)]
+    # round-robin rings also with fewer workgroups than CUs (contiguous chunks
+    # need a workgroup count that divides the 8192 tiles)
+    configs += [(m, n) for m in (3, 5) for n in (192, 208, 224, 256, 512)]
     for mode, n_wg in configs:
         def body():
             for i in range(reads):

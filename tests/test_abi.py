@@ -94,8 +94,9 @@ def test_split_plan():
     bf16, f32 = 1, 0
     for n_prob, rows, kv_len, want in [(4, 7, 1034, 17), (4, 7, 1043, 17), (4, 7, 131072, 64), (4, 70, 131082, 64),
                                         (112, 7, 1034, 1), (112, 7, 2048, 1), (64, 7, 1034, 4), (64, 7, 2048, 4),
-                                        (32, 7, 1034, 8), (224, 7, 1034, 1), (4, 7, 320, 1), (4, 7, 400, 7),
-                                        (4, 7, 64, 1), (4, 7, 1, 1), (4, 70, 4106, 64)]:
+                                        (32, 7, 1034, 8), (32, 7, 2048, 8), (224, 7, 1034, 1), (4, 7, 320, 1),
+                                        (4, 7, 400, 7), (4, 7, 64, 1), (4, 7, 1, 1), (4, 70, 4106, 64),
+                                        (4, 70, 16394, 64), (4, 70, 65546, 64)]:
         assert lib.std_attn_split_count(n_prob, rows, kv_len, bf16) == want, (n_prob, rows, kv_len)
     # fp32 and multi-row-tile launches split to fill the GPU whatever the merge costs
     assert lib.std_attn_split_count(4, 7, 320, f32) == 5
