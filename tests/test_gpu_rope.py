@@ -94,11 +94,13 @@ def test_attention_devlen_equals_host_length_kernel(dtype, q_len, kv, cap):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_attention_devlen_small_cache_matches_oracle(dtype):
-    cap, kv = 1163, 1034
+@pytest.mark.parametrize("dtype,cap,kv", [(torch.bfloat16, 1163, 1034), (torch.float32, 1163, 1034),
+                                          (torch.bfloat16, 300, 200), (torch.bfloat16, 300, 37)])
+def test_attention_devlen_small_cache_matches_oracle(dtype, cap, kv):
+    """A decode planned for the cache capacity reads only the device length's
+    keys; at cap = 300 (five tiles) the bf16 decode streams unsplit."""
     announce(f"attention_devlen decode {dtype} kv={kv} planned for {cap}")
-    g = torch.Generator().manual_seed(22)
+    g = torch.Generator().manual_seed(22 + kv)
     k = torch.randn(1, NKV, cap, D, generator=g).to(dtype)
     v = torch.randn(1, NKV, cap, D, generator=g).to(dtype)
     q = torch.randn(1, NQ, 1, D, generator=g).to(dtype)
