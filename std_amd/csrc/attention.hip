@@ -25,11 +25,13 @@
 // fp32: the same algorithm with register-staged LDS tiles and 16x16x4 fp32
 // MFMA (exactness path for fp32 caches).
 //
-// Splits: the key tiles of a head are spread evenly over n_split workgroups;
+// Splits: the key tiles of a head are dealt round-robin to n_split workgroups;
 // each merges its key-waves in LDS, then writes (m, l, O) partials that a
-// merge kernel combines in split order, so results are deterministic. (A
-// last-arriving-workgroup merge inside the split kernel was measured slower:
-// its device-scope fences write back L2 in every workgroup.)
+// merge kernel combines in split order, so results are deterministic. Merging
+// inside the split launch was measured slower in every form tried (a
+// last-arriving workgroup behind release fences, a grid barrier, merge
+// workgroups appended to the grid reading agent-scope partials): carrying the
+// partials across XCDs within a launch costs more than the second launch.
 #include <algorithm>
 #include <climits>
 #include <mutex>
@@ -59,11 +61,12 @@ struct SplitPlan {
   int n_split;
 };
 
-// Split-count model of the one-row-tile bf16 decode (measured on MI355X with
-// the key-split kernel, graph-replayed): a workgroup takes a 32 KiB tile step
-// in 32 KiB / min(kCuGBs, kHbmGBs / workgroups) -- one CU alone pulls about
-// 50 GB/s, and about 6.3 TB/s is shared by all -- and more than one split adds
-// the merge launch with its partial round trip, kMergeUs.
+// Split-count model of the one-row-tile bf16 decode (fitted on MI355X to the
+// key-split kernel, graph-replayed): a workgroup takes a 32 KiB tile step in
+// 32 KiB / min(kCuGBs, kHbmGBs / workgroups) -- about 50 GB/s is what one
+// such workgroup streams with a hundred others beside it (112 GB/s alone),
+// and about 6.3 TB/s is shared by all -- and more than one split adds the
+// merge launch with its partial round trip, kMergeUs.
 constexpr double kCuGBs = 50.0;
 constexpr double kHbmGBs = 6300.0;
 constexpr double kMergeUs = 3.5;
