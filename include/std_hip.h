@@ -24,7 +24,10 @@
  *             tensor has head stride max_len*D: read in place, no copy)
  *   output    [n_q][q_len][d]
  * Query head h reads KV head h / (n_q / n_kv)  (repeat_kv / enable_gqa order).
- * Supported: d == 128, 1 <= n_q/n_kv <= 16, dtype STD_F32 or STD_BF16.
+ * Supported: d == 128, 1 <= n_q/n_kv <= 16, dtype STD_F32, STD_BF16 or STD_F16
+ * (fp16 as the reference loads its model, scripts/benchmark_std.py:66; the
+ * bf16 and fp16 kernels are the same but for the MFMA element type and the
+ * rounding of probabilities and outputs). Exceptions are noted per call.
  */
 #ifndef STD_HIP_H
 #define STD_HIP_H
@@ -37,7 +40,7 @@ extern "C" {
 #endif
 
 /* element types */
-enum { STD_F32 = 0, STD_BF16 = 1, STD_F16 = 2 };   /* STD_F16: selection probabilities only */
+enum { STD_F32 = 0, STD_BF16 = 1, STD_F16 = 2 };
 
 /* validation errors (negative) */
 enum {
@@ -89,7 +92,7 @@ int std_gqa_decode(const void* q, const void* k, const void* v, void* out,
  * live in a device array of the library (2 MiB + 64 KiB per GPU, held until
  * the process ends; looked up on the first call on each device, which must be
  * the current device and the stream's device). Returns STD_E_WORKSPACE where
- * std_gqa_decode_workspace_bytes() exceeds that size (bf16: never; fp32: more
+ * std_gqa_decode_workspace_bytes() exceeds that size (bf16, fp16: never; fp32: more
  * than 8 query heads per KV head at long kv_len). Calls that overlap on one
  * GPU share the array and race: serialise them (one stream per GPU).
  * Allocates nothing and keeps no other state. */
@@ -319,7 +322,7 @@ int std_attn_devlen(const void* q, const void* k_cache, const void* v_cache, voi
  *
  * len_dev == NULL: kv_len keys. Otherwise the key count is *len_dev + 1 (this
  * step's row last, as std_attn_devlen with q_len = 1) and kv_len is the
- * maximum the launch is planned for. Single query row per head, bf16. index:
+ * maximum the launch is planned for. Single query row per head, bf16 or fp16. index:
  * int32, 16-byte aligned, index_head_stride >= n_index rounded up to 16 (the
  * row is read 16 entries at a time). Workspace:
  * std_gqa_decode_workspace_bytes(n_q, n_kv, kv_len, d).

@@ -11,7 +11,8 @@ sections therefore select one and the same 1-D table:
 with rotate_half(x) = cat(-x[D/2:], x[:D/2]).
 
 The model dtype is "bf16" (round to nearest even on the float32 value, as
-torch's bfloat16 arithmetic does) or "fp32".
+torch's bfloat16 arithmetic does), "fp16" (the same to IEEE half, the dtype the
+reference loads its model in, scripts/benchmark_std.py:66) or "fp32".
 """
 from __future__ import annotations
 
@@ -32,7 +33,11 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
 
 def _round(x: np.ndarray, dtype: str) -> np.ndarray:
     x = np.asarray(x, dtype=np.float32)
-    return round_bf16(x) if dtype == "bf16" else x
+    if dtype == "bf16":
+        return round_bf16(x)
+    if dtype == "fp16":
+        return x.astype(np.float16).astype(np.float32)     # IEEE half, ties to even
+    return x
 
 
 def cos_sin(positions: np.ndarray, inv: np.ndarray, dtype: str):

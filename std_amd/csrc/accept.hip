@@ -235,7 +235,7 @@ extern "C" int std_greedy_accept(const void* logits, long long logits_row_stride
   if (!logits || !draft || !out || !workspace) return STD_E_NULL;
   if (!has_pending && !dense_next) return STD_E_NULL;
   if (n_lens > 0 && !rollback_lens) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (vocab < 1 || n_draft < 1 || n_lens < 0 || q_rows != n_draft + (has_pending ? 1 : 0) || q_rows > kMaxRows)
     return STD_E_SHAPE;
   if (logits_row_stride < vocab) return STD_E_SHAPE;
@@ -246,6 +246,9 @@ extern "C" int std_greedy_accept(const void* logits, long long logits_row_stride
   if (dtype == STD_BF16)
     hipLaunchKernelGGL(argmax_partial_kernel<bf16_t>, dim3(nb, q_rows), dim3(AM_THREADS), 0, st,
                        static_cast<const bf16_t*>(logits), logits_row_stride, vocab, nb, part);
+  else if (dtype == STD_F16)
+    hipLaunchKernelGGL(argmax_partial_kernel<f16_t>, dim3(nb, q_rows), dim3(AM_THREADS), 0, st,
+                       static_cast<const f16_t*>(logits), logits_row_stride, vocab, nb, part);
   else
     hipLaunchKernelGGL(argmax_partial_kernel<float>, dim3(nb, q_rows), dim3(AM_THREADS), 0, st,
                        static_cast<const float*>(logits), logits_row_stride, vocab, nb, part);
@@ -260,7 +263,7 @@ extern "C" int std_kv_append(void* cache_k, void* cache_v, const void* new_k, co
                              int d, long long cache_head_stride, long long new_head_stride, long long new_row_stride,
                              int capacity, const int32_t* len_dev, int dtype, void* stream) {
   if (!cache_k || !cache_v || !new_k || !new_v || !len_dev) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_kv < 1 || rows < 1 || capacity < 1) return STD_E_SHAPE;
   const int es = dtype_size(dtype);
   if (!aligned16(cache_k) || !aligned16(cache_v) || !aligned16(new_k) || !aligned16(new_v)) return STD_E_ALIGN;
@@ -284,7 +287,7 @@ extern "C" int std_len_add(int32_t* len_dev, int n, int delta, void* stream) {
 extern "C" int std_argmax_rows(const void* logits, long long logits_row_stride, int rows, int vocab, int dtype,
                                long long* out, void* workspace, size_t workspace_bytes, void* stream) {
   if (!logits || !out || !workspace) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (rows < 1 || rows > 65535 || vocab < 1 || logits_row_stride < vocab) return STD_E_SHAPE;
   if (workspace_bytes < std_greedy_accept_workspace_bytes(rows, vocab)) return STD_E_WORKSPACE;
   const int nb = accept_blocks(vocab);
@@ -293,6 +296,9 @@ extern "C" int std_argmax_rows(const void* logits, long long logits_row_stride, 
   if (dtype == STD_BF16)
     hipLaunchKernelGGL(argmax_partial_kernel<bf16_t>, dim3(nb, rows), dim3(AM_THREADS), 0, st,
                        static_cast<const bf16_t*>(logits), logits_row_stride, vocab, nb, part);
+  else if (dtype == STD_F16)
+    hipLaunchKernelGGL(argmax_partial_kernel<f16_t>, dim3(nb, rows), dim3(AM_THREADS), 0, st,
+                       static_cast<const f16_t*>(logits), logits_row_stride, vocab, nb, part);
   else
     hipLaunchKernelGGL(argmax_partial_kernel<float>, dim3(nb, rows), dim3(AM_THREADS), 0, st,
                        static_cast<const float*>(logits), logits_row_stride, vocab, nb, part);
@@ -305,12 +311,16 @@ extern "C" int std_argmax_rows(const void* logits, long long logits_row_stride, 
 extern "C" int std_rms_norm(const void* x, long long x_row_stride, const void* weight, void* out,
                             long long out_row_stride, int rows, int hidden, float eps, int dtype, void* stream) {
   if (!x || !weight || !out) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (rows < 1 || hidden < 1 || x_row_stride < hidden || out_row_stride < hidden) return STD_E_SHAPE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == STD_BF16)
     hipLaunchKernelGGL(rms_norm_kernel<bf16_t>, dim3(rows), dim3(256), 0, st, static_cast<const bf16_t*>(x),
                        static_cast<const bf16_t*>(weight), static_cast<bf16_t*>(out), hidden, x_row_stride,
+                       out_row_stride, eps);
+  else if (dtype == STD_F16)
+    hipLaunchKernelGGL(rms_norm_kernel<f16_t>, dim3(rows), dim3(256), 0, st, static_cast<const f16_t*>(x),
+                       static_cast<const f16_t*>(weight), static_cast<f16_t*>(out), hidden, x_row_stride,
                        out_row_stride, eps);
   else
     hipLaunchKernelGGL(rms_norm_kernel<float>, dim3(rows), dim3(256), 0, st, static_cast<const float*>(x),

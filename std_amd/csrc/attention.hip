@@ -75,14 +75,15 @@ constexpr double kMergeUs = 3.5;
 SplitPlan plan_splits(int n_kv, int rows, int kv_len, int dtype) {
   SplitPlan p;
   p.ntiles = (kv_len + TK - 1) / TK;
-  const int target_wg = dtype == STD_BF16 ? 256 : 512;   // bf16: one LDS-heavy workgroup per CU
+  const bool h16 = dtype == STD_BF16 || dtype == STD_F16;          // the 16-bit (bf16 / fp16) kernels
+  const int target_wg = h16 ? 256 : 512;   // one LDS-heavy workgroup per CU
   int per_head = target_wg / n_kv;
   if (per_head < 1) per_head = 1;
   p.n_split = p.ntiles < per_head ? p.ntiles : per_head;
   // A decode over many problems (e.g. the 28 layers of one draft step in one
   // launch, 112 problems) or over few tiles streams each problem in one
   // workgroup when splitting saves less time than the merge costs.
-  if (dtype == STD_BF16 && rows <= 16 && p.n_split > 1) {
+  if (h16 && rows <= 16 && p.n_split > 1) {
     auto est_us = [&](int n) {
       const double rate = std::min(kCuGBs, kHbmGBs / ((double)n * n_kv));   // bytes per ns
       return (double)((p.ntiles + n - 1) / n) * (2.0 * TK * D * 2) / rate * 1e-3 + (n > 1 ? kMergeUs : 0.0);
@@ -136,7 +137,7 @@ struct WsLayout {
 };
 
 // part_bytes: 2 for scaled fp16 partials, 4 for fp32 (part_bytes_of).
-int part_bytes_of(int dtype, int rows) { return dtype == STD_BF16 && rows > 16 ? 2 : 4; }
+int part_bytes_of(int dtype, int rows) { return dtype != STD_F32 && rows > 16 ? 2 : 4; }
 
 WsLayout ws_layout(int n_kv, int rows, const SplitPlan& p, int part_bytes) {
   WsLayout l{0, 0, 0};
@@ -456,6 +457,39 @@ __device__ __forceinline__ i16x4 pack_bf16x4(float a, float b, float c, float d)
   return __builtin_bit_cast(i16x4, (uint64_t)lo | ((uint64_t)hi << 32));
 }
 
+// The 16-bit element arithmetic of the bf16 kernels, for bf16 (bf16_t) or
+// fp16 (f16_t) caches: the MFMA operand vectors, QK^T / PV MFMAs of 32 and
+// 16 contraction elements, the packing of four floats (probabilities, output
+// rows; round to nearest even) and the element 1.0. Storage is the 16-bit
+// pattern either way, so loads, the DMA ring and the appends are shared.
+template <typename E> struct Elem;
+template <> struct Elem<bf16_t> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef short v4 __attribute__((ext_vector_type(4)));
+  static constexpr short kOne = 0x3f80;
+  static __device__ __forceinline__ f32x4 mma32(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(v4 a, v4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ i16x4 pack4(float a, float b, float c, float d) { return pack_bf16x4(a, b, c, d); }
+};
+template <> struct Elem<f16_t> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v4 __attribute__((ext_vector_type(4)));
+  static constexpr short kOne = 0x3c00;
+  static __device__ __forceinline__ f32x4 mma32(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(v4 a, v4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ i16x4 pack4(float a, float b, float c, float d) {
+    return __builtin_bit_cast(i16x4, __builtin_convertvector(f32x4{a, b, c, d}, v4));
+  }
+};
+
 __device__ __forceinline__ float xor16_max(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
@@ -492,7 +526,7 @@ struct Bf16Cfg {
 template <int NT>
 using PartT = typename std::conditional<(NT > 1), half_t, float>::type;
 
-template <int NT, bool KS, bool GA, bool COLL = false>
+template <int NT, bool KS, bool GA, bool COLL = false, typename E = bf16_t>
 __global__ void __launch_bounds__(NT == 1 ? 256 : 512)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
                  bf16_t* __restrict__ out, PartT<NT>* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
@@ -501,6 +535,10 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
                  long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev,
                  AuxArgs<COLL> ga, const int32_t* __restrict__ gidx) {
   using C = Bf16Cfg<NT>;
+  using EL = Elem<E>;
+  using v8 = typename EL::v8;                    // 8 elements: the 16x16x32 MFMA operands
+  using v4 = typename EL::v4;                    // 4 elements: the 16x16x16 MFMA operands
+  static_assert(!COLL || std::is_same<E, bf16_t>::value, "the collector rides the bf16 verify");
   __shared__ __align__(16) char ring[NSTAGE * STAGEB];
   // With the collector the query rows are staged in LDS by the ring's DMA
   // (its group means read every row of the group): 1.7 us less per 128k
@@ -672,20 +710,20 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   const bool row_ok = (computes || ksw) && row < R;
   const int lim = row_ok ? causal_off + (row % q_len) : INT_MAX;
   // Q^T operand, 32-wide chunk c: lane (ln, lg) holds q[row][32c + 8lg, +8).
-  bf16x8 qf[4];
+  v8 qf[4];
   if (row_ok) {
     if constexpr (kQLds) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) qf[c] = *reinterpret_cast<const bf16x8*>(qs + sw_off(row, 4 * c + lg));
+      for (int c = 0; c < 4; ++c) qf[c] = *reinterpret_cast<const v8*>(qs + sw_off(row, 4 * c + lg));
     } else {
       const int hl = row / q_len, i = row - hl * q_len;
       const bf16_t* qrow = q + ((long long)(g * group + hl) * q_len + i) * D;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) qf[c] = *reinterpret_cast<const bf16x8*>(qrow + 32 * c + 8 * lg);
+      for (int c = 0; c < 4; ++c) qf[c] = *reinterpret_cast<const v8*>(qrow + 32 * c + 8 * lg);
     }
   } else {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qf[c] = bf16x8{};
+    for (int c = 0; c < 4; ++c) qf[c] = v8{};
   }
   // Collector rows: lanes q_off .. 15 of the key-split waves (the padding rows
   // of the last row tile, R + q_len <= 80) carry position i = ln - q_off's
@@ -694,10 +732,10 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   // a bf16 head qf and a bf16 remainder qlo, so that K.qf + K.qlo carries the
   // fp32 mean's precision through bf16 MFMAs.
   const int q_off = 16 - q_len;
-  bf16x8 qlo[4];
+  v8 qlo[4];
   if constexpr (COLL) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qlo[c] = bf16x8{};
+    for (int c = 0; c < 4; ++c) qlo[c] = v8{};
     if (ksw && ln >= q_off) {
       const int i = ln - q_off;
 #pragma unroll
@@ -721,8 +759,8 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
           hi[e] = (short)h;
           lo[e] = (short)f32_to_bf16(mean - bf16_to_f32(h));
         }
-        qf[c] = __builtin_bit_cast(bf16x8, hi);
-        qlo[c] = __builtin_bit_cast(bf16x8, lo);
+        qf[c] = __builtin_bit_cast(v8, hi);
+        qlo[c] = __builtin_bit_cast(v8, lo);
       }
     }
   }
@@ -745,8 +783,8 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   f32x4 acc[8], lsum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const bf16x8 ones = __builtin_bit_cast(bf16x8, i16x8{0x3f80, 0x3f80, 0x3f80, 0x3f80, 0x3f80, 0x3f80, 0x3f80,
-                                                       0x3f80});
+  const v8 ones = __builtin_bit_cast(v8, i16x8{EL::kOne, EL::kOne, EL::kOne, EL::kOne, EL::kOne, EL::kOne, EL::kOne,
+                                               EL::kOne});
 
   // S^T sub-tile j (keys 16j..16j+15 of the tile): lane (ln, lg) element i is
   // key 16j + 4lg + i of query row ln.
@@ -755,11 +793,11 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      bf16x8 kf[4];
+      v8 kf[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) kf[j] = *reinterpret_cast<const bf16x8*>(st + sw_off(16 * j + ln, 4 * c + lg));
+      for (int j = 0; j < 4; ++j) kf[j] = *reinterpret_cast<const v8*>(st + sw_off(16 * j + ln, 4 * c + lg));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j], qf[c], s[j], 0, 0, 0);
+      for (int j = 0; j < 4; ++j) s[j] = EL::mma32(kf[j], qf[c], s[j]);
     }
   };
 
@@ -770,7 +808,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   auto softmax_pv = [&](int tt, const char* st, f32x4* s) {
     const char* Vs = st + TILEB;
     const int tile_base = tile_key0(split, tt, n_split);
-    bf16x8 vf[2][8];
+    v8 vf[2][8];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int rv = 32 * p + 4 * lg + (ln >> 2);
@@ -779,7 +817,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
         const int chunk = 2 * t + ((ln >> 1) & 1), half = (ln & 1) << 3;
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Vs + sw_off(rv, chunk) + half));
         const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Vs + sw_off(rv + 16, chunk) + half));
-        vf[p][t] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        vf[p][t] = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     }
 #pragma unroll
@@ -811,7 +849,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       for (int t = 0; t < 8; ++t) acc[t] *= alpha;
       m_run = m_new;
     }
-    bf16x8 pb[2];
+    v8 pb[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       float x[8];
@@ -820,16 +858,16 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
         x[i] = fast_exp2(s[2 * p][i] - m_run);
         x[4 + i] = fast_exp2(s[2 * p + 1][i] - m_run);
       }
-      const i16x4 lo = pack_bf16x4(x[0], x[1], x[2], x[3]);
-      const i16x4 hi = pack_bf16x4(x[4], x[5], x[6], x[7]);
-      pb[p] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      const i16x4 lo = EL::pack4(x[0], x[1], x[2], x[3]);
+      const i16x4 hi = EL::pack4(x[4], x[5], x[6], x[7]);
+      pb[p] = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
 #pragma unroll
-    for (int p = 0; p < 2; ++p) lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[p], lsum, 0, 0, 0);
+    for (int p = 0; p < 2; ++p) lsum = EL::mma32(ones, pb[p], lsum);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[p][t], pb[p], acc[t], 0, 0, 0);
+      for (int p = 0; p < 2; ++p) acc[t] = EL::mma32(vf[p][t], pb[p], acc[t]);
   };
 
   // Key-split tile (KS waves, and the HYB waves on the last row tile): wave
@@ -840,15 +878,14 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   // through one transposed LDS read per 16 output columns, the same keys of V
   // (V^T operand). Each such wave keeps its own running max, row sum and
   // output rows; ks_merge combines the four.
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  const s16x4 ones4 = {0x3f80, 0x3f80, 0x3f80, 0x3f80};
+  const v4 ones4 = __builtin_bit_cast(v4, i16x4{EL::kOne, EL::kOne, EL::kOne, EL::kOne});
   auto ks_tile = [&](int tt, const char* st) {
     f32x4 sc = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(st + sw_off(16 * ks_sub + ln, 4 * c + lg));
-      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], sc, 0, 0, 0);
-      if constexpr (COLL) sl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qlo[c], sl, 0, 0, 0);
+      const v8 kf = *reinterpret_cast<const v8*>(st + sw_off(16 * ks_sub + ln, 4 * c + lg));
+      sc = EL::mma32(kf, qf[c], sc);
+      if constexpr (COLL) sl = EL::mma32(kf, qlo[c], sl);
     }
     if constexpr (COLL) {
       // Collector lanes: logits of this wave's four keys of the tile, over
@@ -878,11 +915,11 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     }
     const char* Vs = st + TILEB;
     const int rv = 16 * ks_sub + 4 * lg + (ln >> 2);
-    s16x4 vf[8];
+    v4 vf[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int chunk = 2 * t + ((ln >> 1) & 1), half = (ln & 1) << 3;
-      vf[t] = __builtin_bit_cast(s16x4,
+      vf[t] = __builtin_bit_cast(v4,
                                  __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(Vs + sw_off(rv, chunk) + half)));
     }
 #pragma unroll
@@ -903,11 +940,11 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       for (int t = 0; t < 8; ++t) acc[t] *= alpha;
       m_run = m_new;
     }
-    const s16x4 pb = __builtin_bit_cast(s16x4, pack_bf16x4(fast_exp2(sc[0] - m_run), fast_exp2(sc[1] - m_run),
+    const v4 pb = __builtin_bit_cast(v4, EL::pack4(fast_exp2(sc[0] - m_run), fast_exp2(sc[1] - m_run),
                                                            fast_exp2(sc[2] - m_run), fast_exp2(sc[3] - m_run)));
-    lsum = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ones4, pb, lsum, 0, 0, 0);
+    lsum = EL::mma16(ones4, pb, lsum);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[t], pb, acc[t], 0, 0, 0);
+    for (int t = 0; t < 8; ++t) acc[t] = EL::mma16(vf[t], pb, acc[t]);
   };
   // Merge of the four key-split waves' (m, l, O) rows r0 + 0..15: each
   // stores its own into LDS (mlw, Ow at ring offset 0 and 1 KiB; the caller
@@ -949,7 +986,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
         if (r < R) {
           bf16_t* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
           const f32x4 on = o / Lr;
-          *reinterpret_cast<i16x4*>(dst) = pack_bf16x4(on[0], on[1], on[2], on[3]);
+          *reinterpret_cast<i16x4*>(dst) = EL::pack4(on[0], on[1], on[2], on[3]);
         }
       } else if constexpr (NT > 1) {
         float amax = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
@@ -1064,7 +1101,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const f32x4 o = acc[t] / l_row;
-      *reinterpret_cast<i16x4*>(dst + 16 * t) = pack_bf16x4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<i16x4*>(dst + 16 * t) = EL::pack4(o[0], o[1], o[2], o[3]);
     }
   } else if constexpr (NT == 1) {
     const long long prow = (long long)g * n_split * R + (long long)split * R + row;
@@ -1326,6 +1363,28 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
 }
 
 // ===========================================================================
+// The split launch of the 16-bit kernels with element type E (bf16_t or
+// f16_t); the caller launches the merge.
+template <int NT, typename E>
+void launch_h16(const void* q, void* k, void* v, void* out, int q_len, int kv_len, int group, long long k_hs,
+                long long v_hs, float scale_log2, const SplitPlan& p, void* ws_o, float2* ws_ml, const void* nk,
+                const void* nv, long long n_hs, long long n_rs, int n_new, dim3 grid, BatchStrides bs,
+                const int32_t* len_dev, GatherArgs ga, hipStream_t st) {
+  // One row tile and at least two tiles per split on average: key split.
+  const bool ks = NT == 1 && p.ntiles >= 2 * p.n_split;
+  // Gathered keys (decode only): a separate instantiation, so the plain
+  // kernels carry none of the gather code or arguments.
+  auto kern = NT == 1 && ga.idx != nullptr ? (ks ? attn_bf16_kernel<NT, NT == 1, NT == 1, false, E>
+                                                 : attn_bf16_kernel<NT, false, NT == 1, false, E>)
+                                           : (ks ? attn_bf16_kernel<NT, NT == 1, false, false, E>
+                                                 : attn_bf16_kernel<NT, false, false, false, E>);
+  hipLaunchKernelGGL(kern, grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
+                     static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
+                     static_cast<bf16_t*>(out), static_cast<PartT<NT>*>(ws_o), ws_ml, q_len, kv_len, group, k_hs,
+                     v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
+                     static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev, ga, ga.idx);
+}
+
 template <int NT>
 int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
               long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
@@ -1340,20 +1399,13 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   const float scale_log2 = scale * 1.4426950408889634f;
   const dim3 grid(p.n_split, n_kv, n_batch);
   bs.w = (long long)n_kv * p.n_split * R;
-  if (dtype == STD_BF16) {
-    // One row tile and at least two tiles per split on average: key split.
-    const bool ks = NT == 1 && p.ntiles >= 2 * p.n_split;
-    // Gathered keys (decode only): a separate instantiation, so the plain
-    // kernels carry none of the gather code or arguments.
-    auto kern = NT == 1 && ga.idx != nullptr ? (ks ? attn_bf16_kernel<NT, NT == 1, NT == 1>
-                                                   : attn_bf16_kernel<NT, false, NT == 1>)
-                                             : (ks ? attn_bf16_kernel<NT, NT == 1, false>
-                                                   : attn_bf16_kernel<NT, false, false>);
-    hipLaunchKernelGGL(kern, grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
-                       static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
-                       static_cast<bf16_t*>(out), static_cast<PartT<NT>*>(ws_o), ws_ml, q_len, kv_len, group, k_hs,
-                       v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
-                       static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev, ga, ga.idx);
+  if (dtype != STD_F32) {
+    if (dtype == STD_BF16)
+      launch_h16<NT, bf16_t>(q, k, v, out, q_len, kv_len, group, k_hs, v_hs, scale_log2, p, ws_o, ws_ml, nk, nv, n_hs,
+                             n_rs, n_new, grid, bs, len_dev, ga, st);
+    else
+      launch_h16<NT, f16_t>(q, k, v, out, q_len, kv_len, group, k_hs, v_hs, scale_log2, p, ws_o, ws_ml, nk, nv, n_hs,
+                            n_rs, n_new, grid, bs, len_dev, ga, st);
   } else {
     hipLaunchKernelGGL((attn_f32_kernel<NT>), grid, dim3(NTHREADS), 0, st, static_cast<const float*>(q),
                        static_cast<float*>(k), static_cast<float*>(v), static_cast<float*>(out),
@@ -1366,6 +1418,10 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   if (dtype == STD_BF16)
     hipLaunchKernelGGL((attn_merge_kernel<bf16_t, PartT<NT>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
                        static_cast<const PartT<NT>*>(ws_o), ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len,
+                       group, bs.o, n_kv);
+  else if (dtype == STD_F16)
+    hipLaunchKernelGGL((attn_merge_kernel<f16_t, PartT<NT>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
+                       static_cast<const PartT<NT>*>(ws_o), ws_ml, static_cast<f16_t*>(out), p.n_split, q_len,
                        group, bs.o, n_kv);
   else
     hipLaunchKernelGGL((attn_merge_kernel<float, float>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
@@ -1407,7 +1463,7 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
     // Gathered keys: one bf16 decode problem; indices padded to 16 per row of
     // the index array and 16-byte aligned (they are read four at a time).
     if (!ga.k || !ga.v) return STD_E_NULL;
-    if (dtype != STD_BF16) return STD_E_DTYPE;
+    if (dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
     if (q_len != 1 || n_batch != 1 || n_new > 0) return STD_E_SHAPE;
     if (ga.n_idx < 0 || ga.n_idx > kv_len || ga.dense_rows < 1) return STD_E_SHAPE;
     if (ga.idx_hs < (long long)round_up((size_t)ga.n_idx, 16)) return STD_E_SHAPE;
@@ -1428,7 +1484,7 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
     if ((bs.q * es) % 16 || (bs.o * es) % 16 || (bs.k * es) % 16 || (bs.v * es) % 16) return STD_E_ALIGN;
   }
   if (n_new > 0 && (!nk || !nv)) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len) return STD_E_SHAPE;
   const int group = n_q / n_kv;
   if ((long long)group * q_len > kMaxRows) return STD_E_SHAPE;
@@ -1558,7 +1614,7 @@ int scratch_address(hipStream_t st, void** out) {
 using namespace stdhip;
 
 extern "C" int std_attn_split_count(int n_problems, int rows, int kv_len, int dtype) {
-  if (dtype != STD_BF16 && dtype != STD_F32) return STD_E_DTYPE;
+  if (dtype != STD_BF16 && dtype != STD_F32 && dtype != STD_F16) return STD_E_DTYPE;
   if (n_problems < 1 || rows < 1 || rows > kMaxRows || kv_len < 1) return STD_E_SHAPE;
   return plan_splits(n_problems, rows, kv_len, dtype).n_split;
 }
@@ -1656,7 +1712,7 @@ extern "C" int std_gqa_decode_noalloc(const void* q, const void* k, const void* 
                                       float scale, int dtype, void* stream) {
   // The size check comes before any HIP call; attn_entry repeats the full validation.
   if (!q || !k || !v || !out) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || kv_len < 1 || n_q / n_kv > kMaxRows) return STD_E_SHAPE;
   const size_t need = attn_workspace_bytes(n_kv, n_q / n_kv, kv_len, dtype);
   if (need > kNoAllocScratchBytes) return STD_E_WORKSPACE;

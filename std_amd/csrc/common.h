@@ -30,15 +30,21 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return u >> 16;
 }
 
+// fp16 is carried as the compiler's half type (its conversions from float
+// round to nearest even, as torch's float -> float16 does).
+typedef _Float16 f16_t;
+
 template <typename T> __device__ __forceinline__ float to_f32(T x);
 template <> __device__ __forceinline__ float to_f32<float>(float x) { return x; }
 template <> __device__ __forceinline__ float to_f32<bf16_t>(bf16_t x) { return bf16_to_f32(x); }
+template <> __device__ __forceinline__ float to_f32<f16_t>(f16_t x) { return (float)x; }
 
 template <typename T> __device__ __forceinline__ T from_f32(float x);
 template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
   return (bf16_t)f32_to_bf16(x);
 }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return (f16_t)x; }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -100,6 +106,6 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 inline size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-inline int dtype_size(int dtype) { return dtype == STD_BF16 ? 2 : 4; }
+inline int dtype_size(int dtype) { return dtype == STD_F32 ? 4 : 2; }
 
 }  // namespace stdhip

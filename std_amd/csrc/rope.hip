@@ -29,14 +29,19 @@ rope_append_kernel(const T* __restrict__ qkv, long long qkv_rs, T* __restrict__ 
                    T* __restrict__ cv, int n_rows, int n_q, int n_kv, long long chs, int capacity,
                    const int32_t* __restrict__ len_dev, const int32_t* __restrict__ pos_dev, int pos_offset,
                    const float* __restrict__ inv_freq) {
+  // Every product is rounded to the dtype before the sum, as torch evaluates
+  // it: plain operators (round to nearest even) with multiply-add
+  // contraction off -- for fp16 the compiler would otherwise fuse x * cos
+  // into the add and drop that rounding.
+#pragma clang fp contract(off)
   const int row = blockIdx.x, head = blockIdx.y, j = threadIdx.x;
   const int pos = *pos_dev + pos_offset + row;
-  const float ang = __fmul_rn((float)pos, inv_freq[j]);
+  const float ang = (float)pos * inv_freq[j];
   const float c = rnd<T>(cosf(ang)), s = rnd<T>(sinf(ang));
   const T* src = qkv + (long long)row * qkv_rs + (long long)head * D;
   const float x1 = to_f32<T>(src[j]), x2 = to_f32<T>(src[j + HALF]);
-  const float lo = rnd<T>(__fadd_rn(rnd<T>(__fmul_rn(x1, c)), rnd<T>(__fmul_rn(-x2, s))));
-  const float hi = rnd<T>(__fadd_rn(rnd<T>(__fmul_rn(x2, c)), rnd<T>(__fmul_rn(x1, s))));
+  const float lo = rnd<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * s));
+  const float hi = rnd<T>(rnd<T>(x2 * c) + rnd<T>(x1 * s));
   if (head < n_q) {
     T* dst = q_out + ((long long)head * n_rows + row) * D;
     dst[j] = from_f32<T>(lo);
@@ -65,7 +70,7 @@ extern "C" int std_rope_append(const void* qkv, long long qkv_row_stride, void* 
                                const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
                                const float* inv_freq, int dtype, void* stream) {
   if (!qkv || !q_out || !cache_k || !cache_v || !len_dev || !pos_dev || !inv_freq) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_rows < 1 || n_rows > 65535 || n_q < 1 || n_kv < 1 || n_q % n_kv != 0 || capacity < 1)
     return STD_E_SHAPE;
   if (qkv_row_stride < (long long)(n_q + 2 * n_kv) * D) return STD_E_SHAPE;
@@ -76,6 +81,11 @@ extern "C" int std_rope_append(const void* qkv, long long qkv_row_stride, void* 
     hipLaunchKernelGGL(rope_append_kernel<bf16_t>, grid, dim3(HALF), 0, st, static_cast<const bf16_t*>(qkv),
                        qkv_row_stride, static_cast<bf16_t*>(q_out), static_cast<bf16_t*>(cache_k),
                        static_cast<bf16_t*>(cache_v), n_rows, n_q, n_kv, cache_head_stride, capacity, len_dev, pos_dev,
+                       pos_offset, inv_freq);
+  else if (dtype == STD_F16)
+    hipLaunchKernelGGL(rope_append_kernel<f16_t>, grid, dim3(HALF), 0, st, static_cast<const f16_t*>(qkv),
+                       qkv_row_stride, static_cast<f16_t*>(q_out), static_cast<f16_t*>(cache_k),
+                       static_cast<f16_t*>(cache_v), n_rows, n_q, n_kv, cache_head_stride, capacity, len_dev, pos_dev,
                        pos_offset, inv_freq);
   else
     hipLaunchKernelGGL(rope_append_kernel<float>, grid, dim3(HALF), 0, st, static_cast<const float*>(qkv),

@@ -799,7 +799,7 @@ extern "C" int std_select_topk(const void* q_text, const void* k, int n_q, int n
                                int n_visual, int k_select, int32_t* topk_out, double* scores_out, void* workspace,
                                size_t workspace_bytes, void* stream) {
   if (!q_text || !k || !visual_pos || !topk_out || !workspace) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (!select_shape_ok(n_q, n_kv, text_len, prompt_len, text_start, d, n_visual, k_select)) return STD_E_SHAPE;
   if (n_kv > 1 && k_head_stride < (long long)prompt_len * D) return STD_E_SHAPE;
   if (workspace_bytes < plan_select(n_q, n_kv, text_len, prompt_len, n_visual).total) return STD_E_WORKSPACE;
@@ -809,6 +809,9 @@ extern "C" int std_select_topk(const void* q_text, const void* k, int n_q, int n
   if (dtype == STD_BF16)
     return launch_select<bf16_t>(q_text, k, n_q, n_kv, text_len, prompt_len, text_start, k_head_stride, visual_pos,
                                  n_visual, k_select, topk_out, scores_out, workspace, st);
+  if (dtype == STD_F16)
+    return launch_select<f16_t>(q_text, k, n_q, n_kv, text_len, prompt_len, text_start, k_head_stride, visual_pos,
+                                n_visual, k_select, topk_out, scores_out, workspace, st);
   return launch_select<float>(q_text, k, n_q, n_kv, text_len, prompt_len, text_start, k_head_stride, visual_pos,
                               n_visual, k_select, topk_out, scores_out, workspace, st);
 }
@@ -828,7 +831,7 @@ extern "C" int std_compact_kv(const void* dense_k, const void* dense_v, void* sp
                               int dense_rows, long long sparse_head_stride, int sparse_rows, int dtype,
                               void* stream) {
   if (!dense_k || !dense_v || !sparse_k || !sparse_v || !idx) return STD_E_NULL;
-  if (dtype != STD_F32 && dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_kv < 1 || compact_len < 1 || dense_rows < 1 || sparse_rows < 1) return STD_E_SHAPE;
   if (compact_len > sparse_rows) return STD_E_RANGE;
   const int es = dtype_size(dtype);

@@ -19,11 +19,15 @@ HEAD_DIM = 128
 
 
 def _dtype_code(t: torch.Tensor) -> int:
+    """fp32, bf16 or fp16 (the reference loads its model in fp16); ops whose
+    kernels lack a dtype report STD_E_DTYPE from the library."""
     if t.dtype == torch.float32:
         return _lib.STD_F32
     if t.dtype == torch.bfloat16:
         return _lib.STD_BF16
-    raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16")
+    if t.dtype == torch.float16:
+        return _lib.STD_F16
+    raise TypeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16")
 
 
 def _check_device(*tensors: torch.Tensor) -> torch.device:
@@ -595,8 +599,8 @@ def gqa_decode_indexed(query: torch.Tensor, dense_k: torch.Tensor, dense_v: torc
     (see pad_index). Host length: kv_len keys. Device length: length[0] + 1
     keys (this step's row written at length[0]), planned for max_kv_len."""
     dev = _check_device(query, dense_k, dense_v, index, key_cache, value_cache)
-    if query.dtype != torch.bfloat16:
-        raise TypeError("gqa_decode_indexed: bf16 only")
+    if query.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("gqa_decode_indexed: bf16 or fp16")
     for name, t in (("dense_k", dense_k), ("dense_v", dense_v), ("key_cache", key_cache), ("value_cache", value_cache)):
         _check_cache_view(name, t)
         if t.dtype != query.dtype:
@@ -638,7 +642,7 @@ def gqa_decode_indexed(query: torch.Tensor, dense_k: torch.Tensor, dense_v: torc
     _lib.call("std_gqa_decode_indexed", query.data_ptr(), dense_k.data_ptr(), dense_v.data_ptr(), dense_k.shape[2],
               dense_k.stride(1), dense_v.stride(1), index.data_ptr(), index.stride(0), n_index, key_cache.data_ptr(),
               value_cache.data_ptr(), key_cache.stride(1), value_cache.stride(1), out.data_ptr(), n_q, n_kv, plan,
-              length.data_ptr() if length is not None else None, d, float(scale), _lib.STD_BF16, ws_ptr, ws_bytes,
+              length.data_ptr() if length is not None else None, d, float(scale), _dtype_code(query), ws_ptr, ws_bytes,
               _stream(dev))
     return out
 

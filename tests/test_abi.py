@@ -147,6 +147,7 @@ def test_verify_collect_validation():
         return lib.std_verify_attn_collect(*a.values())
     assert lib.std_verify_attn_collect_workspace_bytes(28, 4, 10, 4106, 128, 0, 3968) > 0
     assert call(dt=0) == -2                     # bf16 only
+    assert call(dt=2) == -2
     assert call(sc=NULL) == -1
     assert call(nk=16) == -1                    # new_k without new_v
     assert call(ql=11) == -3                    # (7 + 1) * 11 > 80 rows
@@ -218,9 +219,14 @@ def test_gemv_validation():
     assert lib.std_gemv_ex(16, 100, 16, 100, NULL, NULL, 0, 16, 64, 1, 64, 100, 0, 1, NULL) == -3
     assert lib.std_gemv_ex(16, 128, 16, 128, NULL, NULL, 0, 16, 64, 17, 64, 128, 0, 1, NULL) == -3
     assert lib.std_gemv_ex(16, 128, 16, 128, NULL, NULL, 0, 16, 64, 1, 64, 128, 0, 0, NULL) == -2
+    assert lib.std_gemv_ex(16, 128, 16, 128, NULL, NULL, 0, 16, 64, 1, 64, 128, 0, 2, NULL) == -2
     assert lib.std_gemv_ex(16, 128, 16, 128, NULL, 16, 10, 16, 64, 1, 64, 128, 0, 1, NULL) == -3  # residual stride
     assert lib.std_gemv_ex(16, 132, 16, 128, NULL, NULL, 0, 16, 64, 2, 64, 128, 1, 1, NULL) == -5  # x row stride
     assert lib.std_gemv(NULL, 128, 16, 128, NULL, 16, 64, 1, 64, 128, 1, NULL, 0, NULL) == -1
+    # the fused q|k|v projection: bf16 only
+    qkv = [16, 3584, 1, 3584, 16, 3584, NULL, 28, 4, 128, 16, 16, 16, 128 * 1024, 1024, 16, 16, 0, 16, NULL, 1e-6]
+    assert lib.std_qkv_rope_append(*qkv, 2, NULL) == -2
+    assert lib.std_qkv_rope_append(*qkv, 0, NULL) == -2
 
 
 def test_accept_and_append_validation():

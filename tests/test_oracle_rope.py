@@ -1,7 +1,7 @@
 """The rotary-embedding oracle pinned on the CPU: closed forms (position 0 is
 the identity), the rotation invariants (pair norms kept, scores depend only
 on the relative position) and torch's own CPU evaluation of the reference
-formula (modeling_qwen2_5_vl.py:656-671, 690-732) in bf16 and fp32."""
+formula (modeling_qwen2_5_vl.py:656-671, 690-732) in bf16, fp16 and fp32."""
 import numpy as np
 import torch
 
@@ -13,12 +13,16 @@ D, THETA = 128, 1e6
 def _x(n, seed, dtype):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(n, D, generator=g)
-    return x.to(torch.bfloat16).float().numpy() if dtype == "bf16" else x.numpy()
+    if dtype == "bf16":
+        return x.to(torch.bfloat16).float().numpy()
+    if dtype == "fp16":
+        return x.to(torch.float16).float().numpy()
+    return x.numpy()
 
 
 def test_position_zero_is_identity():
     inv = rope.inv_freq(THETA, D)
-    for dtype in ("bf16", "fp32"):
+    for dtype in ("bf16", "fp16", "fp32"):
         x = _x(5, 1, dtype)
         cos, sin = rope.cos_sin(np.zeros(5, dtype=np.int64), inv, dtype)
         assert (cos == 1).all() and (sin == 0).all()
@@ -57,14 +61,14 @@ def test_scores_depend_on_relative_position_only():
 def test_matches_torch_cpu_evaluation():
     """torch's CPU kernels evaluate the reference expression with their own
     cos/sin; the oracle agrees bit for bit except where the two cos/sin
-    evaluations round differently: never in bf16 for these positions; in
-    fp32 torch's cos/sin differ from the correctly rounded value by one ulp
+    evaluations round differently: never in bf16 or fp16 for these
+    positions; in fp32 torch's cos/sin differ from the correctly rounded value by one ulp
     for ~3 % of angles, which moves a result by at most a few fp32 ulps of
     the products (|x| < 5 here)."""
     inv = rope.inv_freq(THETA, D)
     inv_t = torch.from_numpy(inv)
     pos = np.array([0, 1, 7, 1023, 4096, 32767, 65537, 131071, 131081], dtype=np.int64)
-    for dtype, tdt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+    for dtype, tdt in (("bf16", torch.bfloat16), ("fp16", torch.float16), ("fp32", torch.float32)):
         x = _x(len(pos), 5, dtype)
         cos, sin = rope.cos_sin(pos, inv, dtype)
         got = rope.apply_rope(x, cos, sin, dtype)
@@ -75,7 +79,7 @@ def test_matches_torch_cpu_evaluation():
         rot = torch.cat([-xt[:, 64:], xt[:, :64]], dim=-1)
         ref = ((xt * tc) + (rot * ts)).float().numpy()
         diff = np.abs(got - ref)
-        if dtype == "bf16":
+        if dtype in ("bf16", "fp16"):
             np.testing.assert_array_equal(got, ref)
         else:
             assert diff.max() <= 1e-6 and (diff == 0).mean() > 0.9
