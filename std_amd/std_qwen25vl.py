@@ -530,7 +530,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     device-state steps eagerly.
 
     sparse_kv: "compact" gathers the selected prompt rows into the sparse
-    cache; "indexed" (bf16) has the draft read them from the dense cache
+    cache; "indexed" (bf16, fp16) has the draft read them from the dense cache
     through the per-head index lists instead (same keys, same results).
 
     round_hook (a test probe; None adds nothing): called once per round after
@@ -542,8 +542,8 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     lengths."""
     if sparse_kv not in SPARSE_KV_MODES:
         raise ValueError(f"Unsupported sparse_kv={sparse_kv!r}; choose one of {sorted(SPARSE_KV_MODES)}.")
-    if sparse_kv == "indexed" and model.dtype != torch.bfloat16:
-        raise ValueError("the index-addressed sparse cache serves bf16 models")
+    if sparse_kv == "indexed" and model.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("the index-addressed sparse cache serves bf16 and fp16 models")
     if verify_mode != "parallel":
         raise ValueError(f"Unsupported verify_mode={verify_mode!r}; the HIP path implements 'parallel'.")
     if verify_fallback != "none" or verify_margin_threshold is not None:

@@ -194,3 +194,86 @@ def test_rope_append_matches_oracle():
         print(f"[{name}] exact {(diff == 0).mean():.5f}, max diff {diff.max():.3g}", flush=True)
         assert (diff == 0).mean() > 0.995 and (diff <= bound).all()
     np.testing.assert_array_equal(vc[0, :, length:length + n].float().cpu().numpy(), x[:, NQ + NKV:].transpose(1, 0, 2))
+
+
+# -- the whole loop with an fp16 model ------------------------------------------
+# The tiny random decoder in fp16: projections go through torch (the HIP GEMVs
+# are bf16 only), every attention, rotary/append, norm, selection, compaction
+# and acceptance step through the library in fp16.
+
+def _tiny16():
+    from std_amd.decoder import DecoderConfig, RandomDecoder
+    cfg = DecoderConfig.tiny(layers=2)
+    return cfg, RandomDecoder(cfg, dev(), F16, seed=7)
+
+
+def _loop_inputs(cfg, seed, n_visual=1000, n_text=24):
+    g = torch.Generator().manual_seed(seed)
+    text = torch.randint(0, cfg.vocab_size - 2, (n_text,), generator=g)
+    ids = torch.cat([torch.full((n_visual,), cfg.video_token_id), text]).view(1, -1)
+    vis = torch.randn(n_visual, cfg.hidden_size, generator=g)
+    return {"input_ids": ids.to(dev()), "visual_embeds": vis.to(dev(), F16)}
+
+
+def test_loop_selection_and_compaction_from_fp16_prefill():
+    """Selection on an fp16 prefill's captured text queries equals the oracle
+    bit-exactly (fp64 scores of fp16 values); compact rows are bit copies."""
+    from std_amd.kv_cache import initialize_past_key_values
+    from std_amd.std_qwen25vl import (build_sparse_selection_from_queries, compact_sparse_prompt_cache,
+                                      prefill_prompt)
+    cfg, model = _tiny16()
+    inputs = _loop_inputs(cfg, 11)
+    P = inputs["input_ids"].shape[1]
+    announce(f"fp16 loop: selection from prefill P={P}")
+    pkv, _, _ = initialize_past_key_values(cfg, dev(), F16, P + 8)
+    prompt_ids, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
+    queries = list(model.captured_queries)
+    assert queries[0].dtype == F16 and torch.isfinite(queries[0]).all()
+    sel = build_sparse_selection_from_queries(queries, [layer[0].data for layer in pkv], prompt_ids,
+                                              cfg.video_token_id, text_start, target_k_plus_text=256,
+                                              num_key_value_heads=1)
+    want = ref_sel.build_sparse_selection([q.cpu() for q in queries], [layer[0].data[:, :, :P].cpu() for layer in pkv],
+                                          prompt_ids[0].cpu().tolist(), cfg.video_token_id, target_k_plus_text=256)
+    assert (sel.k, sel.prompt_len) == (want["k"], want["prompt_len"])
+    for layer in range(cfg.num_hidden_layers):
+        np.testing.assert_array_equal(sel.topk_positions[layer].numpy(), want["topk_positions"][layer])
+    sparse, _, sparse_len = initialize_past_key_values(cfg, dev(), F16, sel.compact_len + 4)
+    n = compact_sparse_prompt_cache(sparse, sparse_len, sel, pkv)
+    torch.cuda.synchronize()
+    for layer in range(cfg.num_hidden_layers):
+        idx = ref_sel.compact_index(want["non_visual_positions"], want["topk_positions"][layer][0])
+        for kind in range(2):
+            assert torch.equal(sparse[layer][kind].data[0, 0, :n].cpu(),
+                               pkv[layer][kind].data[0, 0, torch.as_tensor(idx)].cpu())
+
+
+def test_loop_graph_rounds_equal_eager_rounds_fp16():
+    """fp16 model: the graph-replayed rounds give the eager rounds' tokens and
+    accept lengths; lengths stay consistent; generation stops at EOS."""
+    from std_amd.std_qwen25vl import first_divergence, std_generate_qwen25vl
+    cfg, model = _tiny16()
+    inputs = _loop_inputs(cfg, 9)
+    announce("fp16 loop: STD eager vs graph rounds, 32 tokens, gamma 9")
+    kw = dict(max_new_tokens=32, gamma=9, target_k_plus_text=256, ignore_eos=True)
+    eager, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, use_graphs=False, **kw)
+    graph, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, use_graphs=True, **kw)
+    assert eager.generate_len == graph.generate_len == 32 and graph.decode_rounds >= 3
+    assert all(0 <= a <= p for a, p in zip(graph.accept_lengths, graph.proposed_lengths))
+    assert graph.accept_lengths == eager.accept_lengths
+    assert first_divergence(graph.output_ids, eager.output_ids) is None
+    gen = graph.output_ids[0, -graph.generate_len:].tolist()
+    eos = gen[5]
+    stop, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, eos, use_graphs=True,
+                                    **dict(kw, ignore_eos=False))
+    assert stop.output_ids[0, -stop.generate_len:].tolist() == gen[:gen.index(eos) + 1]
+
+
+def test_loop_indexed_sparse_kv_equals_compact_fp16():
+    from std_amd.std_qwen25vl import std_generate_qwen25vl
+    cfg, model = _tiny16()
+    inputs = _loop_inputs(cfg, 9)
+    announce("fp16 loop: sparse_kv indexed vs compact, graphs")
+    kw = dict(max_new_tokens=24, gamma=9, target_k_plus_text=256, ignore_eos=True, use_graphs=True)
+    comp, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, **kw)
+    idx, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, sparse_kv="indexed", **kw)
+    assert torch.equal(idx.output_ids, comp.output_ids) and idx.accept_lengths == comp.accept_lengths

@@ -106,7 +106,7 @@ def test_std_generate_rejects_unsupported_options(kwargs):
         std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
 
 
-def test_indexed_sparse_kv_needs_bf16():
+def test_indexed_sparse_kv_needs_a_16_bit_model():
     fp32_model = types.SimpleNamespace(dtype=torch.float32)
     with pytest.raises(ValueError):
         std_generate_qwen25vl(fp32_model, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8,
