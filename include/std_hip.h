@@ -458,7 +458,7 @@ int std_greedy_accept(const void* logits, long long logits_row_stride, int q_row
  *   rows of KV head g's query heads at position i (the hook's
  *   q.float().reshape(...).mean(dim=2)); i < q_len. The visual keys form one
  *   contiguous range of prompt keys (vis_end <= kv_len - q_len), as the video
- *   tokens of a prompt do. bf16 only; (n_q / n_kv + 1) * q_len <= 80 (the
+ *   tokens of a prompt do. bf16 or fp16; (n_q / n_kv + 1) * q_len <= 80 (the
  *   collector's q_len rows use the padding rows of the verify's last row
  *   tile: gamma + 1 <= 10 at seven query heads per KV head).
  * ------------------------------------------------------------------------ */

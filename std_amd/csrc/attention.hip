@@ -416,14 +416,15 @@ __device__ __forceinline__ void coll_finish(const float* __restrict__ logits, co
 // The verify merge and the collector finish in one launch: grid
 // (n_rows + n_col_blocks, n_kv); blocks x < n_rows merge attention row x (none
 // when the verify ran as one split), the others finish 1024 visual keys each.
+template <typename T>
 __global__ void __launch_bounds__(kMergeThreads)
-merge_coll_kernel(const half_t* __restrict__ ws_o, const float2* __restrict__ ws_ml, bf16_t* __restrict__ out,
+merge_coll_kernel(const half_t* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
                   int n_split, int q_len, int group, int n_rows, const float* __restrict__ logits,
                   const float2* __restrict__ stats, float* __restrict__ scores, int n_vtiles, long long score_hs,
                   int vis_begin, int vis_end) {
   static_assert(kMergeThreads == 256, "the collector finish runs 256 threads");
   if ((int)blockIdx.x < n_rows)
-    merge_row<bf16_t, half_t>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
+    merge_row<T, half_t>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
   else
     coll_finish(logits, stats, scores, score_hs, q_len, n_split, n_vtiles, vis_begin, vis_end, blockIdx.x - n_rows,
                 blockIdx.y);
@@ -460,7 +461,8 @@ __device__ __forceinline__ i16x4 pack_bf16x4(float a, float b, float c, float d)
 // The 16-bit element arithmetic of the bf16 kernels, for bf16 (bf16_t) or
 // fp16 (f16_t) caches: the MFMA operand vectors, QK^T / PV MFMAs of 32 and
 // 16 contraction elements, the packing of four floats (probabilities, output
-// rows; round to nearest even) and the element 1.0. Storage is the 16-bit
+// rows; round to nearest even), the element 1.0, and one element's bit
+// pattern to fp32 and back (round to nearest even). Storage is the 16-bit
 // pattern either way, so loads, the DMA ring and the appends are shared.
 template <typename E> struct Elem;
 template <> struct Elem<bf16_t> {
@@ -474,6 +476,8 @@ template <> struct Elem<bf16_t> {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ i16x4 pack4(float a, float b, float c, float d) { return pack_bf16x4(a, b, c, d); }
+  static __device__ __forceinline__ float to_f32(uint32_t bits) { return bf16_to_f32(bits); }
+  static __device__ __forceinline__ uint32_t round_bits(float f) { return f32_to_bf16(f); }
 };
 template <> struct Elem<f16_t> {
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
@@ -488,6 +492,10 @@ template <> struct Elem<f16_t> {
   static __device__ __forceinline__ i16x4 pack4(float a, float b, float c, float d) {
     return __builtin_bit_cast(i16x4, __builtin_convertvector(f32x4{a, b, c, d}, v4));
   }
+  static __device__ __forceinline__ float to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+  }
+  static __device__ __forceinline__ uint32_t round_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 };
 
 __device__ __forceinline__ float xor16_max(float x) {
@@ -538,7 +546,6 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   using EL = Elem<E>;
   using v8 = typename EL::v8;                    // 8 elements: the 16x16x32 MFMA operands
   using v4 = typename EL::v4;                    // 4 elements: the 16x16x16 MFMA operands
-  static_assert(!COLL || std::is_same<E, bf16_t>::value, "the collector rides the bf16 verify");
   __shared__ __align__(16) char ring[NSTAGE * STAGEB];
   // With the collector the query rows are staged in LDS by the ring's DMA
   // (its group means read every row of the group): 1.7 us less per 128k
@@ -727,40 +734,68 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   }
   // Collector rows: lanes q_off .. 15 of the key-split waves (the padding rows
   // of the last row tile, R + q_len <= 80) carry position i = ln - q_off's
-  // group-mean query, the fp32 mean of the group's bf16 query rows
+  // group-mean query, the fp32 mean of the group's 16-bit query rows
   // (modeling_qwen2_5_vl.py hook -> dynamic_selection.py:509-512), split into
-  // a bf16 head qf and a bf16 remainder qlo, so that K.qf + K.qlo carries the
-  // fp32 mean's precision through bf16 MFMAs.
+  // a 16-bit head qf and a 16-bit remainder qlo (bf16 or fp16, as the cache),
+  // so that K.qf + K.qlo carries the mean's precision through the MFMAs.
+  // fp16 rows are first scaled by 2^-k, k chosen per row so that the largest
+  // element lies in [2^14, 2^15): the remainders then stay normal fp16
+  // numbers. Subnormal remainders do not survive the MFMA (unscaled, 66 % of
+  // them were subnormal at 128k and 20 of 523776 scores were off by up to
+  // 3.9e-4 relative). The logits take 2^k back through coll_scale.
   const int q_off = 16 - q_len;
   v8 qlo[4];
+  float coll_scale = scale_log2;        // collector logits (log2 domain) = (K.qf + K.qlo) * coll_scale
   if constexpr (COLL) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) qlo[c] = v8{};
-    if (ksw && ln >= q_off) {
-      const int i = ln - q_off;
+    if (ksw) {                          // wave-uniform; the four lanes of a row (lg) share ln
+      const bool crow = ln >= q_off;
+      float mean[4][8];
+      float amax = 0.f;
+      if (crow) {
+        const int i = ln - q_off;
+        const float inv = 1.f / (float)group;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        float m8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int hl = 0; hl < group; ++hl) {
-          const uint4 v4 = *reinterpret_cast<const uint4*>(qs + sw_off(hl * q_len + i, 4 * c + lg));
-          const uint32_t w4[4] = {v4.x, v4.y, v4.z, v4.w};
+        for (int c = 0; c < 4; ++c) {
+          float m8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          for (int hl = 0; hl < group; ++hl) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(qs + sw_off(hl * q_len + i, 4 * c + lg));
+            const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            m8[2 * e] += bf16_to_f32(w4[e] & 0xffffu);
-            m8[2 * e + 1] += bf16_to_f32(w4[e] >> 16);
+            for (int e = 0; e < 4; ++e) {
+              m8[2 * e] += EL::to_f32(w4[e] & 0xffffu);
+              m8[2 * e + 1] += EL::to_f32(w4[e] >> 16);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            mean[c][e] = m8[e] * inv;
+            amax = fmaxf(amax, fabsf(mean[c][e]));
           }
         }
-        const float inv = 1.f / (float)group;
-        i16x8 hi, lo;
+      }
+      float sx = 1.f;
+      if constexpr (std::is_same<E, f16_t>::value) {
+        amax = xor32_max(xor16_max(amax));
+        const int kx = part_exp(amax);
+        sx = exp2i(-kx);
+        coll_scale = scale_log2 * exp2i(kx);
+      }
+      if (crow) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float mean = m8[e] * inv;
-          const uint32_t h = f32_to_bf16(mean);
-          hi[e] = (short)h;
-          lo[e] = (short)f32_to_bf16(mean - bf16_to_f32(h));
+        for (int c = 0; c < 4; ++c) {
+          i16x8 hi, lo;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float m = mean[c][e] * sx;
+            const uint32_t h = EL::round_bits(m);
+            hi[e] = (short)h;
+            lo[e] = (short)EL::round_bits(m - EL::to_f32(h));
+          }
+          qf[c] = __builtin_bit_cast(v8, hi);
+          qlo[c] = __builtin_bit_cast(v8, lo);
         }
-        qf[c] = __builtin_bit_cast(v8, hi);
-        qlo[c] = __builtin_bit_cast(v8, lo);
       }
     }
   }
@@ -897,7 +932,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const bool vis = key0 + i >= ga.vis_begin && key0 + i < ga.vis_end;
-          z[i] = vis ? (sc[i] + sl[i]) * scale_log2 : -INFINITY;
+          z[i] = vis ? (sc[i] + sl[i]) * coll_scale : -INFINITY;
         }
         const int vt = kb / TK - ga.vis_begin / TK;           // wave-uniform
         if (vt >= 0 && vt < ga.n_vtiles) {
@@ -1527,7 +1562,7 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
                          long long score_hs, void* ws, size_t ws_bytes, void* stream) {
   if (!q || !k || !v || !out || !scores) return STD_E_NULL;
   if ((nk == nullptr) != (nv == nullptr)) return STD_E_NULL;
-  if (dtype != STD_BF16) return STD_E_DTYPE;
+  if (dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len) return STD_E_SHAPE;
   const int group = n_q / n_kv;
   // the collector rows fill the padding lanes of the five-row-tile layout's last row tile
@@ -1543,7 +1578,7 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
   if (!aligned16(ws)) return STD_E_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int R = group * q_len;
-  const SplitPlan p = plan_splits(n_kv, R, kv_len, STD_BF16);
+  const SplitPlan p = plan_splits(n_kv, R, kv_len, STD_BF16);        // bf16 and fp16 plan alike
   const WsLayout wl = ws_layout(n_kv, R, p, part_bytes_of(STD_BF16, R));
   char* base = static_cast<char*>(ws);
   half_t* ws_o = p.n_split > 1 ? reinterpret_cast<half_t*>(base + wl.o_off) : nullptr;      // R > 16: fp16
@@ -1551,19 +1586,23 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
   const CollArgs ca{reinterpret_cast<float*>(base + cl.logits_off), reinterpret_cast<float2*>(base + cl.stats_off),
                     cl.n_vtiles, vis_begin, vis_end};
   const int n_new = nk ? q_len : 0;
-  hipLaunchKernelGGL((attn_bf16_kernel<5, false, false, true>), dim3(p.n_split, n_kv, 1), dim3(Bf16Cfg<5>::kThreads),
-                     0, st, static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
-                     static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs, v_hs,
-                     scale * 1.4426950408889634f, p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
-                     static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, BatchStrides{0, 0, 0, 0, 0}, nullptr, ca,
-                     nullptr);
-  int s = launch_status();
-  if (s != 0) return s;
   const int n_rows = p.n_split > 1 ? R : 0;
-  hipLaunchKernelGGL(merge_coll_kernel, dim3(n_rows + (cl.n_vtiles + 15) / 16, n_kv), dim3(kMergeThreads), 0, st,
-                     ws_o, ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len, group, n_rows, ca.logits, ca.stats,
-                     scores, cl.n_vtiles, n_kv > 1 ? score_hs : 0LL, vis_begin, vis_end);
-  return launch_status();
+  auto run = [&](auto elem) -> int {
+    using E = decltype(elem);
+    hipLaunchKernelGGL((attn_bf16_kernel<5, false, false, true, E>), dim3(p.n_split, n_kv, 1),
+                       dim3(Bf16Cfg<5>::kThreads), 0, st, static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k),
+                       static_cast<bf16_t*>(v), static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs,
+                       v_hs, scale * 1.4426950408889634f, p.ntiles, p.n_split, kv_len - q_len,
+                       static_cast<const bf16_t*>(nk), static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new,
+                       BatchStrides{0, 0, 0, 0, 0}, nullptr, ca, nullptr);
+    const int s = launch_status();
+    if (s != 0) return s;
+    hipLaunchKernelGGL(merge_coll_kernel<E>, dim3(n_rows + (cl.n_vtiles + 15) / 16, n_kv), dim3(kMergeThreads), 0,
+                       st, ws_o, ws_ml, static_cast<E*>(out), p.n_split, q_len, group, n_rows, ca.logits, ca.stats,
+                       scores, cl.n_vtiles, n_kv > 1 ? score_hs : 0LL, vis_begin, vis_end);
+    return launch_status();
+  };
+  return dtype == STD_BF16 ? run(bf16_t{}) : run(f16_t{});
 }
 
 }  // namespace

@@ -810,7 +810,7 @@ def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value
     (VerificationCollectorV3._hook, dynamic_selection.py:504-519, riding the
     verify forward at modeling_qwen2_5_vl.py:1063-1067).
 
-    query [1, n_q, q_len, D] bf16; key_cache / value_cache [1, n_kv, S, D]
+    query [1, n_q, q_len, D] bf16 or fp16; key_cache / value_cache [1, n_kv, S, D]
     cache views (read in place). Without new_key/new_value the caches hold
     kv_len (default S) keys including this step's q_len rows; with them
     ([1, n_kv, q_len, D]) those rows are appended at kv_len - q_len first.
@@ -819,8 +819,8 @@ def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value
     q_len positions, the softmax over the visual keys [vis_begin, vis_end) of
     the group-mean query of KV head g."""
     dev = _check_device(query, key_cache, value_cache)
-    if query.dtype != torch.bfloat16:
-        raise TypeError("the collector path is bf16")
+    if query.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("the collector path is bf16 or fp16")
     if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
         raise TypeError("query and caches must share a dtype")
     _check_cache_view("key_cache", key_cache)
@@ -866,6 +866,6 @@ def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value
               new_key.data_ptr() if appending else None, new_value.data_ptr() if appending else None,
               out.data_ptr(), n_q, n_kv, q_len, int(kv_len), d, key_cache.stride(1), value_cache.stride(1),
               new_key.stride(1) if appending else 0, new_key.stride(2) if appending else 0, float(scale),
-              _lib.STD_BF16, int(vis_begin), int(vis_end), scores.data_ptr(), scores.stride(0), ws_ptr, ws_bytes,
+              _dtype_code(query), int(vis_begin), int(vis_end), scores.data_ptr(), scores.stride(0), ws_ptr, ws_bytes,
               _stream(dev))
     return out, scores

@@ -146,8 +146,8 @@ def test_verify_collect_validation():
         a = dict(args, **kw)
         return lib.std_verify_attn_collect(*a.values())
     assert lib.std_verify_attn_collect_workspace_bytes(28, 4, 10, 4106, 128, 0, 3968) > 0
-    assert call(dt=0) == -2                     # bf16 only
-    assert call(dt=2) == -2
+    assert call(dt=0) == -2                     # bf16 or fp16
+    assert call(dt=3) == -2
     assert call(sc=NULL) == -1
     assert call(nk=16) == -1                    # new_k without new_v
     assert call(ql=11) == -3                    # (7 + 1) * 11 > 80 rows

@@ -14,27 +14,30 @@ from tests.gpu_helpers import announce, cache_buffer, dev
 pytestmark = pytest.mark.gpu
 
 # Scores: fp32 sums of exp2 of fp32 logits whose queries carry the fp32 mean
-# (bf16 head + bf16 remainder), against fp64: relative 2e-4.
+# (bf16 head + bf16 remainder; fp16 head + fp16 remainder for fp16 caches),
+# against fp64: relative 2e-4.
 RTOL, ATOL = 2e-4, 1e-9
 
 
-def _layer(wname, layer, prompt_len=None, q_len=None):
+def _layer(wname, layer, prompt_len=None, q_len=None, dtype=torch.bfloat16):
     w = WORKLOADS[wname]
     x = make_layer(w, layer, prompt_len=prompt_len)
     if q_len is not None and q_len != x["q_verify"].shape[2]:
         x = dict(x, q_verify=x["q_verify"][:, :, :q_len].contiguous(), new_k=x["new_k"][:, :, :q_len].contiguous(),
                  new_v=x["new_v"][:, :, :q_len].contiguous())
+    if dtype != torch.bfloat16:
+        x = {n: x[n].to(dtype) for n in ("q_verify", "k", "v", "new_k", "new_v")}
     k = torch.cat([x["k"], x["new_k"]], 2)
     v = torch.cat([x["v"], x["new_v"]], 2)
     return w, x, k, v
 
 
-def _check(wname, layer, vis_begin, vis_end, prompt_len=None, q_len=None, append=False):
-    w, x, k, v = _layer(wname, layer, prompt_len, q_len)
+def _check(wname, layer, vis_begin, vis_end, prompt_len=None, q_len=None, append=False, dtype=torch.bfloat16):
+    w, x, k, v = _layer(wname, layer, prompt_len, q_len, dtype)
     q = x["q_verify"]
     Q, kv_len = q.shape[2], k.shape[2]
     announce(f"collector {wname} layer={layer} kv_len={kv_len} q_len={Q} visual=[{vis_begin},{vis_end}) "
-             f"append={append}")
+             f"append={append} dtype={dtype}")
     kb = cache_buffer(k, kv_len + 29)
     vb = cache_buffer(v, kv_len + 29)
     qd = q.to(dev())
@@ -78,6 +81,14 @@ def test_collector_c4_full_context_lognormal_keys():
     """131082 keys with heavy-tailed key norms, the 128k-context verify."""
     w = WORKLOADS["c4"]
     _check("c4", 0, 0, w.prompt_len - w.text_len, append=True)
+
+
+@pytest.mark.parametrize("wname", ["c2", "c4"])
+def test_collector_fp16(wname):
+    """fp16 caches and queries (the dtype the reference loads its model in):
+    the same workloads' values converted to fp16, with the fused append."""
+    w = WORKLOADS[wname]
+    _check(wname, 0, 0, w.prompt_len - w.text_len, append=True, dtype=torch.float16)
 
 
 def test_collector_class_on_a_decoder_verify_forward():
