@@ -461,8 +461,8 @@ __device__ __forceinline__ i16x4 pack_bf16x4(float a, float b, float c, float d)
 // The 16-bit element arithmetic of the bf16 kernels, for bf16 (bf16_t) or
 // fp16 (f16_t) caches: the MFMA operand vectors, QK^T / PV MFMAs of 32 and
 // 16 contraction elements, the packing of four floats (probabilities, output
-// rows; round to nearest even), the element 1.0, and one element's bit
-// pattern to fp32 and back (round to nearest even). Storage is the 16-bit
+// rows; round to nearest even), the element 1.0, one element's bit pattern
+// to fp32, and the split of an fp32 value into a 16-bit head and remainder. Storage is the 16-bit
 // pattern either way, so loads, the DMA ring and the appends are shared.
 template <typename E> struct Elem;
 template <> struct Elem<bf16_t> {
@@ -477,7 +477,11 @@ template <> struct Elem<bf16_t> {
   }
   static __device__ __forceinline__ i16x4 pack4(float a, float b, float c, float d) { return pack_bf16x4(a, b, c, d); }
   static __device__ __forceinline__ float to_f32(uint32_t bits) { return bf16_to_f32(bits); }
-  static __device__ __forceinline__ uint32_t round_bits(float f) { return f32_to_bf16(f); }
+  static __device__ __forceinline__ void split(float m, short& hi, short& lo) {
+    const uint32_t h = f32_to_bf16(m);
+    hi = (short)h;
+    lo = (short)f32_to_bf16(m - bf16_to_f32(h));
+  }
 };
 template <> struct Elem<f16_t> {
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
@@ -495,7 +499,16 @@ template <> struct Elem<f16_t> {
   static __device__ __forceinline__ float to_f32(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
   }
-  static __device__ __forceinline__ uint32_t round_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+  // The head comes from one conversion instruction (round toward zero) and
+  // the remainder is taken against that same value. Written as two plain
+  // fp16 roundings, the compiler formed the head twice, once from the fp32
+  // product and once inside a mixed-precision FMA from the exact product, and
+  // where the two differed head + remainder was off by a whole fp16 ulp.
+  static __device__ __forceinline__ void split(float m, short& hi, short& lo) {
+    const auto h2 = __builtin_amdgcn_cvt_pkrtz(m, 0.f);
+    hi = __builtin_bit_cast(short, h2[0]);
+    lo = __builtin_bit_cast(short, (_Float16)(m - (float)h2[0]));
+  }
 };
 
 __device__ __forceinline__ float xor16_max(float x) {
@@ -738,64 +751,36 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   // (modeling_qwen2_5_vl.py hook -> dynamic_selection.py:509-512), split into
   // a 16-bit head qf and a 16-bit remainder qlo (bf16 or fp16, as the cache),
   // so that K.qf + K.qlo carries the mean's precision through the MFMAs.
-  // fp16 rows are first scaled by 2^-k, k chosen per row so that the largest
-  // element lies in [2^14, 2^15): the remainders then stay normal fp16
-  // numbers. Subnormal remainders do not survive the MFMA (unscaled, 66 % of
-  // them were subnormal at 128k and 20 of 523776 scores were off by up to
-  // 3.9e-4 relative). The logits take 2^k back through coll_scale.
   const int q_off = 16 - q_len;
   v8 qlo[4];
-  float coll_scale = scale_log2;        // collector logits (log2 domain) = (K.qf + K.qlo) * coll_scale
   if constexpr (COLL) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) qlo[c] = v8{};
-    if (ksw) {                          // wave-uniform; the four lanes of a row (lg) share ln
-      const bool crow = ln >= q_off;
-      float mean[4][8];
-      float amax = 0.f;
-      if (crow) {
-        const int i = ln - q_off;
+    if (ksw && ln >= q_off) {
+      const int i = ln - q_off;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float m8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int hl = 0; hl < group; ++hl) {
+          const uint4 raw = *reinterpret_cast<const uint4*>(qs + sw_off(hl * q_len + i, 4 * c + lg));
+          const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            m8[2 * e] += EL::to_f32(w4[e] & 0xffffu);
+            m8[2 * e + 1] += EL::to_f32(w4[e] >> 16);
+          }
+        }
         const float inv = 1.f / (float)group;
+        i16x8 hi, lo;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          float m8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-          for (int hl = 0; hl < group; ++hl) {
-            const uint4 raw = *reinterpret_cast<const uint4*>(qs + sw_off(hl * q_len + i, 4 * c + lg));
-            const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              m8[2 * e] += EL::to_f32(w4[e] & 0xffffu);
-              m8[2 * e + 1] += EL::to_f32(w4[e] >> 16);
-            }
-          }
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            mean[c][e] = m8[e] * inv;
-            amax = fmaxf(amax, fabsf(mean[c][e]));
-          }
+        for (int e = 0; e < 8; ++e) {
+          short h, l;
+          EL::split(m8[e] * inv, h, l);
+          hi[e] = h;
+          lo[e] = l;
         }
-      }
-      float sx = 1.f;
-      if constexpr (std::is_same<E, f16_t>::value) {
-        amax = xor32_max(xor16_max(amax));
-        const int kx = part_exp(amax);
-        sx = exp2i(-kx);
-        coll_scale = scale_log2 * exp2i(kx);
-      }
-      if (crow) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          i16x8 hi, lo;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float m = mean[c][e] * sx;
-            const uint32_t h = EL::round_bits(m);
-            hi[e] = (short)h;
-            lo[e] = (short)EL::round_bits(m - EL::to_f32(h));
-          }
-          qf[c] = __builtin_bit_cast(v8, hi);
-          qlo[c] = __builtin_bit_cast(v8, lo);
-        }
+        qf[c] = __builtin_bit_cast(v8, hi);
+        qlo[c] = __builtin_bit_cast(v8, lo);
       }
     }
   }
@@ -932,7 +917,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const bool vis = key0 + i >= ga.vis_begin && key0 + i < ga.vis_end;
-          z[i] = vis ? (sc[i] + sl[i]) * coll_scale : -INFINITY;
+          z[i] = vis ? (sc[i] + sl[i]) * scale_log2 : -INFINITY;
         }
         const int vt = kb / TK - ga.vis_begin / TK;           // wave-uniform
         if (vt >= 0 && vt < ga.n_vtiles) {

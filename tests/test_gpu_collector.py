@@ -32,7 +32,8 @@ def _layer(wname, layer, prompt_len=None, q_len=None, dtype=torch.bfloat16):
     return w, x, k, v
 
 
-def _check(wname, layer, vis_begin, vis_end, prompt_len=None, q_len=None, append=False, dtype=torch.bfloat16):
+def _check(wname, layer, vis_begin, vis_end, prompt_len=None, q_len=None, append=False, dtype=torch.bfloat16,
+           rtol=RTOL):
     w, x, k, v = _layer(wname, layer, prompt_len, q_len, dtype)
     q = x["q_verify"]
     Q, kv_len = q.shape[2], k.shape[2]
@@ -57,7 +58,7 @@ def _check(wname, layer, vis_begin, vis_end, prompt_len=None, q_len=None, append
     want = ref_coll.verification_scores(q, k, np.arange(vis_begin, vis_end))
     got = scores.double().cpu().numpy()
     assert np.isfinite(got).all()
-    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(got, want, rtol=rtol, atol=ATOL)
     np.testing.assert_allclose(got.sum(axis=1), Q, rtol=1e-4)
 
 
@@ -86,9 +87,12 @@ def test_collector_c4_full_context_lognormal_keys():
 @pytest.mark.parametrize("wname", ["c2", "c4"])
 def test_collector_fp16(wname):
     """fp16 caches and queries (the dtype the reference loads its model in):
-    the same workloads' values converted to fp16, with the fused append."""
+    the same workloads' values converted to fp16, with the fused append. An
+    fp16 head + fp16 remainder carries about 22 bits of the mean, so the
+    bound is 2e-5 relative (1.9e-6 measured at 131082 keys); a head formed
+    twice with different roundings left 4e4 scores beyond 1e-5."""
     w = WORKLOADS[wname]
-    _check(wname, 0, 0, w.prompt_len - w.text_len, append=True, dtype=torch.float16)
+    _check(wname, 0, 0, w.prompt_len - w.text_len, append=True, dtype=torch.float16, rtol=2e-5)
 
 
 def test_collector_class_on_a_decoder_verify_forward():
