@@ -520,7 +520,8 @@ def main():
         "salient_selected_frac": salient_frac_selected,
         "select_compact_ms_first_call": round(select_ms_first, 3),
         "roofline": {
-            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false> + attn_merge_kernel<bf16, fp16 partials>)",
+            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false, false, unsigned short> split + "
+                      "attn_merge_kernel<unsigned short, _Float16> merge)",
             "bound": "hbm",
             "achieved": round(verify_gbps, 1),
             "peak": HBM_PEAK_GBPS,
