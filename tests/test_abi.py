@@ -91,13 +91,15 @@ def test_split_plan():
     launch (112 problems) and decodes of at most five tiles stream unsplit,
     and 32 / 64 problems keep their 256-workgroup plans."""
     lib = _lib.load_library()
-    bf16, f32 = 1, 0
+    bf16, f32, f16 = 1, 0, 2
     for n_prob, rows, kv_len, want in [(4, 7, 1034, 17), (4, 7, 1043, 17), (4, 7, 131072, 64), (4, 70, 131082, 64),
                                         (112, 7, 1034, 1), (112, 7, 2048, 1), (64, 7, 1034, 4), (64, 7, 2048, 4),
                                         (32, 7, 1034, 8), (32, 7, 2048, 8), (224, 7, 1034, 1), (4, 7, 320, 1),
                                         (4, 7, 400, 7), (4, 7, 64, 1), (4, 7, 1, 1), (4, 70, 4106, 64),
                                         (4, 70, 16394, 64), (4, 70, 65546, 64)]:
         assert lib.std_attn_split_count(n_prob, rows, kv_len, bf16) == want, (n_prob, rows, kv_len)
+        # fp16 runs the same kernels, partials and workspace layout as bf16
+        assert lib.std_attn_split_count(n_prob, rows, kv_len, f16) == want, (n_prob, rows, kv_len)
     # fp32 and multi-row-tile launches split to fill the GPU whatever the merge costs
     assert lib.std_attn_split_count(4, 7, 320, f32) == 5
     assert lib.std_attn_split_count(112, 70, 1034, bf16) == 2
