@@ -18,6 +18,7 @@ Prints one JSON line (value = draft tokens/s of the attention hot path).
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -50,6 +51,9 @@ def parse_args():
     ap.add_argument("--sparse-kv", default="compact", choices=["compact", "indexed"],
                     help="c5: draft reads the selected prompt rows from a compacted copy or through index lists")
     ap.add_argument("--layers", type=int, default=None, help="override the layer count (default: workload's)")
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"],
+                    help="c2-c4: cache, query and logit element type (fp16 is the dtype the reference loads its "
+                         "model in; the headline is bf16)")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cold-iters", type=int, default=10)
     ap.add_argument("--pmc-run", action="store_true",
@@ -136,6 +140,8 @@ def main():
         run_stream(args)
         return
     w = WORKLOADS[args.workload]
+    if args.dtype == "fp16":
+        w = dataclasses.replace(w, dtype=torch.float16)
     if args.pmc_run:
         pmc_run(w)
         return
@@ -446,7 +452,9 @@ def main():
 
     draft_tokens_per_s = G * args.steps / elapsed
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"verify_attn_{w.name}_traffic.json")
+    # counter passes are per element type (the committed ones are bf16)
+    tsuffix = "_fp16" if w.dtype == torch.float16 else ""
+    tpath = os.path.join(ROOT, "profiles", f"verify_attn_{w.name}{tsuffix}_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -462,7 +470,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if w.dtype == torch.bfloat16 else "fp32",
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16"}.get(w.dtype, "fp32"),
         "data": "synthetic (device-generated, seeded; selection + compaction run on it)",
         "config": {
             "workload": f"{w.name}: {L}-layer attention stack, {Hq}q/{Hkv}kv heads, d={D}, context {P} "
@@ -520,8 +528,9 @@ def main():
         "salient_selected_frac": salient_frac_selected,
         "select_compact_ms_first_call": round(select_ms_first, 3),
         "roofline": {
-            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false, false, unsigned short> split + "
-                      "attn_merge_kernel<unsigned short, _Float16> merge)",
+            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false, false, {e}> split + "
+                      "attn_merge_kernel<{e}, _Float16> merge)".format(
+                          e="_Float16" if w.dtype == torch.float16 else "unsigned short"),
             "bound": "hbm",
             "achieved": round(verify_gbps, 1),
             "peak": HBM_PEAK_GBPS,
