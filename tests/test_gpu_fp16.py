@@ -50,6 +50,31 @@ def test_verify_matches_oracle(kv):
     assert_close(out, ref.verify_attention(q, k, v), F16)
 
 
+@pytest.mark.parametrize("kind,kv", [("decode", 16384), ("decode", 131072), ("verify", 16394), ("verify", 131082)])
+def test_large_magnitudes_stay_finite_and_accurate(kind, kv):
+    """fp16 tops out at 65504: values near it in V and logits sharpened about
+    16x (q and k scaled by 4, so the softmax is dominated by a few keys) must
+    neither overflow an intermediate (split partials, the key-split combine,
+    the merge) nor lose accuracy. Bound: the fp16 tolerance with the absolute
+    part scaled by the value scale."""
+    g = torch.Generator().manual_seed(700 + kv)
+    rows = 1 if kind == "decode" else 10
+    vscale = 15000.0
+    k = (torch.randn(1, NKV, kv, D, generator=g) * 4).to(F16)
+    v = (torch.randn(1, NKV, kv, D, generator=g) * vscale).clamp(-60000, 60000).to(F16)
+    q = (torch.randn(1, NQ, rows, D, generator=g) * 4).to(F16)
+    announce(f"fp16 large magnitudes {kind} kv={kv}")
+    kb, vb = cache_buffer(k, kv + 7)[:, :, :kv], cache_buffer(v, kv + 7)[:, :, :kv]
+    if kind == "decode":
+        out, want = ops.gqa_decode(q.to(dev()), kb, vb), ref.gqa_sdpa(q, k, v)
+    else:
+        out, want = ops.verify_attention(q.to(dev()), kb, vb), ref.verify_attention(q, k, v)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, rtol=5e-3, atol=5e-4 * vscale)
+
+
 @pytest.mark.parametrize("kv", [130, 16394])
 def test_append_paths_write_the_rows_and_match_oracle(kv):
     Q = 10
