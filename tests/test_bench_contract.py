@@ -21,5 +21,5 @@ def test_more_than_one_gpu_is_refused_before_any_device_work():
 def test_options_include_the_driver_contract():
     r = subprocess.run([sys.executable, BENCH, "--help"], capture_output=True, text=True, timeout=60, cwd=ROOT)
     assert r.returncode == 0
-    for opt in ("--gpus", "--steps", "--warmup", "--workload"):
+    for opt in ("--gpus", "--steps", "--warmup", "--workload", "--dtype"):
         assert opt in r.stdout
