@@ -462,8 +462,9 @@ __device__ __forceinline__ i16x4 pack_bf16x4(float a, float b, float c, float d)
 // fp16 (f16_t) caches: the MFMA operand vectors, QK^T / PV MFMAs of 32 and
 // 16 contraction elements, the packing of four floats (probabilities, output
 // rows; round to nearest even), the element 1.0, one element's bit pattern
-// to fp32, and the split of an fp32 value into a 16-bit head and remainder. Storage is the 16-bit
-// pattern either way, so loads, the DMA ring and the appends are shared.
+// to fp32, and the split of an fp32 value into a 16-bit head and remainder.
+// Storage is the 16-bit pattern either way, so loads, the DMA ring and the
+// appends are shared.
 template <typename E> struct Elem;
 template <> struct Elem<bf16_t> {
   typedef __bf16 v8 __attribute__((ext_vector_type(8)));
