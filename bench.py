@@ -765,7 +765,8 @@ def run_stream(args) -> None:
             times.append(e0.elapsed_time(e1) * 1e3 / reads)
         us = statistics.median(times)
         gbps = nbytes / (us * 1e-6) / 1e9
-        results.append({"mode": mode, "pattern": ops.STREAM_MODES[mode], "workgroups": n_wg, "us_per_256MiB": round(us, 2),
+        results.append({"mode": mode, "pattern": ops.STREAM_MODES[mode], "workgroups": n_wg,
+                        "us_per_256MiB": round(us, 2),
                         "GB_s": round(gbps, 1), "pct_of_8TB_s": round(100 * gbps / HBM_PEAK_GBPS, 1)})
         log(f"stream mode {mode} wg {n_wg}: {us:.2f} us, {gbps:.0f} GB/s")
         del graph

@@ -83,11 +83,13 @@ def test_append_paths_write_the_rows_and_match_oracle(kv):
     kb, vb = cache_buffer(k[:, :, :kv - Q], kv + 7), cache_buffer(v[:, :, :kv - Q], kv + 7)
     out = ops.verify_attention_append(q.to(dev()), kb, vb, k[:, :, kv - Q:].to(dev()), v[:, :, kv - Q:].to(dev()), kv)
     torch.cuda.synchronize()
-    assert torch.equal(kb[:, :, kv - Q:kv].cpu(), k[:, :, kv - Q:]) and torch.equal(vb[:, :, kv - Q:kv].cpu(), v[:, :, kv - Q:])
+    assert torch.equal(kb[:, :, kv - Q:kv].cpu(), k[:, :, kv - Q:])
+    assert torch.equal(vb[:, :, kv - Q:kv].cpu(), v[:, :, kv - Q:])
     assert torch.isnan(vb[:, :, kv:].float()).all()
     assert_close(out, ref.verify_attention(q, k, v), F16)
     kb, vb = cache_buffer(k[:, :, :kv - 1], kv + 7), cache_buffer(v[:, :, :kv - 1], kv + 7)
-    out = ops.gqa_decode_append(q[:, :, :1].to(dev()), kb, vb, k[:, :, kv - 1:].to(dev()), v[:, :, kv - 1:].to(dev()), kv)
+    out = ops.gqa_decode_append(q[:, :, :1].to(dev()), kb, vb, k[:, :, kv - 1:].to(dev()), v[:, :, kv - 1:].to(dev()),
+                                kv)
     sep = ops.gqa_decode(q[:, :, :1].to(dev()), kb[:, :, :kv], vb[:, :, :kv])
     torch.cuda.synchronize()
     assert torch.equal(out, sep)
@@ -189,7 +191,8 @@ def test_selection_and_compaction():
     torch.cuda.synchronize()
     rows = idx.cpu().long()
     for h in range(NKV):
-        assert torch.equal(sk[0, h, :K + T].cpu(), k[0, h, rows[h]]) and torch.equal(sv[0, h, :K + T].cpu(), v[0, h, rows[h]])
+        assert torch.equal(sk[0, h, :K + T].cpu(), k[0, h, rows[h]])
+        assert torch.equal(sv[0, h, :K + T].cpu(), v[0, h, rows[h]])
 
 
 def test_rope_append_matches_oracle():
