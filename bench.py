@@ -778,14 +778,23 @@ def run_stream(args) -> None:
 
 
 def _cpu_model() -> str:
-    """The host CPU's model name as lscpu reports it (else /proc/cpuinfo)."""
+    """The host CPU's model name as lscpu reports it, with its family / model /
+    stepping numbers and the BIOS model name where lscpu gives them (a
+    virtualised host may report only a generic name); else /proc/cpuinfo."""
     import subprocess
 
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = {}
         for line in out.splitlines():
-            if line.strip().startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, val = line.split(":", 1)
+                fields.setdefault(key.strip(), val.strip())
+        if fields.get("Model name"):
+            ids = ", ".join(f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if fields.get(k))
+            name = fields["Model name"] + (f" ({ids})" if ids else "")
+            bios = fields.get("BIOS Model name")
+            return name + (f"; BIOS: {bios}" if bios and bios != fields["Model name"] else "")
     except (OSError, subprocess.SubprocessError):
         pass
     try:
