@@ -1,8 +1,8 @@
 """Run-to-run determinism of the hot path on the GPU: the same inputs give
 bit-identical selection scores and indices, verify outputs, collector scores
-and acceptance results on every call. Every reduction is done in a fixed
-order (no atomics in the arithmetic), so these hold exactly, not within a
-tolerance."""
+and acceptance results on every call. Every floating-point reduction is done
+in a fixed order (the only atomics are the radix select's integer histogram
+counts), so these hold exactly, not within a tolerance."""
 import numpy as np
 import pytest
 import torch
