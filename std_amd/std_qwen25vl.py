@@ -42,6 +42,19 @@ SPARSE_ATTN_MODES = {"hip", "gqa_sdpa", "triton_gqa", "repeat_sdpa"}
 # a selection refresh rewrites the indices only).
 SPARSE_KV_MODES = {"compact", "indexed"}
 
+_TRACE_COLLECTOR = None
+
+
+def set_trace_collector(collector) -> None:
+    """Install (None removes) an object whose ``begin_prefill()`` /
+    ``end_prefill()`` bracket the prompt prefill of std_generate_qwen25vl and
+    whose ``begin_verification(round)`` / ``end_verification()`` bracket each
+    round's verify step (std_qwen25vl.py:30-38, 693-698, 799-805). The
+    brackets run on the host around the step; with ``use_graphs=True`` a
+    verify step is a graph replay, inside which no Python hook runs."""
+    global _TRACE_COLLECTOR
+    _TRACE_COLLECTOR = collector
+
 
 @dataclass
 class SparseSelection:
@@ -568,8 +581,13 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     cache_init_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
 
     stage = _profile_mark(profile_prefill)
+    trace = _TRACE_COLLECTOR
+    if trace is not None:
+        trace.begin_prefill()
     prompt_ids, dense_next, text_start = prefill_prompt(model, inputs, dense_pkv, video_token_id,
                                                         capture_text_queries=True)
+    if trace is not None:
+        trace.end_prefill()
     selection_prefill_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
 
     stage = _profile_mark(profile_prefill)
@@ -701,6 +719,9 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         pending_lengths.append(len(dense_pending))
 
         stage = _profile_mark(profile_decode)
+        trace = _TRACE_COLLECTOR
+        if trace is not None:
+            trace.begin_verification(decode_rounds)
         if replay:
             graphs[0][1][0].replay()
             res = graphs[2]
@@ -717,6 +738,8 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
             last_logits[0] = logits[0]
             res = ops.greedy_accept(logits[0], draft_dev.to(torch.int32), has_pending=bool(dense_pending),
                                     dense_next=None if dense_pending else dense_next_i32)
+        if trace is not None:
+            trace.end_verification()
         host = torch.cat([res[:2], draft_dev.to(torch.int32)]).tolist()     # the round's one readback
         accept_len, bonus_token, draft = host[0], host[1], host[2:]
         verify_time += _profile_mark(profile_decode) - stage
@@ -796,3 +819,31 @@ def first_divergence(a: torch.Tensor, b: torch.Tensor) -> Optional[int]:
         if x != y:
             return i
     return None if len(a) == len(b) else min(len(a), len(b))
+
+
+def generated_suffix(output_ids: torch.Tensor, prompt_len: int) -> torch.Tensor:
+    """The generated tokens of ``output_ids`` [1, prompt + generated]
+    (std_qwen25vl.py:981-982)."""
+    return output_ids[:, prompt_len:]
+
+
+def tokens_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Same shape and the same tokens (std_qwen25vl.py:985-986)."""
+    return a.shape == b.shape and bool(torch.equal(a.detach().cpu(), b.detach().cpu()))
+
+
+def copy_prompt_cache(source_past_key_values, target_past_key_values, target_length_data: torch.Tensor,
+                      prompt_len: int) -> None:
+    """Copy the first ``prompt_len`` rows of every layer's K and V from one
+    cache set into another and set the target lengths to ``prompt_len``
+    (std_qwen25vl.py:301-320). The generate loop does not need it (compaction
+    gathers the selected rows straight from the dense cache); it is kept for
+    callers that build a second cache from a prefilled one."""
+    for source_layer, target_layer in zip(source_past_key_values, target_past_key_values):
+        for src, dst in zip(source_layer, target_layer):
+            if src.length < prompt_len:
+                raise RuntimeError(f"Cannot copy prompt cache: source length {src.length} is shorter than "
+                                   f"prompt length {prompt_len}.")
+            dst.data.narrow(2, 0, prompt_len).copy_(src.data.narrow(2, 0, prompt_len))
+            dst.current_length.fill_(prompt_len)
+    target_length_data.fill_(prompt_len)

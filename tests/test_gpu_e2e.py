@@ -185,3 +185,43 @@ def test_indexed_sparse_kv_tokens_equal_compact(use_graphs):
     idx, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, sparse_kv="indexed", **kw)
     assert torch.equal(idx.output_ids, comp.output_ids)
     assert idx.accept_lengths == comp.accept_lengths and idx.generate_len == 32
+
+
+@pytest.mark.parametrize("use_graphs", [False, True])
+def test_trace_collector_brackets_prefill_and_each_verify(tiny32, use_graphs):
+    """set_trace_collector: one prefill bracket, then one verify bracket per
+    round carrying the round number, opened and closed in order; removing
+    the collector stops the calls (std_qwen25vl.py:30-38, 693-698, 799-805)."""
+    from std_amd.std_qwen25vl import set_trace_collector
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 5)
+    events = []
+
+    class Recorder:
+        def begin_prefill(self):
+            events.append("bp")
+
+        def end_prefill(self):
+            events.append("ep")
+
+        def begin_verification(self, round_idx):
+            events.append(("bv", round_idx))
+
+        def end_verification(self):
+            events.append("ev")
+
+    announce(f"e2e trace collector brackets, graphs={use_graphs}")
+    set_trace_collector(Recorder())
+    try:
+        std, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=20, gamma=4,
+                                       target_k_plus_text=TARGET, ignore_eos=True, use_graphs=use_graphs)
+    finally:
+        set_trace_collector(None)
+    want = ["bp", "ep"]
+    for r in range(1, std.decode_rounds + 1):
+        want += [("bv", r), "ev"]
+    assert events == want
+    events.clear()
+    std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=4, gamma=2,
+                          target_k_plus_text=TARGET, ignore_eos=True, use_graphs=use_graphs)
+    assert events == []

@@ -152,3 +152,26 @@ def test_same_layout_ignores_size_one_strides():
     vv = torch.randn(1, 3, 4, 128).transpose(1, 2)
     assert not same_layout(kk, vv)
     assert not same_layout(k, kk)
+
+
+def test_generated_suffix_and_tokens_equal():
+    from std_amd.std_qwen25vl import generated_suffix, tokens_equal
+    ids = torch.tensor([[5, 6, 7, 8, 9]])
+    assert generated_suffix(ids, 3).tolist() == [[8, 9]]
+    assert tokens_equal(ids, ids.clone()) and not tokens_equal(ids, ids[:, :4])
+    assert not tokens_equal(ids, torch.tensor([[5, 6, 7, 8, 0]]))
+
+
+def test_copy_prompt_cache_copies_the_prefix_and_sets_lengths():
+    from std_amd.std_qwen25vl import copy_prompt_cache
+    cfg = DecoderConfig.tiny(layers=2)
+    src, src_data, src_len = kv_cache.initialize_past_key_values(cfg, torch.device("cpu"), torch.float32, 16)
+    dst, dst_data, dst_len = kv_cache.initialize_past_key_values(cfg, torch.device("cpu"), torch.float32, 12)
+    src_data.copy_(torch.randn(src_data.shape, generator=torch.Generator().manual_seed(3)))
+    src_len.fill_(10)
+    copy_prompt_cache(src, dst, dst_len, 7)
+    assert torch.equal(dst_data[:, :, :, :7], src_data[:, :, :, :7])
+    assert not dst_data[:, :, :, 7:].any()
+    assert dst_len.tolist() == [7] * len(dst_len) and all(c.length == 7 for layer in dst for c in layer)
+    with pytest.raises(RuntimeError):
+        copy_prompt_cache(src, dst, dst_len, 11)             # longer than the source's 10 rows
