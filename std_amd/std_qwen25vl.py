@@ -13,8 +13,9 @@ bonus-token append. What changes underneath:
   lazily built host mirror);
 * compaction gathers straight from the dense cache into the sparse cache
   (no full-prompt copy);
-* ``sparse_attn_mode="hip"``: every attention call of the decode loop is a
-  libstdhip.so launch with the KV append fused in;
+* every attention call of the decode loop is a libstdhip.so launch with the
+  KV append fused in, whichever ``sparse_attn_mode`` is named (the
+  reference's default ``"gqa_sdpa"``, its other modes, or ``"hip"``);
 * acceptance and rollback are computed on the device, and draft tokens stay
   on the device, so a round reads back a handful of int32 values once.
 
@@ -281,7 +282,7 @@ class SparseDraftController:
     lists set (index-addressed sparse KV) the first compact_len keys of each
     layer are read from the dense cache through them."""
 
-    def __init__(self, model, selection: SparseSelection, sparse_attn_mode: str = "hip",
+    def __init__(self, model, selection: SparseSelection, sparse_attn_mode: str = "gqa_sdpa",
                  use_compile: bool = False):
         if sparse_attn_mode not in SPARSE_ATTN_MODES:
             raise ValueError(f"Unsupported sparse_attn_mode={sparse_attn_mode!r}.")
@@ -527,10 +528,10 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
                           max_new_tokens: int = 256, gamma: int = 9, target_k_plus_text: int = 1024,
                           explicit_k: Optional[int] = None, verify_mode: str = "parallel",
                           verify_fallback: str = "none", sequential_fallback_max_accept: int = 1,
-                          profile_decode: bool = False, sparse_attn_mode: str = "hip",
+                          profile_decode: bool = False, sparse_attn_mode: str = "gqa_sdpa",
                           adaptive_gamma_min: Optional[int] = None, adaptive_gamma_mode: str = "accept_len",
                           copy_sparse_prefill: bool = True, profile_prefill: bool = False,
-                          verify_attn_backend: str = "math", verify_margin_threshold: Optional[float] = None,
+                          verify_attn_backend: str = "default", verify_margin_threshold: Optional[float] = None,
                           use_compile: bool = False, ignore_eos: bool = False, use_graphs: bool = False,
                           sparse_kv: str = "compact", round_hook=None) -> Tuple[GenerateResult, SparseSelection]:
     """Sparse-to-Dense greedy decoding (std_qwen25vl.py:609-978).
