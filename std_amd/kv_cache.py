@@ -74,13 +74,23 @@ def default_max_cache_len(max_position_embeddings: int) -> int:
 
 
 def initialize_past_key_values(
-    config, device: torch.device, dtype: torch.dtype, max_cache_len: int = None
+    config, device: torch.device = None, dtype: torch.dtype = None, max_cache_len: int = None
 ) -> Tuple[List[List[KVCache]], torch.Tensor, torch.Tensor]:
     """Allocate one cache (kv_cache.py:72-165) on a single device.
 
-    Returns ``(past_key_values, data [2L, 1, Hkv, max_len, D], current_length_data [2L])``;
+    ``config`` is a model config, or the model itself as the reference passes
+    it (``initialize_past_key_values(model)``): then the config, device and
+    dtype come from the model. Returns
+    ``(past_key_values, data [2L, 1, Hkv, max_len, D], current_length_data [2L])``;
     ``past_key_values[l] = [K cache, V cache]``. Rows are zero-initialised as
     in the reference."""
+    if hasattr(config, "config"):                     # the reference's form: a model
+        model = config
+        config = model.config
+        device = model.device if device is None else device
+        dtype = model.dtype if dtype is None else dtype
+    if device is None or dtype is None:
+        raise ValueError("initialize_past_key_values needs a model, or a config with a device and a dtype")
     if max_cache_len is None:
         max_cache_len = default_max_cache_len(config.max_position_embeddings)
     n_layers = config.num_hidden_layers

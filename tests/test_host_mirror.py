@@ -175,3 +175,15 @@ def test_copy_prompt_cache_copies_the_prefix_and_sets_lengths():
     assert dst_len.tolist() == [7] * len(dst_len) and all(c.length == 7 for layer in dst for c in layer)
     with pytest.raises(RuntimeError):
         copy_prompt_cache(src, dst, dst_len, 11)             # longer than the source's 10 rows
+
+
+def test_initialize_past_key_values_takes_the_model_as_the_reference_does(monkeypatch):
+    cfg = DecoderConfig.tiny(layers=2)
+    model = types.SimpleNamespace(config=cfg, device=torch.device("cpu"), dtype=torch.bfloat16)
+    monkeypatch.setenv("SPECVLM_MAX_CACHE_LEN", "96")
+    pkv, data, lengths = kv_cache.initialize_past_key_values(model)
+    assert data.dtype == torch.bfloat16 and data.device.type == "cpu"
+    assert tuple(data.shape) == (4, 1, cfg.num_key_value_heads, 96, cfg.hidden_size // cfg.num_attention_heads)
+    assert len(pkv) == 2 and pkv[1][1].capacity == 96 and lengths.tolist() == [0, 0, 0, 0]
+    with pytest.raises(ValueError):
+        kv_cache.initialize_past_key_values(cfg)          # a bare config needs a device and a dtype
