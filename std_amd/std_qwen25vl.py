@@ -57,21 +57,34 @@ def set_trace_collector(collector) -> None:
     _TRACE_COLLECTOR = collector
 
 
-@dataclass
 class SparseSelection:
     """Per-layer sparse visual KV choices (std_qwen25vl.py:41-50).
 
-    ``topk_device``: int32 [L, Hkv, k] on the device, each row ascending.
-    ``topk_positions`` gives the reference's per-layer CPU int64 [Hkv, k]
-    tensors, built on first access."""
+    Built as the reference builds it, ``SparseSelection(topk_positions,
+    non_visual_positions, prompt_len, visual_len, text_len, k)`` with the
+    per-layer ascending [Hkv, k] position tensors (a list, or one [L, Hkv, k]
+    tensor), or with ``topk_device=`` an int32 [L, Hkv, k] device tensor in
+    place of ``topk_positions`` (what the selection kernels produce; the
+    per-layer CPU tensors are then built on first access of
+    ``topk_positions``). Compaction moves the indices to the cache's device."""
 
-    topk_device: torch.Tensor
-    non_visual_positions: torch.Tensor      # CPU int64 [N_nv], ascending
-    prompt_len: int
-    visual_len: int
-    text_len: int
-    k: int
-    _host: Optional[List[torch.Tensor]] = field(default=None, repr=False)
+    def __init__(self, topk_positions=None, non_visual_positions=None, prompt_len: int = 0, visual_len: int = 0,
+                 text_len: int = 0, k: int = 0, *, topk_device: Optional[torch.Tensor] = None):
+        if (topk_positions is None) == (topk_device is None):
+            raise ValueError("SparseSelection needs exactly one of topk_positions and topk_device")
+        self._host: Optional[List[torch.Tensor]] = None
+        if topk_device is None:
+            if isinstance(topk_positions, torch.Tensor):
+                topk_positions = list(topk_positions.unbind(0))
+            layers = [torch.as_tensor(t) for t in topk_positions]
+            topk_device = torch.stack(layers).to(torch.int32)
+            self._host = [t.to("cpu", torch.int64) for t in layers]
+        self.topk_device = topk_device
+        self.non_visual_positions = torch.as_tensor(non_visual_positions).to("cpu", torch.int64)
+        self.prompt_len = int(prompt_len)
+        self.visual_len = int(visual_len)
+        self.text_len = int(text_len)
+        self.k = int(k)
 
     @property
     def topk_positions(self) -> List[torch.Tensor]:
@@ -83,6 +96,10 @@ class SparseSelection:
     @property
     def compact_len(self) -> int:
         return int(self.non_visual_positions.numel()) + self.k
+
+    def __repr__(self) -> str:
+        return (f"SparseSelection(layers={self.topk_device.shape[0]}, heads={self.topk_device.shape[1]}, k={self.k}, "
+                f"prompt_len={self.prompt_len}, visual_len={self.visual_len}, text_len={self.text_len})")
 
 
 @dataclass
@@ -249,7 +266,7 @@ def compact_sparse_prompt_cache(past_key_values, current_length_data: torch.Tens
     dev = past_key_values[0][0].data.device
     non_visual = selection.non_visual_positions.to(dev, torch.int32)
     for layer_idx, (sparse_layer, dense_layer) in enumerate(zip(past_key_values, dense_past_key_values)):
-        index = ops.build_compact_index(non_visual, selection.topk_device[layer_idx])
+        index = ops.build_compact_index(non_visual, selection.topk_device[layer_idx].to(dev))
         if index.shape[1] != compact_len:
             raise RuntimeError("Compacted sparse KV produced an unexpected length.")
         ops.compact_kv(dense_layer[0].data, dense_layer[1].data, sparse_layer[0].data, sparse_layer[1].data, index)
@@ -268,7 +285,7 @@ def index_sparse_prompt_cache(past_key_values, current_length_data: torch.Tensor
     non_visual = selection.non_visual_positions.to(dev, torch.int32)
     gathers = []
     for layer_idx, dense_layer in enumerate(dense_past_key_values):
-        index = ops.build_compact_index(non_visual, selection.topk_device[layer_idx])
+        index = ops.build_compact_index(non_visual, selection.topk_device[layer_idx].to(dev))
         if index.shape[1] != compact_len:
             raise RuntimeError("Sparse key list has an unexpected length.")
         gathers.append((dense_layer[0].data, dense_layer[1].data, ops.pad_index(index)))

@@ -8,7 +8,7 @@ import torch
 from oracle import selection as ref_sel
 from std_amd.decoder import DecoderConfig, RandomDecoder
 from std_amd.kv_cache import initialize_past_key_values
-from std_amd.std_qwen25vl import (ar_generate_qwen25vl, build_sparse_selection_from_queries,
+from std_amd.std_qwen25vl import (SparseSelection, ar_generate_qwen25vl, build_sparse_selection_from_queries,
                                   compact_sparse_prompt_cache, first_divergence, prefill_prompt,
                                   std_generate_qwen25vl)
 from tests.gpu_helpers import announce, dev
@@ -61,6 +61,30 @@ def test_selection_and_compaction_from_prefill(tiny32):
         for kind in range(2):
             got = sparse[layer][kind].data[0, 0, :n].cpu()
             assert torch.equal(got, pkv[layer][kind].data[0, 0, torch.as_tensor(idx)].cpu())
+
+
+def test_compaction_from_a_reference_built_selection(tiny32):
+    """A SparseSelection built as the reference builds it (per-layer CPU
+    position tensors) compacts exactly as the selection kernels' own."""
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 12)
+    P = inputs["input_ids"].shape[1]
+    announce(f"e2e compaction from a reference-built selection P={P}")
+    pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.float32, P + 8)
+    prompt_ids, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
+    sel = build_sparse_selection_from_queries(list(model.captured_queries), [layer[0].data for layer in pkv],
+                                              prompt_ids, cfg.video_token_id, text_start, target_k_plus_text=TARGET,
+                                              num_key_value_heads=1)
+    ref_built = SparseSelection([t.clone() for t in sel.topk_positions], sel.non_visual_positions, sel.prompt_len,
+                                sel.visual_len, sel.text_len, sel.k)
+    caches = []
+    for s in (sel, ref_built):
+        sparse, data, lengths = initialize_past_key_values(cfg, dev(), torch.float32, sel.compact_len + 4)
+        n = compact_sparse_prompt_cache(sparse, lengths, s, pkv)
+        caches.append((n, data))
+    torch.cuda.synchronize()
+    assert caches[0][0] == caches[1][0] == sel.compact_len
+    assert torch.equal(caches[0][1], caches[1][1])
 
 
 def test_std_tokens_equal_dense_ar_fp32(tiny32):

@@ -187,3 +187,17 @@ def test_initialize_past_key_values_takes_the_model_as_the_reference_does(monkey
     assert len(pkv) == 2 and pkv[1][1].capacity == 96 and lengths.tolist() == [0, 0, 0, 0]
     with pytest.raises(ValueError):
         kv_cache.initialize_past_key_values(cfg)          # a bare config needs a device and a dtype
+
+
+def test_sparse_selection_is_built_as_the_reference_builds_it():
+    layers = [torch.tensor([[1, 4, 6]]), torch.tensor([[0, 2, 5]])]          # per-layer [Hkv, k], CPU int64
+    sel = SparseSelection(layers, torch.tensor([7, 8]), 9, 7, 2, 3)            # positional, as the reference's test
+    assert sel.topk_device.dtype == torch.int32 and tuple(sel.topk_device.shape) == (2, 1, 3)
+    assert all(torch.equal(a, b) for a, b in zip(sel.topk_positions, layers)) and sel.compact_len == 5
+    kw = SparseSelection(topk_positions=layers, non_visual_positions=[7, 8], prompt_len=9, visual_len=7, text_len=2,
+                         k=3)
+    assert torch.equal(kw.topk_device, sel.topk_device) and kw.non_visual_positions.dtype == torch.int64
+    with pytest.raises(ValueError):
+        SparseSelection(layers, torch.tensor([7, 8]), 9, 7, 2, 3, topk_device=sel.topk_device)
+    with pytest.raises(ValueError):
+        SparseSelection(None, torch.tensor([7, 8]), 9, 7, 2, 3)
