@@ -251,9 +251,22 @@ def _attention(fn: str, query, key, value, scale, out, new_key=None, new_value=N
     return out
 
 
+class ShapeAssertionError(ValueError, AssertionError):
+    """A shape the reference rejects with an ``assert`` (q_len != 1, or query
+    heads not a multiple of KV heads: triton_attention.py:89, 94). Catchable
+    as AssertionError, as there, and as ValueError, as every shape error of
+    this module."""
+
+
 def fused_gqa_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
     """Drop-in for std_repro.triton_attention.fused_gqa_attention (same
-    signature and output allocation: a new tensor in query dtype)."""
+    signature, output allocation -- a new tensor in query dtype -- and shape
+    assertions)."""
+    if query.dim() != 4 or query.shape[2] != 1:
+        raise ShapeAssertionError(f"Expected q_len=1, got {tuple(query.shape)}")
+    if key.dim() != 4 or key.shape[1] == 0 or query.shape[1] % key.shape[1] != 0:
+        raise ShapeAssertionError(f"query heads {query.shape[1]} are not a multiple of KV heads in "
+                                  f"{tuple(key.shape)}")
     return gqa_decode(query, key, value)
 
 

@@ -256,6 +256,13 @@ def test_python_shim_shape_errors():
     # reference's q_len assertion (triton_attention.py:89)
     with pytest.raises(ValueError, match="q_len=1"):
         ops.gqa_decode(torch.zeros(1, 28, 2, 128), torch.zeros(1, 4, 8, 128), torch.zeros(1, 4, 8, 128))
+    # the reference's drop-in asserts its shapes (triton_attention.py:89, 94): the error is both kinds
+    kv = torch.zeros(1, 4, 8, 128)
+    for q, k in ((torch.zeros(1, 28, 2, 128), kv), (torch.zeros(1, 30, 1, 128), kv)):
+        with pytest.raises(AssertionError):
+            ops.fused_gqa_attention(q, k, kv)
+        with pytest.raises(ValueError):
+            ops.fused_gqa_attention(q, k, kv)
 
 
 def test_status_error_is_runtime_error():
