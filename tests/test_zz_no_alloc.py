@@ -30,7 +30,7 @@ def _workspace_decode(q, k, v):
     """The existing entry point, with a caller workspace, through the C ABI."""
     lib = _lib.load_library()
     n_q, n_kv, kv_len = q.shape[1], k.shape[1], k.shape[2]
-    code = _lib.STD_BF16 if q.dtype == torch.bfloat16 else _lib.STD_F32
+    code = {torch.bfloat16: _lib.STD_BF16, torch.float16: _lib.STD_F16}.get(q.dtype, _lib.STD_F32)
     out = torch.empty_like(q)
     ws_bytes = lib.std_gqa_decode_workspace_bytes(n_q, n_kv, kv_len, D)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev())
@@ -42,7 +42,7 @@ def _workspace_decode(q, k, v):
 
 def _noalloc_decode(q, k, v):
     n_q, n_kv, kv_len = q.shape[1], k.shape[1], k.shape[2]
-    code = _lib.STD_BF16 if q.dtype == torch.bfloat16 else _lib.STD_F32
+    code = {torch.bfloat16: _lib.STD_BF16, torch.float16: _lib.STD_F16}.get(q.dtype, _lib.STD_F32)
     out = torch.full_like(q, float("nan"))
     st = torch.cuda.current_stream().cuda_stream
     _lib.call("std_gqa_decode_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), n_q, n_kv, kv_len,
@@ -50,7 +50,7 @@ def _noalloc_decode(q, k, v):
     return out
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_noalloc_decode_equals_workspace_decode(dtype):
     # first call: the dense 128k AR decode (64 splits per KV head, the largest
     # partial set of the decode path); second: the 1034-key sparse draft, which
