@@ -210,7 +210,9 @@ int std_select_topk(const void* q_text, const void* k,
  * columns visual_pos[n_visual] per KV head -> topk_out int32
  * [n_kv][k_select], ascending; ties go to the lowest position. The sums are
  * fp64 (exact for fp16 probabilities); scores_out (optional, fp64
- * [n_kv][prompt_len]) receives them. Rows and the base 4-element aligned. */
+ * [n_kv][prompt_len]) receives them. Any prompt length and strides (the
+ * reference's contiguous tensor has row stride P); rows aligned to four
+ * elements are read four columns at a time, others element by element. */
 size_t std_select_topk_probs_workspace_bytes(int n_q, int n_kv, int text_len, int prompt_len, int n_visual);
 
 int std_select_topk_probs(const void* probs, long long head_stride, long long row_stride, int dtype,
@@ -450,17 +452,20 @@ int std_greedy_accept(const void* logits, long long logits_row_stride, int q_row
  *   504-519), called from the verify forward at
  *   src/specvlm/models/modeling_qwen2_5_vl.py:1063-1067, together with the
  *   verify attention it rides (std_verify_attn / std_verify_attn_append).
- * out: exactly std_verify_attn's (bit for bit); with new_k / new_v (both or
+ * out: the verify attention of std_verify_attn; with new_k / new_v (both or
  * neither) the q_len new rows are appended first, as std_verify_attn_append.
  * scores[g][j - vis_begin] (fp32, head stride scores_head_stride) =
  *   sum_i softmax_j( qbar[g][i] . k[g][j] * scale ) over the visual keys
  *   j in [vis_begin, vis_end), where qbar[g][i] is the fp32 mean of the query
  *   rows of KV head g's query heads at position i (the hook's
- *   q.float().reshape(...).mean(dim=2)); i < q_len. The visual keys form one
- *   contiguous range of prompt keys (vis_end <= kv_len - q_len), as the video
- *   tokens of a prompt do. bf16 or fp16; (n_q / n_kv + 1) * q_len <= 80 (the
- *   collector's q_len rows use the padding rows of the verify's last row
- *   tile: gamma + 1 <= 10 at seven query heads per KV head).
+ *   q.float().reshape(...).mean(dim=2)); i < q_len. Visual keys must be prompt
+ *   keys (vis_end <= kv_len - q_len). bf16 or fp16.
+ * The collector rows ride the padding rows of the verify's last row tile, so
+ * one launch serves (n_q / n_kv + 1) * q <= 80, q <= 16 positions (gamma + 1
+ * <= 10 at seven query heads per KV head); out is then std_verify_attn's bit
+ * for bit. Longer verifies run in chunks of positions (each chunk reads the
+ * cache once more; out within the verify's tolerance, scores summed in the
+ * same row order).
  * ------------------------------------------------------------------------ */
 size_t std_verify_attn_collect_workspace_bytes(int n_q, int n_kv, int q_len, int kv_len, int d,
                                                int vis_begin, int vis_end);
@@ -473,6 +478,30 @@ int std_verify_attn_collect(const void* q, void* k_cache, void* v_cache,
                             float scale, int dtype, int vis_begin, int vis_end,
                             float* scores, long long scores_head_stride,
                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* The general form (same workspace query, with the visual set's first
+ * position and last position + 1 as vis_begin / vis_end):
+ *  - any ascending set of visual positions, as the hook gathers
+ *    key_states[:, :, visual_positions] (dynamic_selection.py:515):
+ *    vis_mask (uint32, at least (vis_end + 31) / 32 words) has bit j % 32 of
+ *    word j / 32 set for each visual key j, vis_rank[w] = the number of
+ *    visual keys below 32 w, n_visual the set's size; scores[g][r] is the
+ *    r-th visual key's. vis_mask == vis_rank == NULL: the whole range
+ *    [vis_begin, vis_end) (n_visual = vis_end - vis_begin);
+ *  - len_dev != NULL (device int32): the cache holds *len_dev rows plus this
+ *    step's q_len rows, read on the device (graph-replayed verify steps);
+ *    kv_len is then the largest such total the launch serves, and *len_dev
+ *    must cover the visual keys (keys at or past it are not scored).
+ * --------------------------------------------------------------------- */
+int std_verify_attn_collect_ex(const void* q, void* k_cache, void* v_cache,
+                               const void* new_k, const void* new_v, void* out,
+                               int n_q, int n_kv, int q_len, int kv_len, const int32_t* len_dev, int d,
+                               long long k_head_stride, long long v_head_stride,
+                               long long new_head_stride, long long new_row_stride,
+                               float scale, int dtype, int vis_begin, int vis_end,
+                               const uint32_t* vis_mask, const int32_t* vis_rank, int n_visual,
+                               float* scores, long long scores_head_stride,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Streaming-read ceiling (measurement helper; no counterpart in the

@@ -53,6 +53,10 @@ SIGNATURES = {
     "std_verify_attn_collect": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                         c_int, c_int, c_int, c_longlong, c_longlong, c_longlong, c_longlong, c_float,
                                         c_int, c_int, c_int, c_void_p, c_longlong, c_void_p, c_size_t, c_void_p]),
+    "std_verify_attn_collect_ex": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                           c_int, c_int, c_void_p, c_int, c_longlong, c_longlong, c_longlong,
+                                           c_longlong, c_float, c_int, c_int, c_int, c_void_p, c_void_p, c_int,
+                                           c_void_p, c_longlong, c_void_p, c_size_t, c_void_p]),
     "std_select_topk_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "std_select_topk": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_longlong, c_int,
                                 c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

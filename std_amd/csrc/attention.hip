@@ -117,16 +117,23 @@ struct GatherArgs {
 
 // Visual-attention collector riding the verify pass (COLL): the group-mean
 // query of each verify position, a softmax over the visual keys only, summed
-// over the positions. logits: [n_kv][n_vtiles][q_len][64] log2-domain scaled
-// logits of the 64-key tiles that hold visual keys (tile vt = key / 64 -
-// vis_begin / 64; -inf at non-visual keys), so that a split writes one
-// contiguous block per tile; stats: [n_kv][n_split][q_len] per-split (max, sum
-// of exp2(logit - max)).
+// over the positions. The visual keys lie in [vis_begin, vis_end); with vmask
+// == nullptr they are that whole range, otherwise key j is visual iff bit
+// j % 32 of vmask[j / 32] is set (any ascending position set; vis_begin and
+// vis_end are then its first position and last + 1). logits:
+// [n_kv][n_vtiles][q_len][64] log2-domain scaled logits of the 64-key tiles
+// that hold visual keys (tile vt = key / 64 - vis_begin / 64; -inf at
+// non-visual keys), so that a split writes one contiguous block per tile;
+// stats: [n_kv][n_split][q_len] per-split (max, sum of exp2(logit - max)).
+// len_off: a device-length launch reads *len_dev + len_off cached keys (the
+// positions before a chunk of verify rows, see verify_collect_entry).
 struct CollArgs {
   float* logits;
   float2* stats;
   int n_vtiles;
   int vis_begin, vis_end;
+  const uint32_t* vmask;
+  int len_off;
 };
 
 template <bool COLL>
@@ -136,8 +143,9 @@ struct WsLayout {
   size_t o_off, ml_off, total;
 };
 
-// part_bytes: 2 for scaled fp16 partials, 4 for fp32 (part_bytes_of).
-int part_bytes_of(int dtype, int rows) { return dtype != STD_F32 && rows > 16 ? 2 : 4; }
+// part_bytes: 2 for scaled fp16 partials (bf16 launches with several row
+// tiles), 4 for fp32 (part_bytes_of).
+int part_bytes_of(int dtype, int rows) { return dtype == STD_BF16 && rows > 16 ? 2 : 4; }
 
 WsLayout ws_layout(int n_kv, int rows, const SplitPlan& p, int part_bytes) {
   WsLayout l{0, 0, 0};
@@ -164,8 +172,8 @@ __device__ __forceinline__ int tile_key0(int split, int tt, int n_split) { retur
 // length outside [0, kv_len - q_len] empties every split: nothing is read and
 // the outputs become 0/0 = NaN.
 __device__ __forceinline__ void device_length(const int32_t* len_dev, int q_len, int& kv_len, int& ntiles_total,
-                                              int& causal_off) {
-  const int len = *len_dev;
+                                              int& causal_off, int len_off = 0) {
+  const int len = *len_dev + len_off;
   kv_len = (len >= 0 && len <= kv_len - q_len) ? len + q_len : 0;
   ntiles_total = (kv_len + TK - 1) / TK;
   causal_off = kv_len - q_len;
@@ -229,7 +237,9 @@ __device__ void finish_split(OLoad load_o, const float2* ml_f, T* __restrict__ o
 // arithmetic is the same as for fp32 partials, at half the bytes written and
 // read back (128k verify: 9.3 -> 4.7 MB, 0.5 us less per layer). The decodes
 // keep fp32 partials: their few partial bytes save nothing, and the row-max
-// reduction lengthened the latency-bound launches (draft +0.35 us).
+// reduction lengthened the latency-bound launches (draft +0.35 us). fp16
+// caches keep fp32 partials as well: their outputs have an fp16 partial's own
+// precision, so its rounding would add up to half an output ulp.
 typedef _Float16 half_t;
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 
@@ -347,6 +357,25 @@ attn_merge_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
   merge_row<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y);
 }
 
+// Where the collector's per-key sums go: the visual keys' scores in position
+// order (dynamic_selection.py:515 gathers key_states at visual_positions).
+// vmask == nullptr: keys [vis_begin, vis_end), key j -> j - vis_begin;
+// otherwise key j (bit j % 32 of vmask[j / 32] set) -> vrank[j / 32] + the
+// set bits below it in its word; n_visual bounds every write. Keys at or past
+// key_lim (the cached keys of a device-length launch) are never scored.
+// accumulate: add to the scores instead of overwriting them (verify rows
+// collected chunk by chunk, in row order).
+struct CollOut {
+  float* scores;
+  long long score_hs;
+  const uint32_t* vmask;
+  const int32_t* vrank;
+  int n_visual;
+  const int32_t* len_dev;
+  int len_off;
+  int accumulate;
+};
+
 // Collector finish (the column sums of VerificationCollectorV3._hook,
 // dynamic_selection.py:504-519), one 256-thread block per 16 visual tiles
 // (1024 keys) of a KV head: thread t's four keys are columns 4 (t % 16) .. +3
@@ -356,8 +385,8 @@ attn_merge_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
 // fixed butterfly, then the thread sums exp2(logit - lse) over the rows in
 // row order.
 __device__ __forceinline__ void coll_finish(const float* __restrict__ logits, const float2* __restrict__ stats,
-                                            float* __restrict__ scores, long long score_hs, int q_len, int n_split,
-                                            int n_vtiles, int vis_begin, int vis_end, int cb, int g) {
+                                            const CollOut co, int q_len, int n_split, int n_vtiles, int vis_begin,
+                                            int vis_end, int cb, int g) {
   __shared__ float lse[16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int vt = min(16 * cb + tid / 16, n_vtiles - 1), c = 4 * (tid % 16);
@@ -396,38 +425,60 @@ __device__ __forceinline__ void coll_finish(const float* __restrict__ logits, co
     if (lane == 0 && i < q_len) lse[i] = m + __log2f(l);
   }
   __syncthreads();
+  // The four keys' score slots (-1: not scored). They share one mask word.
+  const bool live = 16 * cb + tid / 16 < n_vtiles;
+  float* dst = co.scores + (long long)g * co.score_hs;
+  const int key0 = (vis_begin / TK + vt) * TK + c;
+  const int key_lim = co.len_dev != nullptr ? min(vis_end, *co.len_dev + co.len_off) : vis_end;
+  uint32_t word = 0;
+  int rank0 = 0;
+  if (live && co.vmask != nullptr && key0 < vis_end) {
+    word = co.vmask[key0 >> 5];
+    rank0 = co.vrank[key0 >> 5];
+  }
+  int slot[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int key = key0 + e;
+    int sl = key - vis_begin;
+    if (co.vmask != nullptr) {
+      const int bit = key & 31;
+      sl = ((word >> bit) & 1u) ? rank0 + __popc(word & ((1u << bit) - 1u)) : -1;
+    }
+    slot[e] = (live && key >= vis_begin && key < key_lim && sl >= 0 && sl < co.n_visual) ? sl : -1;
+  }
+  // Sum over the rows in row order, continuing from the earlier chunks' sum
+  // when accumulating (so chunked rows fold exactly as one pass would).
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (co.accumulate) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (slot[e] >= 0) acc[e] = dst[slot[e]];
+  }
 #pragma unroll
   for (int i = 0; i < 16; ++i)
     if (i < q_len) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[e] += fast_exp2(z[i][e] - lse[i]);
     }
-  if (16 * cb + tid / 16 >= n_vtiles) return;
-  float* dst = scores + (long long)g * score_hs;
-  const int key0 = (vis_begin / TK + vt) * TK + c;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int key = key0 + e;
-    if (key >= vis_begin && key < vis_end) dst[key - vis_begin] = acc[e];
-  }
+  for (int e = 0; e < 4; ++e)
+    if (slot[e] >= 0) dst[slot[e]] = acc[e];
 }
 
 // The verify merge and the collector finish in one launch: grid
 // (n_rows + n_col_blocks, n_kv); blocks x < n_rows merge attention row x (none
 // when the verify ran as one split), the others finish 1024 visual keys each.
-template <typename T>
+template <typename T, typename PT>
 __global__ void __launch_bounds__(kMergeThreads)
-merge_coll_kernel(const half_t* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
+merge_coll_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
                   int n_split, int q_len, int group, int n_rows, const float* __restrict__ logits,
-                  const float2* __restrict__ stats, float* __restrict__ scores, int n_vtiles, long long score_hs,
-                  int vis_begin, int vis_end) {
+                  const float2* __restrict__ stats, CollOut co, int n_vtiles, int vis_begin, int vis_end) {
   static_assert(kMergeThreads == 256, "the collector finish runs 256 threads");
   if ((int)blockIdx.x < n_rows)
-    merge_row<T, half_t>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
+    merge_row<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
   else
-    coll_finish(logits, stats, scores, score_hs, q_len, n_split, n_vtiles, vis_begin, vis_end, blockIdx.x - n_rows,
-                blockIdx.y);
+    coll_finish(logits, stats, co, q_len, n_split, n_vtiles, vis_begin, vis_end, blockIdx.x - n_rows, blockIdx.y);
 }
 
 // ===========================================================================
@@ -545,13 +596,17 @@ struct Bf16Cfg {
   static constexpr int kLoadsPerTile = 2 * kSegsPerWave;
 };
 
-template <int NT>
-using PartT = typename std::conditional<(NT > 1), half_t, float>::type;
+// Split partials: scaled fp16 for the bf16 launches with several row tiles
+// (verify), whose 8-bit outputs are far coarser than an fp16 partial; fp32
+// otherwise -- the decodes, and fp16 caches, whose outputs carry as many
+// significand bits as an fp16 partial would.
+template <int NT, typename E>
+using PartT = typename std::conditional<(NT > 1) && std::is_same<E, bf16_t>::value, half_t, float>::type;
 
 template <int NT, bool KS, bool GA, bool COLL = false, typename E = bf16_t>
 __global__ void __launch_bounds__(NT == 1 ? 256 : 512)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
-                 bf16_t* __restrict__ out, PartT<NT>* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
+                 bf16_t* __restrict__ out, PartT<NT, E>* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                  int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                  int n_split, int causal_off, const bf16_t* __restrict__ new_k, const bf16_t* __restrict__ new_v,
                  long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev,
@@ -597,7 +652,12 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       ws_ml += b * bs.w;
     }
   }
-  if (len_dev != nullptr) device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
+  if (len_dev != nullptr) {
+    if constexpr (COLL)
+      device_length(len_dev, q_len, kv_len, ntiles_total, causal_off, ga.len_off);
+    else
+      device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
+  }
   const int ntiles = split_ntiles(split, ntiles_total, n_split);
   bf16_t* kh = kc + (long long)g * k_hs;
   bf16_t* vh = vc + (long long)g * v_hs;
@@ -786,6 +846,15 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     }
   }
   float m_c = -1e30f, l_c = 0.f;       // collector row statistics of this lane's keys (log2 domain)
+  // With a visual mask, lane t of a key-split wave holds the 16 mask bits of
+  // the wave's keys in the split's tile t (t < 64; later tiles load theirs).
+  uint32_t vbits = 0;
+  if constexpr (COLL) {
+    if (ksw && ga.vmask != nullptr && lane < ntiles) {
+      const int kb = tile_key0(split, lane, n_split) + 16 * ks_sub;
+      if (kb < ga.vis_end && kb + 16 > ga.vis_begin) vbits = (ga.vmask[kb >> 5] >> (kb & 31)) & 0xffffu;
+    }
+  }
   // Retire the query loads (and with them the two ring tiles issued before
   // them) here: the compiler counts only its own loads, and a wait for them
   // placed inside the loop would drain the ring there. (With kQLds there are
@@ -914,10 +983,21 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       if (ln >= q_off) {
         const int kb = tile_key0(split, tt, n_split);
         const int key0 = kb + 16 * ks_sub + 4 * lg;
+        uint32_t mb = 0xfu;                                   // the lane's four keys: visual-mask bits
+        if (ga.vmask != nullptr) {                            // wave-uniform
+          uint32_t w16;
+          if (tt < 64) {
+            w16 = (uint32_t)__builtin_amdgcn_readlane((int)vbits, tt);
+          } else {
+            const int kw = kb + 16 * ks_sub;
+            w16 = (kw < ga.vis_end && kw + 16 > ga.vis_begin) ? (ga.vmask[kw >> 5] >> (kw & 31)) & 0xffffu : 0u;
+          }
+          mb = (w16 >> (4 * lg)) & 0xfu;
+        }
         float z[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const bool vis = key0 + i >= ga.vis_begin && key0 + i < ga.vis_end;
+          const bool vis = key0 + i >= ga.vis_begin && key0 + i < ga.vis_end && ((mb >> i) & 1u);
           z[i] = vis ? (sc[i] + sl[i]) * scale_log2 : -INFINITY;
         }
         const int vt = kb / TK - ga.vis_begin / TK;           // wave-uniform
@@ -1009,7 +1089,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
           const f32x4 on = o / Lr;
           *reinterpret_cast<i16x4*>(dst) = EL::pack4(on[0], on[1], on[2], on[3]);
         }
-      } else if constexpr (NT > 1) {
+      } else if constexpr (std::is_same<PartT<NT, E>, half_t>::value) {
         float amax = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
 #pragma unroll
         for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
@@ -1124,7 +1204,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       const f32x4 o = acc[t] / l_row;
       *reinterpret_cast<i16x4*>(dst + 16 * t) = EL::pack4(o[0], o[1], o[2], o[3]);
     }
-  } else if constexpr (NT == 1) {
+  } else if constexpr (!std::is_same<PartT<NT, E>, half_t>::value) {
     const long long prow = (long long)g * n_split * R + (long long)split * R + row;
 #pragma unroll
     for (int t = 0; t < 8; ++t) *reinterpret_cast<f32x4*>(ws_o + prow * D + 16 * t + 4 * lg) = acc[t];
@@ -1401,7 +1481,7 @@ void launch_h16(const void* q, void* k, void* v, void* out, int q_len, int kv_le
                                                  : attn_bf16_kernel<NT, false, false, false, E>);
   hipLaunchKernelGGL(kern, grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
                      static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
-                     static_cast<bf16_t*>(out), static_cast<PartT<NT>*>(ws_o), ws_ml, q_len, kv_len, group, k_hs,
+                     static_cast<bf16_t*>(out), static_cast<PartT<NT, E>*>(ws_o), ws_ml, q_len, kv_len, group, k_hs,
                      v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
                      static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev, ga, ga.idx);
 }
@@ -1437,12 +1517,12 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   int s = launch_status();
   if (s != 0 || p.n_split == 1) return s;
   if (dtype == STD_BF16)
-    hipLaunchKernelGGL((attn_merge_kernel<bf16_t, PartT<NT>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
-                       static_cast<const PartT<NT>*>(ws_o), ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len,
+    hipLaunchKernelGGL((attn_merge_kernel<bf16_t, PartT<NT, bf16_t>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0,
+                       st, static_cast<const PartT<NT, bf16_t>*>(ws_o), ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len,
                        group, bs.o, n_kv);
   else if (dtype == STD_F16)
-    hipLaunchKernelGGL((attn_merge_kernel<f16_t, PartT<NT>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
-                       static_cast<const PartT<NT>*>(ws_o), ws_ml, static_cast<f16_t*>(out), p.n_split, q_len,
+    hipLaunchKernelGGL((attn_merge_kernel<f16_t, PartT<NT, f16_t>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0,
+                       st, static_cast<const PartT<NT, f16_t>*>(ws_o), ws_ml, static_cast<f16_t*>(out), p.n_split, q_len,
                        group, bs.o, n_kv);
   else
     hipLaunchKernelGGL((attn_merge_kernel<float, float>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
@@ -1522,73 +1602,128 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
                      n_new, n_batch, bs, len_dev, ga, static_cast<hipStream_t>(stream));
 }
 
-// Verify + collector workspace: the verify attention's (split partials), then
-// the collector logits [n_kv][q_len][logit_rs] and statistics
-// [n_kv][n_split][q_len].
+// Verify + collector. The collector's query rows fill the padding lanes of the
+// five-row-tile verify layout's last row tile, so one fused launch serves at
+// most coll_chunk(group) verify positions: (group + 1) q <= 80 and q <= 16.
+// Longer verifies run chunk by chunk: chunk [a, b) of the positions is the
+// verify of rows a..b-1 over the first kv_len - q_len + b keys (row i still
+// sees keys [0, kv_len - q_len + i]), with its query rows gathered into the
+// workspace and its output rows copied back, and each chunk adds its
+// positions' softmax rows to the scores in row order -- the same sums, in the
+// same order, as one launch over all rows would form.
+int coll_chunk(int group) { return std::min(16, 80 / (group + 1)); }
+
+// Workspace: the verify attention's split partials, then the collector logits
+// [n_kv][n_vtiles][q][64] and statistics [n_kv][n_split][q] (q = the chunk
+// size), then, for a chunked verify, one chunk's query rows and output rows.
 struct CollLayout {
-  size_t attn, logits_off, stats_off, total;
-  int n_vtiles, n_split;
+  size_t attn, logits_off, stats_off, q_off, o_off, total;
+  int n_vtiles, n_split, q_chunk;
 };
 
-CollLayout coll_layout(int n_kv, int group, int q_len, int kv_len, int vis_begin, int vis_end) {
+// es: element bytes of the rows (2); part_bytes: the split partials' (2 for
+// bf16, 4 for fp16; the workspace query sizes for 4, the larger).
+CollLayout coll_layout(int n_kv, int group, int q_len, int kv_len, int vis_begin, int vis_end, int es,
+                       int part_bytes) {
   CollLayout c{};
-  const SplitPlan p = plan_splits(n_kv, group * q_len, kv_len, STD_BF16);
+  c.q_chunk = std::min(q_len, coll_chunk(group));
+  const int R = group * c.q_chunk;
+  const SplitPlan p = plan_splits(n_kv, R, kv_len, STD_BF16);     // the largest chunk plan (the longest key range)
   c.n_split = p.n_split;
-  c.attn = round_up(ws_layout(n_kv, group * q_len, p, part_bytes_of(STD_BF16, group * q_len)).total, 256);
+  c.attn = round_up(ws_layout(n_kv, R, p, part_bytes).total, 256);
   c.n_vtiles = (vis_end - 1) / TK - vis_begin / TK + 1;
   c.logits_off = c.attn;
-  c.stats_off = round_up(c.logits_off + (size_t)n_kv * c.n_vtiles * q_len * TK * sizeof(float), 256);
-  c.total = round_up(c.stats_off + (size_t)n_kv * p.n_split * q_len * sizeof(float2), 256);
+  c.stats_off = round_up(c.logits_off + (size_t)n_kv * c.n_vtiles * c.q_chunk * TK * sizeof(float), 256);
+  c.q_off = round_up(c.stats_off + (size_t)n_kv * p.n_split * c.q_chunk * sizeof(float2), 256);
+  c.o_off = c.q_off;
+  c.total = c.q_off;
+  if (c.q_chunk < q_len) {
+    const size_t rows = (size_t)n_kv * group * c.q_chunk * D * es;
+    c.o_off = round_up(c.q_off + rows, 256);
+    c.total = round_up(c.o_off + rows, 256);
+  }
   return c;
 }
 
 int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, int q_len, int kv_len,
-                         int d, long long k_hs, long long v_hs, float scale, int dtype, const void* nk,
-                         const void* nv, long long n_hs, long long n_rs, int vis_begin, int vis_end, float* scores,
-                         long long score_hs, void* ws, size_t ws_bytes, void* stream) {
+                         const int32_t* len_dev, int d, long long k_hs, long long v_hs, float scale, int dtype,
+                         const void* nk, const void* nv, long long n_hs, long long n_rs, int vis_begin, int vis_end,
+                         const uint32_t* vmask, const int32_t* vrank, int n_visual, float* scores, long long score_hs,
+                         void* ws, size_t ws_bytes, void* stream) {
   if (!q || !k || !v || !out || !scores) return STD_E_NULL;
   if ((nk == nullptr) != (nv == nullptr)) return STD_E_NULL;
+  if ((vmask == nullptr) != (vrank == nullptr)) return STD_E_NULL;
   if (dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len) return STD_E_SHAPE;
   const int group = n_q / n_kv;
-  // the collector rows fill the padding lanes of the five-row-tile layout's last row tile
-  if (q_len > 16 || (long long)group * q_len + q_len > 80) return STD_E_SHAPE;
+  if (coll_chunk(group) < 1 || (long long)group * q_len > 65535) return STD_E_SHAPE;
   if (vis_begin < 0 || vis_end <= vis_begin || vis_end > kv_len - q_len) return STD_E_SHAPE;
+  if (vmask == nullptr ? n_visual != vis_end - vis_begin : (n_visual < 1 || n_visual > vis_end - vis_begin))
+    return STD_E_SHAPE;
   if (n_kv > 1 && (k_hs < (long long)kv_len * D || v_hs < (long long)kv_len * D)) return STD_E_SHAPE;
-  if (n_kv > 1 && score_hs < vis_end - vis_begin) return STD_E_SHAPE;
+  if (n_kv > 1 && score_hs < n_visual) return STD_E_SHAPE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return STD_E_ALIGN;
   if ((k_hs * 2) % 16 != 0 || (v_hs * 2) % 16 != 0) return STD_E_ALIGN;
   if (nk && (!aligned16(nk) || !aligned16(nv) || (n_hs * 2) % 16 != 0 || (n_rs * 2) % 16 != 0)) return STD_E_ALIGN;
-  const CollLayout cl = coll_layout(n_kv, group, q_len, kv_len, vis_begin, vis_end);
+  const int part_bytes = dtype == STD_BF16 ? 2 : 4;
+  const CollLayout cl = coll_layout(n_kv, group, q_len, kv_len, vis_begin, vis_end, 2, part_bytes);
   if (ws == nullptr || ws_bytes < cl.total) return STD_E_WORKSPACE;
   if (!aligned16(ws)) return STD_E_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int R = group * q_len;
-  const SplitPlan p = plan_splits(n_kv, R, kv_len, STD_BF16);        // bf16 and fp16 plan alike
-  const WsLayout wl = ws_layout(n_kv, R, p, part_bytes_of(STD_BF16, R));
   char* base = static_cast<char*>(ws);
-  half_t* ws_o = p.n_split > 1 ? reinterpret_cast<half_t*>(base + wl.o_off) : nullptr;      // R > 16: fp16
-  float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
-  const CollArgs ca{reinterpret_cast<float*>(base + cl.logits_off), reinterpret_cast<float2*>(base + cl.stats_off),
-                    cl.n_vtiles, vis_begin, vis_end};
-  const int n_new = nk ? q_len : 0;
-  const int n_rows = p.n_split > 1 ? R : 0;
-  auto run = [&](auto elem) -> int {
-    using E = decltype(elem);
-    hipLaunchKernelGGL((attn_bf16_kernel<5, false, false, true, E>), dim3(p.n_split, n_kv, 1),
-                       dim3(Bf16Cfg<5>::kThreads), 0, st, static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k),
-                       static_cast<bf16_t*>(v), static_cast<bf16_t*>(out), ws_o, ws_ml, q_len, kv_len, group, k_hs,
-                       v_hs, scale * 1.4426950408889634f, p.ntiles, p.n_split, kv_len - q_len,
-                       static_cast<const bf16_t*>(nk), static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new,
-                       BatchStrides{0, 0, 0, 0, 0}, nullptr, ca, nullptr);
-    const int s = launch_status();
+  const size_t row_bytes = (size_t)D * 2;
+  for (int a = 0; a < q_len; a += cl.q_chunk) {
+    const int qc = std::min(cl.q_chunk, q_len - a);
+    const bool chunked = qc < q_len;
+    const int kv_c = kv_len - q_len + a + qc;                 // keys the chunk's last row sees, plus one
+    const int R = group * qc;
+    const SplitPlan p = plan_splits(n_kv, R, kv_c, STD_BF16);        // bf16 and fp16 plan alike
+    const WsLayout wl = ws_layout(n_kv, R, p, part_bytes);
+    void* ws_o = p.n_split > 1 ? static_cast<void*>(base + wl.o_off) : nullptr;
+    float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
+    const CollArgs ca{reinterpret_cast<float*>(base + cl.logits_off), reinterpret_cast<float2*>(base + cl.stats_off),
+                      cl.n_vtiles, vis_begin, vis_end, vmask, a};
+    const CollOut co{scores, n_kv > 1 ? score_hs : 0LL, vmask, vrank, n_visual, len_dev, a, a > 0 ? 1 : 0};
+    const void* qa = q;
+    void* oa = out;
+    if (chunked) {
+      // the chunk's query rows [n_q][qc][D] out of [n_q][q_len][D]
+      qa = base + cl.q_off;
+      oa = base + cl.o_off;
+      const hipError_t e = hipMemcpy2DAsync(base + cl.q_off, qc * row_bytes, static_cast<const char*>(q) + a * row_bytes,
+                                            q_len * row_bytes, qc * row_bytes, n_q, hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return (int)e;
+    }
+    const bf16_t* nka = nk ? static_cast<const bf16_t*>(nk) + a * n_rs : nullptr;
+    const bf16_t* nva = nv ? static_cast<const bf16_t*>(nv) + a * n_rs : nullptr;
+    const int n_new = nk ? qc : 0;
+    const int n_rows = p.n_split > 1 ? R : 0;
+    auto run = [&](auto elem) -> int {
+      using E = decltype(elem);
+      using PT = PartT<5, E>;
+      hipLaunchKernelGGL((attn_bf16_kernel<5, false, false, true, E>), dim3(p.n_split, n_kv, 1),
+                         dim3(Bf16Cfg<5>::kThreads), 0, st, static_cast<const bf16_t*>(qa), static_cast<bf16_t*>(k),
+                         static_cast<bf16_t*>(v), static_cast<bf16_t*>(oa), static_cast<PT*>(ws_o), ws_ml, qc, kv_c,
+                         group, k_hs, v_hs,
+                         scale * 1.4426950408889634f, p.ntiles, p.n_split, kv_c - qc, nka, nva, n_hs, n_rs, n_new,
+                         BatchStrides{0, 0, 0, 0, 0}, len_dev, ca, nullptr);
+      const int s = launch_status();
+      if (s != 0) return s;
+      hipLaunchKernelGGL((merge_coll_kernel<E, PT>), dim3(n_rows + (cl.n_vtiles + 15) / 16, n_kv),
+                         dim3(kMergeThreads), 0, st, static_cast<const PT*>(ws_o), ws_ml, static_cast<E*>(oa), p.n_split, qc, group, n_rows, ca.logits, ca.stats, co,
+                         cl.n_vtiles, vis_begin, vis_end);
+      return launch_status();
+    };
+    const int s = dtype == STD_BF16 ? run(bf16_t{}) : run(f16_t{});
     if (s != 0) return s;
-    hipLaunchKernelGGL(merge_coll_kernel<E>, dim3(n_rows + (cl.n_vtiles + 15) / 16, n_kv), dim3(kMergeThreads), 0,
-                       st, ws_o, ws_ml, static_cast<E*>(out), p.n_split, q_len, group, n_rows, ca.logits, ca.stats,
-                       scores, cl.n_vtiles, n_kv > 1 ? score_hs : 0LL, vis_begin, vis_end);
-    return launch_status();
-  };
-  return dtype == STD_BF16 ? run(bf16_t{}) : run(f16_t{});
+    if (chunked) {
+      const hipError_t e = hipMemcpy2DAsync(static_cast<char*>(out) + a * row_bytes, q_len * row_bytes,
+                                            base + cl.o_off, qc * row_bytes, qc * row_bytes, n_q,
+                                            hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return (int)e;
+    }
+  }
+  return 0;
 }
 
 }  // namespace
@@ -1625,9 +1760,17 @@ int scratch_address(hipStream_t st, void** out) {
   }
   std::lock_guard<std::mutex> lock(scratch_mu);
   if (scratch_dev[dev] == nullptr) {
+    // The lookup enqueues nothing, so a first call made while the caller's
+    // stream is being captured into a graph performs it in relaxed capture
+    // mode (a global-mode capture may refuse other HIP calls on this thread).
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    e = hipThreadExchangeStreamCaptureMode(&mode);
+    if (e != hipSuccess) return (int)e;
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess) return (int)e;
+    if (e2 != hipSuccess) return (int)e2;
     scratch_dev[dev] = p;
   }
   *out = scratch_dev[dev];
@@ -1755,7 +1898,8 @@ extern "C" size_t std_verify_attn_collect_workspace_bytes(int n_q, int n_kv, int
                                                           int vis_begin, int vis_end) {
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || q_len < 1 || kv_len < q_len || d != D) return 0;
   if (vis_begin < 0 || vis_end <= vis_begin || vis_end > kv_len) return 0;
-  return coll_layout(n_kv, n_q / n_kv, q_len, kv_len, vis_begin, vis_end).total;
+  if (coll_chunk(n_q / n_kv) < 1) return 0;
+  return coll_layout(n_kv, n_q / n_kv, q_len, kv_len, vis_begin, vis_end, 2, 4).total;
 }
 
 extern "C" int std_verify_attn_collect(const void* q, void* k_cache, void* v_cache, const void* new_k,
@@ -1764,7 +1908,22 @@ extern "C" int std_verify_attn_collect(const void* q, void* k_cache, void* v_cac
                                        long long new_head_stride, long long new_row_stride, float scale, int dtype,
                                        int vis_begin, int vis_end, float* scores, long long scores_head_stride,
                                        void* workspace, size_t workspace_bytes, void* stream) {
-  return verify_collect_entry(q, k_cache, v_cache, out, n_q, n_kv, q_len, kv_len, d, k_head_stride, v_head_stride,
-                              scale, dtype, new_k, new_v, new_head_stride, new_row_stride, vis_begin, vis_end, scores,
-                              scores_head_stride, workspace, workspace_bytes, stream);
+  return verify_collect_entry(q, k_cache, v_cache, out, n_q, n_kv, q_len, kv_len, nullptr, d, k_head_stride,
+                              v_head_stride, scale, dtype, new_k, new_v, new_head_stride, new_row_stride, vis_begin,
+                              vis_end, nullptr, nullptr, vis_end - vis_begin, scores, scores_head_stride, workspace,
+                              workspace_bytes, stream);
+}
+
+extern "C" int std_verify_attn_collect_ex(const void* q, void* k_cache, void* v_cache, const void* new_k,
+                                          const void* new_v, void* out, int n_q, int n_kv, int q_len, int kv_len,
+                                          const int32_t* len_dev, int d, long long k_head_stride,
+                                          long long v_head_stride, long long new_head_stride,
+                                          long long new_row_stride, float scale, int dtype, int vis_begin,
+                                          int vis_end, const uint32_t* vis_mask, const int32_t* vis_rank,
+                                          int n_visual, float* scores, long long scores_head_stride, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  return verify_collect_entry(q, k_cache, v_cache, out, n_q, n_kv, q_len, kv_len, len_dev, d, k_head_stride,
+                              v_head_stride, scale, dtype, new_k, new_v, new_head_stride, new_row_stride, vis_begin,
+                              vis_end, vis_mask, vis_rank, n_visual, scores, scores_head_stride, workspace,
+                              workspace_bytes, stream);
 }

@@ -670,7 +670,11 @@ template <> __device__ __forceinline__ double prob_to_f64<f16_bits>(f16_bits x) 
   return (double)(float)__builtin_bit_cast(_Float16, x.v);
 }
 
-template <typename T>
+// VEC: four-column vector loads (rows 8-byte aligned for 16-bit types,
+// 16-byte for fp32); otherwise element loads, for any prompt length and
+// stride (the reference's contiguous [1, Hq, T, P] probabilities have row
+// stride P, which is odd for most prompts).
+template <typename T, bool VEC>
 __global__ void __launch_bounds__(256)
 probs_colsum_kernel(const T* __restrict__ probs, long long head_stride, long long row_stride, int group, int text_len,
                     int prompt_len, int rows_per_rg, double* __restrict__ colpart, int n_kv) {
@@ -686,7 +690,7 @@ probs_colsum_kernel(const T* __restrict__ probs, long long head_stride, long lon
     const int hl = r / text_len, t = r - hl * text_len;
     const T* row = probs + (long long)(g * group + hl) * head_stride + (long long)t * row_stride + j0;
     T x[4];
-    if (full) {
+    if (VEC && full) {
       if constexpr (sizeof(T) == 2) {
         const uint2 u = *reinterpret_cast<const uint2*>(row);
         x[0] = __builtin_bit_cast(T, (uint16_t)(u.x & 0xffffu));
@@ -702,7 +706,7 @@ probs_colsum_kernel(const T* __restrict__ probs, long long head_stride, long lon
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = row[min(e, prompt_len - 1 - j0)];
+      for (int e = 0; e < 4; ++e) x[e] = row[min(e, prompt_len - 1 - j0)];   // in-row: columns past P re-read P - 1
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] += prob_to_f64<T>(x[e]);
@@ -743,7 +747,11 @@ int launch_select_probs(const void* probs, long long head_stride, long long row_
   const ProbsPlan p = plan_probs(n_q, n_kv, text_len, prompt_len, n_vis);
   char* base = static_cast<char*>(ws);
   double* colpart = reinterpret_cast<double*>(base + p.off_col);
-  hipLaunchKernelGGL((probs_colsum_kernel<T>), dim3((prompt_len + 1023) / 1024, n_kv, p.n_rg), dim3(256), 0, st,
+  const size_t vb = 4 * sizeof(T);
+  const bool vec = (uintptr_t)probs % vb == 0 && (row_stride * (long long)sizeof(T)) % vb == 0 &&
+                   (head_stride * (long long)sizeof(T)) % vb == 0;
+  auto kern = vec ? probs_colsum_kernel<T, true> : probs_colsum_kernel<T, false>;
+  hipLaunchKernelGGL(kern, dim3((prompt_len + 1023) / 1024, n_kv, p.n_rg), dim3(256), 0, st,
                      static_cast<const T*>(probs), head_stride, row_stride, n_q / n_kv, text_len, prompt_len,
                      p.rows_per_rg, colpart, n_kv);
   const int s = launch_status();
@@ -863,11 +871,9 @@ extern "C" int std_select_topk_probs(const void* probs, long long head_stride, l
   if (n_visual < 1 || n_visual > prompt_len || k_select < 1 || k_select > n_visual) return STD_E_SHAPE;
   if (row_stride < prompt_len || head_stride < row_stride * text_len) return STD_E_SHAPE;
   if (workspace_bytes < plan_probs(n_q, n_kv, text_len, prompt_len, n_visual).total) return STD_E_WORKSPACE;
-  // four-column loads: 8-byte (16-bit types) or 16-byte (fp32) aligned rows
+  // element-aligned probabilities; rows aligned to four elements take vector loads
   const int es = dtype == STD_F32 ? 4 : 2;
-  if (!aligned16(workspace) || ((uintptr_t)probs % (4 * es)) != 0 || (row_stride * es) % (4 * es) != 0 ||
-      (head_stride * es) % (4 * es) != 0)
-    return STD_E_ALIGN;
+  if (!aligned16(workspace) || ((uintptr_t)probs % es) != 0) return STD_E_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == STD_F16)
     return launch_select_probs<f16_bits>(probs, head_stride, row_stride, n_q, n_kv, text_len, prompt_len, visual_pos,

@@ -22,7 +22,10 @@ so eager and captured steps run identical kernels. Longer inputs (the prompt
 prefill, which is not part of the decode path) use torch's rotary embedding
 and chunked fp32 matrix products.
 
-Dense GEMMs/GEMVs, norms and the MLP run in torch (hipBLASLt).
+Decode and verify rows (at most 16) run their projections, norms and the
+MLP on the HIP GEMV and RMSNorm kernels (std_gemv, std_rms_norm), with
+hipBLASLt only for the ten-row q/k/v and lm_head projections; the prompt
+prefill uses torch.
 """
 from __future__ import annotations
 
@@ -214,13 +217,13 @@ class RandomDecoder:
                 self.captured_queries[li] = q
             gather = controller.gather_for(li) if controller is not None and controller.enabled else None
             collector = self.verify_collector
-            if collector is not None and collector.active and n > 1:
+            if collector is not None and collector.collecting and n > 1:
                 # the verify forward with the visual-attention collector riding its attention pass
-                if not host_lengths:
-                    raise RuntimeError("the verification collector runs in eager (host-length) verify steps")
-                out, scores = ops.verify_attention_collect(q, kc.data, vc.data, collector.vis_begin,
-                                                           collector.vis_end, kv_len=kc.length + n)
-                collector.record(li, scores)
+                # (planned for the cache capacity, as attention_devlen: the same attention rows)
+                out, _ = ops.verify_attention_collect(q, kc.data, vc.data, visual=collector.visual,
+                                                      kv_len=kc.capacity, length=state[0:1],
+                                                      scores=collector.scores_out(li))
+                collector.record(li)
             elif gather is not None:      # index-addressed sparse cache: prompt keys read from the dense cache
                 dk, dv, index, n_index = gather
                 out = ops.gqa_decode_indexed(q, dk, dv, index, n_index, kc.data, vc.data, length=state[0:1],

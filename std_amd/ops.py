@@ -814,11 +814,55 @@ def gqa_decode_noalloc(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
     return out
 
 
+class VisualKeys:
+    """The visual key positions a collector scores, in the form the collector
+    launch reads: the first position and last + 1 (begin, end), the count n,
+    and, unless the positions are the whole range [begin, end), a device
+    bitmask (uint32 words as int32, bit j % 32 of word j // 32 set for a
+    visual key j) with each word's rank (visual keys below it). Build it once
+    per prompt with ``visual_keys(positions, device)``."""
+
+    def __init__(self, begin: int, end: int, n: int, mask: Optional[torch.Tensor], rank: Optional[torch.Tensor],
+                 positions: torch.Tensor):
+        self.begin, self.end, self.n = int(begin), int(end), int(n)
+        self.mask, self.rank = mask, rank
+        self.positions = positions
+
+    @property
+    def contiguous(self) -> bool:
+        return self.mask is None
+
+
+def visual_keys(positions, device) -> VisualKeys:
+    """VisualKeys of an ascending set of visual positions (a tensor or a
+    sequence of ints); dynamic_selection.py:515 gathers key_states at them."""
+    pos = torch.as_tensor(positions).to("cpu", torch.int64).reshape(-1)
+    if pos.numel() == 0:
+        raise ValueError("no visual positions")
+    if int(pos[0]) < 0 or (pos.numel() > 1 and not bool((pos[1:] > pos[:-1]).all())):
+        raise ValueError("visual positions must be nonnegative and strictly ascending")
+    begin, end, n = int(pos[0]), int(pos[-1]) + 1, int(pos.numel())
+    if n == end - begin:
+        return VisualKeys(begin, end, n, None, None, pos)
+    n_words = (end + 31) // 32
+    bits = torch.zeros(n_words * 32, dtype=torch.int64)
+    bits[pos] = 1
+    weights = torch.tensor([1 << i for i in range(32)], dtype=torch.int64)
+    words = (bits.view(n_words, 32) * weights).sum(1)
+    words = torch.where(words >= 1 << 31, words - (1 << 32), words).to(torch.int32)     # uint32 bit pattern
+    counts = bits.view(n_words, 32).sum(1)
+    rank = (torch.cumsum(counts, 0) - counts).to(torch.int32)
+    dev = torch.device(device)
+    return VisualKeys(begin, end, n, words.to(dev), rank.to(dev), pos)
+
+
 def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
-                             vis_begin: int, vis_end: int, new_key: Optional[torch.Tensor] = None,
-                             new_value: Optional[torch.Tensor] = None, kv_len: Optional[int] = None,
-                             scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                             scores: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                             vis_begin: Optional[int] = None, vis_end: Optional[int] = None,
+                             new_key: Optional[torch.Tensor] = None, new_value: Optional[torch.Tensor] = None,
+                             kv_len: Optional[int] = None, scale: Optional[float] = None,
+                             out: Optional[torch.Tensor] = None, scores: Optional[torch.Tensor] = None,
+                             visual: Optional[VisualKeys] = None,
+                             length: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Dense verify attention plus the visual-attention collector in one pass
     (VerificationCollectorV3._hook, dynamic_selection.py:504-519, riding the
     verify forward at modeling_qwen2_5_vl.py:1063-1067).
@@ -827,10 +871,16 @@ def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value
     cache views (read in place). Without new_key/new_value the caches hold
     kv_len (default S) keys including this step's q_len rows; with them
     ([1, n_kv, q_len, D]) those rows are appended at kv_len - q_len first.
-    Returns (out [1, n_q, q_len, D], scores [n_kv, vis_end - vis_begin] fp32):
-    out is verify_attention's result bit for bit; scores[g, j] sums, over the
-    q_len positions, the softmax over the visual keys [vis_begin, vis_end) of
-    the group-mean query of KV head g."""
+    With ``length`` (device int32 [1]) the cache instead holds length[0] rows
+    plus this step's q_len, read on the device (a graph-replayed verify), and
+    kv_len is the largest such total (default S).
+    The visual keys are [vis_begin, vis_end), or any ascending set given as
+    ``visual`` (see visual_keys).
+    Returns (out [1, n_q, q_len, D], scores [n_kv, n_visual] fp32):
+    scores[g, r] sums, over the q_len positions, the softmax over the visual
+    keys of the group-mean query of KV head g, at the r-th visual key. out is
+    verify_attention's result bit for bit when (group + 1) * q_len <= 80;
+    longer verifies run in chunks of positions."""
     dev = _check_device(query, key_cache, value_cache)
     if query.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError("the collector path is bf16 or fp16")
@@ -843,10 +893,18 @@ def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value
         raise ValueError(f"Expected query [1, n_q, q_len, D], got {tuple(query.shape)}")
     _, n_q, q_len, d = query.shape
     n_kv = key_cache.shape[1]
+    if n_q % n_kv:
+        raise ValueError(f"Query heads ({n_q}) must be divisible by KV heads ({n_kv}).")
+    if n_q // n_kv + 1 > 80:
+        raise ValueError(f"{n_q // n_kv} query heads per KV head exceed the collector's 79")
     if kv_len is None:
         kv_len = key_cache.shape[2]
     if not (q_len <= kv_len <= key_cache.shape[2]):
         raise ValueError(f"kv_len={kv_len} must be in [q_len, cache capacity {key_cache.shape[2]}]")
+    if length is not None:
+        _check_dev_scalar("length", length)
+        if length.device != dev:
+            raise RuntimeError("length must be on the query's device")
     appending = new_key is not None
     if appending != (new_value is not None):
         raise ValueError("new_key and new_value go together")
@@ -858,27 +916,36 @@ def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value
                 raise TypeError(f"{name} must match the query dtype and device")
         if not same_layout(new_key, new_value):
             raise ValueError("new_key and new_value must share strides")
-    if not (0 <= vis_begin < vis_end <= kv_len - q_len):
-        raise ValueError(f"visual keys [{vis_begin}, {vis_end}) must be prompt keys below {kv_len - q_len}")
+    if visual is None:
+        if vis_begin is None or vis_end is None:
+            raise ValueError("give the visual keys as vis_begin/vis_end or as visual=")
+        visual = VisualKeys(vis_begin, vis_end, vis_end - vis_begin, None, None, None)
+    elif vis_begin is not None or vis_end is not None:
+        raise ValueError("give the visual keys once")
+    elif visual.mask is not None and visual.mask.device != dev:
+        raise RuntimeError("the visual key mask must be on the query's device")
+    if not (0 <= visual.begin < visual.end <= kv_len - q_len):
+        raise ValueError(f"visual keys [{visual.begin}, {visual.end}) must be prompt keys below {kv_len - q_len}")
     if out is None:
         out = torch.empty_like(query)
     elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped like query")
-    n_vis = vis_end - vis_begin
     if scores is None:
-        scores = torch.empty(n_kv, n_vis, dtype=torch.float32, device=dev)
-    elif scores.dtype != torch.float32 or scores.dim() != 2 or tuple(scores.shape) != (n_kv, n_vis) or \
+        scores = torch.empty(n_kv, visual.n, dtype=torch.float32, device=dev)
+    elif scores.dtype != torch.float32 or scores.dim() != 2 or tuple(scores.shape) != (n_kv, visual.n) or \
             scores.stride(1) != 1:
-        raise ValueError(f"scores must be float32 [{n_kv}, {n_vis}] with contiguous rows")
+        raise ValueError(f"scores must be float32 [{n_kv}, {visual.n}] with contiguous rows")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     lib = _lib.load_library()
-    ws_bytes = lib.std_verify_attn_collect_workspace_bytes(n_q, n_kv, q_len, kv_len, d, vis_begin, vis_end)
+    ws_bytes = lib.std_verify_attn_collect_workspace_bytes(n_q, n_kv, q_len, kv_len, d, visual.begin, visual.end)
     ws_ptr = _attn_workspace(ws_bytes, dev)
-    _lib.call("std_verify_attn_collect", query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+    _lib.call("std_verify_attn_collect_ex", query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
               new_key.data_ptr() if appending else None, new_value.data_ptr() if appending else None,
-              out.data_ptr(), n_q, n_kv, q_len, int(kv_len), d, key_cache.stride(1), value_cache.stride(1),
-              new_key.stride(1) if appending else 0, new_key.stride(2) if appending else 0, float(scale),
-              _dtype_code(query), int(vis_begin), int(vis_end), scores.data_ptr(), scores.stride(0), ws_ptr, ws_bytes,
-              _stream(dev))
+              out.data_ptr(), n_q, n_kv, q_len, int(kv_len), length.data_ptr() if length is not None else None, d,
+              key_cache.stride(1), value_cache.stride(1), new_key.stride(1) if appending else 0,
+              new_key.stride(2) if appending else 0, float(scale), _dtype_code(query), visual.begin, visual.end,
+              visual.mask.data_ptr() if visual.mask is not None else None,
+              visual.rank.data_ptr() if visual.rank is not None else None, visual.n, scores.data_ptr(),
+              scores.stride(0), ws_ptr, ws_bytes, _stream(dev))
     return out, scores

@@ -6,11 +6,12 @@ prompt prefill, a gamma-token draft with sparse attention over a compact
 cache, one parallel dense verification, greedy acceptance, rollback and the
 bonus-token append. What changes underneath:
 
-* selection (``build_sparse_selection``) takes each layer's text-suffix
-  queries and the dense key cache instead of materialised attention
-  probabilities, and keeps the selected indices on the device
+* selection keeps the selected indices on the device
   (``SparseSelection.topk_device``; the reference's per-layer CPU lists are a
-  lazily built host mirror);
+  lazily built host mirror). ``build_sparse_selection`` takes the reference's
+  input, the materialised attention probabilities; the generate loop uses
+  ``build_sparse_selection_from_queries``, which reads each layer's
+  text-suffix queries and the dense key cache and never materialises them;
 * compaction gathers straight from the dense cache into the sparse cache
   (no full-prompt copy);
 * every attention call of the decode loop is a libstdhip.so launch with the
@@ -343,25 +344,38 @@ class VerificationCollectorV3:
     gathered visual keys in separate GEMMs, each layer's scores here come out
     of the verify attention launch itself (``ops.verify_attention_collect``):
     the collector's query rows ride the verify kernel's padding rows, so the
-    visual keys are read once. The visual positions must form one contiguous
-    range (the video tokens of a prompt do); verify steps must run eagerly
-    (host lengths)."""
+    visual keys are read once. Any ascending set of visual positions is
+    served (the hook gathers key_states at visual_positions); a verify of more
+    positions than one launch carries ((group + 1) * q_len > 80, e.g. gamma >=
+    10 at seven query heads per KV head) runs in chunks of positions. Each
+    layer's scores land in one persistent device buffer, so a verify step
+    captured in a HIP graph (std_generate_qwen25vl(use_graphs=True)) writes
+    them on every replay and end_verification reads them back with the round.
+    begin_prefill / end_prefill do nothing, so the collector can also be
+    installed with set_trace_collector, which brackets every verify step."""
 
     def __init__(self, model, visual_positions: torch.Tensor):
-        pos = visual_positions.to(torch.long).cpu().reshape(-1)
+        pos = torch.as_tensor(visual_positions).to(torch.long).cpu().reshape(-1)
         if pos.numel() == 0:
             raise ValueError("no visual positions")
-        self.vis_begin, self.vis_end = int(pos[0]), int(pos[-1]) + 1
-        if not torch.equal(pos, torch.arange(self.vis_begin, self.vis_end)):
-            raise ValueError("the HIP collector serves one contiguous, ascending range of visual positions")
         self.model = model
         self.visual_positions = pos
         self.visual_len = int(pos.numel())
         self.num_kv_heads = model.config.num_key_value_heads
+        self.visual = ops.visual_keys(pos, model.device)       # raises unless strictly ascending
+        self.vis_begin, self.vis_end = self.visual.begin, self.visual.end
+        self.scores_dev = torch.zeros(model.config.num_hidden_layers, self.num_kv_heads, self.visual_len,
+                                      dtype=torch.float32, device=model.device)
         self.rounds: List[torch.Tensor] = []
         self.active = False
-        self._layer_scores: Dict[int, torch.Tensor] = {}
+        self.capturing = False            # set while a verify graph with the collector is captured
+        self.graph_layers: List[int] = []
+        self._layers: List[int] = []
         self.collect_time = 0.0
+
+    @property
+    def collecting(self) -> bool:
+        return self.active or self.capturing
 
     def install(self) -> None:
         self.model.verify_collector = self
@@ -370,27 +384,61 @@ class VerificationCollectorV3:
         if getattr(self.model, "verify_collector", None) is self:
             self.model.verify_collector = None
 
+    def begin_prefill(self) -> None:
+        pass
+
+    def end_prefill(self) -> None:
+        pass
+
     def begin_verification(self, round_id: int) -> None:
         self.active = True
-        self._layer_scores = {}
+        self._layers = []
 
-    def record(self, layer_idx: int, scores: torch.Tensor) -> None:
-        """Called by the verify forward with one layer's device scores [kv_heads, visual_len]."""
-        self._layer_scores[layer_idx] = scores
+    def scores_out(self, layer_idx: int) -> torch.Tensor:
+        """The device buffer [kv_heads, visual_len] that a verify forward's
+        layer writes its scores into."""
+        return self.scores_dev[layer_idx]
+
+    def record(self, layer_idx: int) -> None:
+        """Called by the verify forward once layer layer_idx has written its scores."""
+        if self.capturing:
+            self.graph_layers.append(layer_idx)
+        else:
+            self._layers.append(layer_idx)
+
+    def note_replay(self) -> None:
+        """A captured verify graph with the collector was replayed: its layers
+        wrote this round's scores."""
+        if self.active:
+            self._layers = list(self.graph_layers)
 
     def end_verification(self) -> None:
         self.active = False
-        if not self._layer_scores:
+        if not self._layers:
             return
         t0 = time.perf_counter()
-        order = sorted(self._layer_scores)
-        stacked = torch.stack([self._layer_scores[i] for i in order], dim=0).cpu()  # single sync
+        order = sorted(set(self._layers))
+        if order == list(range(self.scores_dev.shape[0])):
+            stacked = self.scores_dev.cpu()                                  # single sync
+        else:
+            stacked = self.scores_dev[torch.tensor(order, device=self.scores_dev.device)].cpu()
         self.collect_time += time.perf_counter() - t0
         self.rounds.append(stacked)
-        self._layer_scores = {}
+        self._layers = []
 
     def latest_scores(self) -> Optional[torch.Tensor]:
         return self.rounds[-1] if self.rounds else None
+
+
+def math_reverify_count(verify_attn_backend: str, accept_len: int, draft_len: int) -> int:
+    """1 if the reference would re-verify this round with the math SDPA
+    backend, else 0. With "math_on_full_accept" the reference re-runs a fully
+    accepted draft's verification with math attention and counts it in
+    fallback_count (std_qwen25vl.py:843-858). The HIP verify already computes
+    the math definition, so that re-run returns the same predictions: the
+    round is counted, the accepted length and bonus stay, and
+    fallback_accepted_extra gains nothing."""
+    return int(verify_attn_backend == "math_on_full_accept" and accept_len == draft_len)
 
 
 def _token_argmax(logits: torch.Tensor) -> torch.Tensor:
@@ -558,7 +606,15 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     pending token as three captured HIP graphs (gamma sparse draft steps; the
     dense verify forward with greedy acceptance; the sparse bonus step), with
     one readback per round; the first round and any shorter round run the same
-    device-state steps eagerly.
+    device-state steps eagerly. With a VerificationCollectorV3 installed on the
+    model when the call begins, a second verify graph carries its kernels and
+    replaces the plain one in the rounds where the collector is active.
+
+    verify_attn_backend: "default", "math" and "math_on_full_accept" all run
+    the exact HIP verify (the math definition). With "math_on_full_accept" a
+    fully accepted draft counts in ``fallback_count``, as the reference's
+    math re-verification does (std_qwen25vl.py:843-858); that re-run would
+    return the same predictions, so ``fallback_accepted_extra`` stays 0.
 
     sparse_kv: "compact" gathers the selected prompt rows into the sparse
     cache; "indexed" (bf16, fp16) has the draft read them from the dense cache
@@ -579,8 +635,8 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         raise ValueError(f"Unsupported verify_mode={verify_mode!r}; the HIP path implements 'parallel'.")
     if verify_fallback != "none" or verify_margin_threshold is not None:
         raise ValueError("verify fallbacks and margin re-runs are not part of the HIP decode path")
-    if verify_attn_backend not in {"default", "math"}:
-        raise ValueError("verify_attn_backend must be 'default' or 'math' (both run the exact HIP verify).")
+    if verify_attn_backend not in {"default", "math", "math_on_full_accept"}:
+        raise ValueError("verify_attn_backend must be 'default', 'math', or 'math_on_full_accept'.")
     if adaptive_gamma_min is not None and not (1 <= adaptive_gamma_min <= gamma):
         raise ValueError("adaptive_gamma_min must be between 1 and gamma.")
     if adaptive_gamma_mode not in {"accept_len", "conservative"}:
@@ -638,7 +694,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     pending_lengths: List[int] = []
     gamma_history: List[int] = []
     dense_pending: List[int] = []
-    accepted_total = proposed_total = decode_rounds = 0
+    accepted_total = proposed_total = decode_rounds = fallback_count = 0
     draft_time = verify_time = bonus_time = cache_adjust_time = 0.0
     current_gamma = gamma
     dense_next_i32 = dense_next.reshape(1).to(torch.int32)
@@ -683,11 +739,29 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
             controller.set_enabled(False)
         return tok_s
 
+    collector = getattr(model, "verify_collector", None)      # captured into the verify graph with graphs
+
+    def verify_collect_phase(draft: torch.Tensor) -> torch.Tensor:
+        # the verify forward with the installed collector's kernels in it (captured once, replayed in the
+        # rounds where the collector is active)
+        collector.capturing = True
+        collector.graph_layers = []
+        try:
+            return verify_phase(draft, True)
+        finally:
+            collector.capturing = False
+
     def capture_round():
         snap = (st4.clone(), tok_s.clone(), pending.clone())
 
         def run_all():
-            bonus_phase(verify_phase(draft_phase(gamma), True))
+            draft = draft_phase(gamma)
+            state = st4.clone()
+            res = verify_phase(draft, True)
+            if collector is not None:        # the same verify again, with the collector (same rows, same result)
+                st4.copy_(state)
+                res = verify_collect_phase(draft)
+            bonus_phase(res)
 
         def restore():
             st4.copy_(snap[0])
@@ -702,11 +776,19 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
 
         def verify_static(has_pending):
             holder["res"] = verify_phase(holder["draft"], has_pending)
+            holder["logits"] = last_logits[0]
             return holder["res"]
 
-        caps = _warm_and_capture(run_all, restore, [(draft_static, ()), (verify_static, (True,)),
-                                                    (lambda: bonus_phase(holder["res"]), ())])
-        return caps, holder["draft"], holder["res"], last_logits[0]     # the verify graph's logits buffer
+        phases = [(draft_static, ()), (verify_static, (True,)), (lambda: bonus_phase(holder["res"]), ())]
+        if collector is not None:
+            def verify_collect_static():
+                holder["res"].copy_(verify_collect_phase(holder["draft"]))     # the bonus graph reads holder["res"]
+                holder["coll_logits"] = last_logits[0]
+                return holder["res"]
+            phases.append((verify_collect_static, ()))
+        caps = _warm_and_capture(run_all, restore, phases)
+        # the verify graphs' logits buffers: plain, and with the collector (or None)
+        return caps, holder["draft"], holder["res"], (holder["logits"], holder.get("coll_logits"))
 
     torch.cuda.synchronize()
     decode_start = time.time()
@@ -740,10 +822,22 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         trace = _TRACE_COLLECTOR
         if trace is not None:
             trace.begin_verification(decode_rounds)
-        if replay:
+        current = getattr(model, "verify_collector", None)
+        collecting = current is not None and current.active
+        if replay and collecting and (len(graphs[0]) < 4 or current is not collector):
+            # a collector installed after the call began has no captured verify: this round's verify runs
+            # eagerly (device state), and the captured bonus step reads its result from the verify graph's buffer
+            graphs[2].copy_(verify_phase(draft_dev, True))
+            res = graphs[2]
+        elif replay and collecting:
+            graphs[0][3][0].replay()
+            collector.note_replay()
+            res = graphs[2]
+            last_logits[0] = graphs[3][1]
+        elif replay:
             graphs[0][1][0].replay()
             res = graphs[2]
-            last_logits[0] = graphs[3]
+            last_logits[0] = graphs[3][0]
         elif use_graphs:
             res = verify_phase(draft_dev, bool(dense_pending))
         else:
@@ -763,6 +857,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         verify_time += _profile_mark(profile_decode) - stage
         accept_lengths.append(accept_len)
         accepted_total += accept_len
+        fallback_count += math_reverify_count(verify_attn_backend, accept_len, propose_len)
         if adaptive_gamma_min is not None:
             if accept_len < propose_len:
                 if adaptive_gamma_mode == "accept_len":
@@ -825,7 +920,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         draft_time=draft_time, verify_time=verify_time, bonus_time=bonus_time, cache_adjust_time=cache_adjust_time,
         cache_init_time=cache_init_time, prefill_time=selection_prefill_time,
         selection_prefill_time=selection_prefill_time, selection_time=selection_time, dense_prefill_time=0.0,
-        sparse_cache_time=sparse_cache_time)
+        sparse_cache_time=sparse_cache_time, fallback_count=fallback_count)
     return result, selection
 
 

@@ -152,12 +152,39 @@ def test_verify_collect_validation():
     assert call(dt=3) == -2
     assert call(sc=NULL) == -1
     assert call(nk=16) == -1                    # new_k without new_v
-    assert call(ql=11) == -3                    # (7 + 1) * 11 > 80 rows
-    assert call(nq=4, ql=17) == -3              # more than 16 collector rows
+    # (7 + 1) * 11 > 80 rows: served in chunks of positions, which need room
+    # for one chunk's query and output rows
+    ws10 = lib.std_verify_attn_collect_workspace_bytes(28, 4, 10, 4106, 128, 0, 3968)
+    ws11 = lib.std_verify_attn_collect_workspace_bytes(28, 4, 11, 4106, 128, 0, 3968)
+    assert ws11 >= ws10 + 2 * 28 * 10 * 128 * 2
+    assert call(ql=11, dt=2, wsb=ws10) == -4   # fp16: fp32 partials, the size the query reports
+    assert call(nq=4, ql=17, wsb=10) == -4      # chunks of 16 positions
+    assert lib.std_verify_attn_collect_workspace_bytes(80, 1, 2, 4106, 128, 0, 3968) == 0   # 81 > 80 rows
+    assert call(nq=80, nkv=1, ql=2) == -3
     assert call(ve=4100) == -3                  # visual keys must be prompt keys
     assert call(vb=3968) == -3                  # empty visual range
     assert call(schs=100) == -3                 # score rows overlap
     assert call(wsb=10) == -4
+
+
+def test_verify_collect_ex_validation():
+    lib = _lib.load_library()
+    hs = 4106 * 128
+    args = dict(q=16, k=16, v=16, nk=NULL, nv=NULL, out=16, nq=28, nkv=4, ql=10, kv=4106, len_dev=NULL, d=128,
+                khs=hs, vhs=hs, nhs=0, nrs=0, scale=0.088, dt=1, vb=0, ve=3968, mask=NULL, rank=NULL, nvis=3968,
+                sc=16, schs=3968, ws=16, wsb=1 << 30, st=NULL)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.std_verify_attn_collect_ex(*a.values())
+    assert call(mask=16) == -1                  # mask and rank go together
+    assert call(rank=16) == -1
+    assert call(nvis=3000) == -3                # a whole range counts vis_end - vis_begin keys
+    assert call(mask=16, rank=16, nvis=0) == -3
+    assert call(mask=16, rank=16, nvis=3969) == -3   # more than the range holds
+    assert call(mask=16, rank=16, nvis=100, schs=99) == -3
+    assert call(mask=16, rank=16, nvis=100, wsb=10) == -4
+    assert call(dt=0) == -2
 
 
 def test_select_probs_validation():
@@ -175,8 +202,7 @@ def test_select_probs_validation():
     assert call(k=P) == -3                      # k above the visual count
     assert call(rs=P - 1) == -3                 # rows overlap
     assert call(nkv=5) == -3                    # 28 % 5
-    assert call(p=18) == -5                     # fp16 rows read four columns (8 bytes) at a time
-    assert call(rs=P + 2, hs=T * (P + 2)) == -5
+    assert call(p=17) == -5                     # fp16 elements must be 2-byte aligned
     assert call(wsb=100) == -4
 
 

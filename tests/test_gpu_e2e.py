@@ -140,6 +140,13 @@ def test_full_selection_draft_equals_dense(tiny32):
     assert std.acceptance_rate == 1.0
     ar = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=36, ignore_eos=True)
     assert first_divergence(std.output_ids, ar.output_ids) is None
+    # "math_on_full_accept": every round accepts its whole draft, so every
+    # round counts one math re-verification, which changes nothing
+    math, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=36, gamma=5,
+                                    explicit_k=300, ignore_eos=True, verify_attn_backend="math_on_full_accept")
+    assert torch.equal(math.output_ids, std.output_ids) and math.accept_lengths == std.accept_lengths
+    assert math.fallback_count == math.decode_rounds and math.fallback_accepted_extra == 0
+    assert std.fallback_count == 0
 
 
 def test_graph_rounds_equal_eager_rounds_fp32(tiny32):

@@ -57,6 +57,27 @@ def test_select_topk_probs_strided_view():
     np.testing.assert_array_equal(topk.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("dtype,P", [(torch.float16, 4093), (torch.bfloat16, 2047), (torch.float32, 4094)])
+def test_select_topk_probs_odd_prompt_length(dtype, P):
+    """The reference's contiguous [1, n_q, T, P] probabilities with a prompt
+    length that is not a multiple of four (row stride P): rows are not
+    four-element aligned, so the column sums take element loads."""
+    n_q, n_kv, T = 28, 4, 128
+    V = P - T
+    announce(f"select from probs {dtype} odd P={P}")
+    probs = _probs(n_q, T, P, dtype, P + 11, 0.05)
+    assert probs.is_contiguous() and probs.stride(2) == P
+    vis = torch.arange(V, dtype=torch.int32)
+    topk, scores = ops.select_topk_probs(probs.to(dev()), vis.to(dev()), 896, n_kv, return_scores=True)
+    torch.cuda.synchronize()
+    want_scores = ref_sel.scores_from_probs(probs, n_kv)
+    np.testing.assert_array_equal(topk.cpu().numpy(), ref_sel.topk_positions(want_scores, np.arange(V), 896))
+    if dtype == torch.float16:
+        assert np.array_equal(scores.cpu().numpy(), want_scores)        # exact sums
+    else:
+        np.testing.assert_allclose(scores.cpu().numpy(), want_scores, rtol=1e-13)
+
+
 def test_build_sparse_selection_reference_signature():
     """build_sparse_selection(attentions, full_input_ids, video_token_id,
     text_start, target_k_plus_text, explicit_k, num_key_value_heads) on two

@@ -106,6 +106,23 @@ def test_std_generate_rejects_unsupported_options(kwargs):
         std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
 
 
+def test_math_on_full_accept_is_accepted_and_counts_full_accepts():
+    """verify_attn_backend="math_on_full_accept" (std_qwen25vl.py:111-116,
+    657-658, 843-858) is a valid option, and a round counts as one math
+    re-verification exactly when its whole draft was accepted."""
+    from std_amd.std_qwen25vl import math_reverify_count
+    assert math_reverify_count("math_on_full_accept", 9, 9) == 1
+    assert math_reverify_count("math_on_full_accept", 3, 3) == 1
+    assert math_reverify_count("math_on_full_accept", 8, 9) == 0
+    assert math_reverify_count("math_on_full_accept", 0, 9) == 0
+    for backend in ("default", "math"):
+        assert math_reverify_count(backend, 9, 9) == 0
+    # validation passes (the call then fails on the missing model, not on the option)
+    with pytest.raises(AttributeError):
+        std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8,
+                              verify_attn_backend="math_on_full_accept")
+
+
 def test_indexed_sparse_kv_needs_a_16_bit_model():
     fp32_model = types.SimpleNamespace(dtype=torch.float32)
     with pytest.raises(ValueError):

@@ -1,8 +1,14 @@
 """The allocation-free decode entry point (std_gqa_decode_noalloc, which keeps
 its split partials in the library's own per-GPU scratch array) against the
 workspace entry point std_gqa_decode, through the C ABI: bit-equal outputs on
-two calls in a row, the second with a smaller input, in bf16 and fp32."""
+two calls in a row, the second with a smaller input, in bf16, fp16 and fp32;
+and a process whose first allocation-free call is made under HIP graph
+capture."""
 import math
+import os
+import subprocess
+import sys
+import textwrap
 
 import pytest
 import torch
@@ -72,3 +78,40 @@ def test_noalloc_ops_wrapper_matches():
     got = ops.gqa_decode_noalloc(q, k, v)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+_CAPTURE_FIRST_CALL = textwrap.dedent("""
+    import math, sys
+    import torch
+    sys.path.insert(0, {root!r})
+    from std_amd import ops
+    g = torch.Generator(device="cuda").manual_seed(21)
+    q = torch.randn(1, 28, 1, 128, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(1, 4, 8192, 128, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(1, 4, 8192, 128, generator=g, device="cuda").to(torch.bfloat16)
+    want = ops.gqa_decode(q, k, v)          # the same kernels, launched eagerly before the capture
+    torch.cuda.synchronize()
+    out = torch.full_like(q, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):           # the process's first allocation-free call, under capture
+        ops.gqa_decode_noalloc(q, k, v, out=out)
+    for i in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), "replay %d differs from the eager decode" % i
+        ops.gqa_decode(q[:, :, :, :].clone(), k, v)       # eager work between replays
+        torch.cuda.synchronize()
+    print("CAPTURE_FIRST_CALL_OK", flush=True)
+""")
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """A fresh process whose first std_gqa_decode_noalloc call is recorded
+    into a HIP graph (the scratch address lookup then runs during the
+    capture): every replay equals the eager workspace decode bit for bit."""
+    announce("noalloc decode: first call of a process under graph capture")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_FIRST_CALL.format(root=root)], capture_output=True,
+                         text=True, timeout=240)
+    assert res.returncode == 0 and "CAPTURE_FIRST_CALL_OK" in res.stdout, res.stdout[-2000:] + res.stderr[-4000:]
