@@ -40,11 +40,13 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c4", choices=["c2", "c3", "c4", "c5", "gemv", "stream"],
+    ap.add_argument("--workload", default="c4", choices=["c2", "c3", "c4", "c5", "gemv", "stream", "phases"],
                     help="c2-c4: attention hot path at 16k/64k/128k context (default c4, the headline); "
                          "c5: end-to-end STD vs dense AR decode on a random-init Qwen2.5-VL-7B-shaped decoder; "
                          "gemv: the decoder's weight-streaming projections at one and ten rows; "
-                         "stream: the HBM streaming-read ceiling in the attention kernels' access patterns")
+                         "stream: the HBM streaming-read ceiling in the attention kernels' access patterns; "
+                         "phases: per-phase timing of the c4 verify, dense decode and draft launches from the "
+                         "timing build (libstdhip_stamps.so)")
     ap.add_argument("--new-tokens", type=int, default=128, help="c5: tokens to decode")
     ap.add_argument("--eager", action="store_true",
                     help="c5: run the decode loops eagerly (host lengths) instead of replaying captured HIP graphs")
@@ -135,6 +137,9 @@ def main():
         return
     if args.workload == "gemv":
         run_gemv(args)
+        return
+    if args.workload == "phases":
+        run_phases(args)
         return
     if args.workload == "stream":
         run_stream(args)
@@ -710,6 +715,134 @@ def run_gemv(args) -> None:
                       "config": {"workload": "gemv: Qwen2.5-VL-7B projections (hidden 3584, SwiGLU 18944, vocab "
                                              "152064) at 1 and 10 rows"},
                       "results": results}))
+
+
+def _phase_summary(st, mt, n_wg, n_merge):
+    """Phases of one split launch and its merge launch from the timing build's
+    stamps (100 MHz ticks; see attention.hip): times in us from the first
+    workgroup's entry."""
+    import numpy as np
+
+    st = st.astype(np.int64).reshape(-1, 48)[:n_wg]
+    t0 = st[:, 0].min()
+    us = lambda x: (x - t0) / 100.0
+    ntl = st[:, 46]
+    entry = us(st[:, 0])
+    first = us(st[:, 2]) - entry
+    steps = np.array([(st[i, 2 + ntl[i] - 1] - st[i, 3]) / 100.0 / max(1, ntl[i] - 2) if ntl[i] > 2 else np.nan
+                      for i in range(n_wg)])
+    loop_end = us(st[:, 43])
+    end = us(np.maximum(st[:, 47], st[:, 45]))
+    r = {"workgroups": int(n_wg), "tiles_per_wg": [int(ntl.min()), int(ntl.max())],
+         "entry_spread": float(entry.max()), "first_tile_median": float(np.median(first)),
+         "first_tile_max": float(first.max()), "step_median": float(np.nanmedian(steps)) if n_wg and (ntl > 2).any()
+         else None, "loop_end_median": float(np.median(loop_end)), "output_stores_median": float(np.median(end - loop_end)),
+         "wg_end_min": float(end.min()), "wg_end_median": float(np.median(end)), "wg_end_max": float(end.max())}
+    if n_wg % 8 == 0 and (ntl > 2).any():
+        xcd = np.arange(n_wg) % 8            # workgroup i runs on XCD i % 8 (round-robin dispatch)
+        r["step_by_xcd"] = [float(np.nanmean(steps[xcd == x])) for x in range(8)]
+        r["wg_end_by_xcd"] = [float(end[xcd == x].mean()) for x in range(8)]
+    if n_merge:
+        mt = mt.astype(np.int64).reshape(-1, 2)[:n_merge]
+        r["merge_first_entry"] = float(us(mt[:, 0].min()))
+        r["gap_split_end_to_merge"] = float(us(mt[:, 0].min()) - end.max())
+        r["merge_span"] = float(us(mt[:, 1].max()) - us(mt[:, 0].min()))
+        r["merge_end"] = float(us(mt[:, 1].max()))
+    return r
+
+
+def run_phases(args) -> None:
+    """Per-phase timing of the c4 attention launches from the timing build of
+    the library (libstdhip_stamps.so: the same kernels with s_memrealtime
+    stamps at each workgroup's phases; build it with `python -m std_amd.build
+    --stamps`). Each case is 28 launches captured in one HIP graph, as in the
+    c4 bench; after each replay the stamps of its last launch are read. Prints
+    one JSON line per case (medians over replays, microseconds from the first
+    workgroup's entry) and one summary line."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from std_amd import _lib, build
+
+    if not build.STAMPS_LIB_PATH.exists():
+        raise SystemExit(f"{build.STAMPS_LIB_PATH} is missing: build it with `python -m std_amd.build --stamps`")
+    _lib.LIB_PATH = build.STAMPS_LIB_PATH
+    lib = _lib.load_library()
+    lib.std_phase_stamps.restype = ctypes.c_int
+    lib.std_phase_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+    from std_amd import ops
+
+    dev = torch.device("cuda:0")
+    L, D, Hq, Hkv, P, Q, S = 28, 128, 28, 4, 131072, 10, 1034
+    KV = P + Q
+    gen = torch.Generator(device=dev).manual_seed(4001)
+    kc = torch.randn(L, 1, Hkv, KV + 64, D, generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn(L, 1, Hkv, KV + 64, D, generator=gen, device=dev).to(torch.bfloat16)
+    qv = torch.randn(L, 1, Hq, Q, D, generator=gen, device=dev).to(torch.bfloat16)
+    qd = torch.randn(L, 1, Hq, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    sk = kc[:, :, :, 5000:5000 + S].contiguous()
+    sv = vc[:, :, :, 5000:5000 + S].contiguous()
+    vo, do = torch.empty_like(qv), torch.empty_like(qd)
+    def n_wg(rows, kv):
+        return lib.std_attn_split_count(Hkv, rows, kv, _lib.STD_BF16) * Hkv
+
+    # (launch of layer l, split workgroups, merge blocks)
+    cases = {
+        "verify": (lambda l: ops.verify_attention(qv[l], kc[l][:, :, :KV], vc[l][:, :, :KV], out=vo[l]),
+                   n_wg(7 * Q, KV), 7 * Q * Hkv),
+        "dense_decode": (lambda l: ops.gqa_decode(qd[l], kc[l][:, :, :P], vc[l][:, :, :P], out=do[l]), n_wg(7, P),
+                         7 * Hkv),
+        "draft": (lambda l: ops.gqa_decode(qd[l], sk[l], sv[l], out=do[l]), n_wg(7, S), 7 * Hkv),
+    }
+    stream = torch.cuda.current_stream()
+    out = {}
+    for name, (fn, n_wg, n_merge) in cases.items():
+        def body():
+            for l in range(L):
+                fn(l)
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            body()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            body()
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = []
+        for _ in range(max(8, args.steps // 2)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            st = np.zeros(2048 * 48, dtype=np.uint64)
+            mt = np.zeros(8192 * 2, dtype=np.uint64)
+            _lib.check("std_phase_stamps", lib.std_phase_stamps(st.ctypes.data, 0, st.size))
+            _lib.check("std_phase_stamps", lib.std_phase_stamps(mt.ctypes.data, 1, mt.size))
+            r = _phase_summary(st, mt, n_wg, n_merge if n_wg > Hkv else 0)
+            r["per_launch_us"] = e0.elapsed_time(e1) * 1e3 / L
+            reps.append(r)
+        med = {}
+        for key in reps[0]:
+            vals = [x[key] for x in reps]
+            if isinstance(vals[0], list) and isinstance(vals[0][0], float):
+                med[key] = [round(float(np.median([v[i] for v in vals])), 3) for i in range(len(vals[0]))]
+            elif isinstance(vals[0], float):
+                med[key] = round(float(np.median(vals)), 3)
+            else:
+                med[key] = vals[0]
+        out[name] = med
+        print(json.dumps({"case": name, **med}), flush=True)
+        del graph
+    print(json.dumps({"metric": "per-phase timing of the c4 attention launches (timing build)", "n_gpus": 1,
+                      "config": {"workload": "c4 shapes: verify 70 rows x 131082 keys, dense decode 7 rows x 131072 "
+                                             "keys, draft 7 rows x 1034 keys; 28 launches per graph"},
+                      "cases": sorted(out)}), flush=True)
 
 
 def run_stream(args) -> None:

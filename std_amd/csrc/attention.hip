@@ -40,8 +40,36 @@
 #include "common.h"
 #include "lds_dma.h"
 
+// Timing build (STD_PHASE_STAMPS=1, a separate library that the measurement
+// workload loads; the product library compiles none of this): each
+// workgroup of the 16-bit attention kernels records s_memrealtime (a 100 MHz
+// clock common to the whole chip) at its phases -- entry, first DMA issued,
+// every tile barrier, loop end, end of its output stores -- and each merge
+// block its entry and end.
+#ifndef STD_PHASE_STAMPS
+#define STD_PHASE_STAMPS 0
+#endif
+#if STD_PHASE_STAMPS
+constexpr int kStampSlots = 48, kStampWgs = 2048, kStampMerge = 8192;
+__device__ unsigned long long phase_stamps[kStampWgs * kStampSlots];
+__device__ unsigned long long merge_stamps[kStampMerge * 2];
+#endif
+
 namespace stdhip {
 namespace {
+
+// Slots of a workgroup's stamp row: 0 entry, 1 first tiles issued, 2 + u the
+// barrier of step u (u < 40), 43 compute loop done, 44/45 key-split waves'
+// output stores begin/end, 46 the tile count, 47 row owners' output stores end.
+__device__ __forceinline__ void stamp(int slot, unsigned long long v = 0) {
+#if STD_PHASE_STAMPS
+  const int wg = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  if (wg < kStampWgs) phase_stamps[wg * kStampSlots + slot] = v ? v : __builtin_amdgcn_s_memrealtime();
+#else
+  (void)slot;
+  (void)v;
+#endif
+}
 
 constexpr int D = kHeadDim;
 constexpr int TK = 64;              // keys per tile
@@ -354,7 +382,18 @@ template <typename T, typename PT>
 __global__ void __launch_bounds__(kMergeThreads)
 attn_merge_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
                   int n_split, int q_len, int group, long long out_bs, int n_kv) {
+#if STD_PHASE_STAMPS
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+#endif
   merge_row<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y);
+#if STD_PHASE_STAMPS
+  const int b = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  if (threadIdx.x == 0 && b < kStampMerge) {
+    __builtin_amdgcn_s_waitcnt(0);
+    merge_stamps[2 * b] = t0;
+    merge_stamps[2 * b + 1] = __builtin_amdgcn_s_memrealtime();
+  }
+#endif
 }
 
 // Where the collector's per-key sums go: the visual keys' scores in position
@@ -623,9 +662,15 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   constexpr bool kQLds = COLL;
   __shared__ __align__(16) char qs[kQLds ? 16 * NT * ROWB : 16];
 
+#if STD_PHASE_STAMPS
+  const unsigned long long t_entry = __builtin_amdgcn_s_memrealtime();
+#endif
   const int g = blockIdx.y, split = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+#if STD_PHASE_STAMPS
+  if (tid == 0) stamp(0, t_entry);
+#endif
   // Wave roles. Key split (KS, one row tile): every wave computes, on its own
   // 16 keys of each tile. Otherwise waves w < NT own one 16-row tile each
   // (row owners) and the rest only help issue the DMA ring -- except with
@@ -780,6 +825,9 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
   }
   if (ntiles > 0) issue(0, stage(0));
   if (ntiles > 1) issue(1, stage(1));
+#if STD_PHASE_STAMPS
+  if (tid == 0) stamp(1);
+#endif
   if constexpr (kQLds) {
     if (dma_wave) wait_vm_ahead<kLoads>(min(1, ntiles - 1));
     wg_barrier();
@@ -1124,6 +1172,9 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     if (u > ntiles) return;
     if (u < ntiles && dma_wave) wait_vm_ahead<kLoads>(u + 1 < ntiles ? 1 : 0);
     wg_barrier();
+#if STD_PHASE_STAMPS
+    if (tid == 0 && u < 40) stamp(2 + u);
+#endif
     if (u + 2 < ntiles) issue(u + 2, ahead2);
     if (computes) {
       if (u < ntiles) qk(cur, s_new);
@@ -1141,12 +1192,25 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     for (int u = 0; u < ntiles; ++u) {
       wait_vm_ahead<kLoads>(min(2, ntiles - 1 - u));
       wg_barrier();
+#if STD_PHASE_STAMPS
+      if (tid == 0 && u < 40) stamp(2 + u);
+#endif
       if (u + 3 < ntiles) issue(u + 3, stage(u + 3));
       ks_tile(u, stage(u));
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();                             // the ring is free: reuse it for the merge
+#if STD_PHASE_STAMPS
+    if (tid == 0) stamp(43);
+#endif
     ks_merge(ring, 0, C::kThreads, tid);
+#if STD_PHASE_STAMPS
+    if (tid == 0) {
+      __builtin_amdgcn_s_waitcnt(0);
+      stamp(47);
+      stamp(46, (unsigned long long)ntiles);
+    }
+#endif
     return;
   } else {
     for (int u = 0; u <= ntiles; u += 2) {
@@ -1188,10 +1252,25 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
           ga.stats[((long long)g * n_split + split) * q_len + t] = make_float2(M, L);
         }
       }
+#if STD_PHASE_STAMPS
+      if (tid == 64 * kOwners) stamp(44);
+#endif
       ks_merge_rows(region, 16 * kOwners, C::kThreads - 64 * kOwners, tid - 64 * kOwners);
+#if STD_PHASE_STAMPS
+      if (tid == 64 * kOwners) {
+        __builtin_amdgcn_s_waitcnt(0);
+        stamp(45);
+      }
+#endif
       return;
     }
   }
+#if STD_PHASE_STAMPS
+  if (tid == 0) {
+    stamp(43);
+    stamp(46, (unsigned long long)ntiles);
+  }
+#endif
   if (!row_ok) return;
 
   // Complete rows: normalised output (one split) or the (m, l, O) partial.
@@ -1224,6 +1303,12 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       *reinterpret_cast<half4_t*>(ws_o + prow * D + 16 * t + 4 * lg) = __builtin_convertvector(acc[t] * sx, half4_t);
     if (lg == 0) ws_ml[prow] = make_float2(m_run + (float)kx, l_row * sx);
   }
+#if STD_PHASE_STAMPS
+  if (tid == 0) {
+    __builtin_amdgcn_s_waitcnt(0);
+    stamp(47);
+  }
+#endif
 }
 
 // ===========================================================================
@@ -1927,3 +2012,15 @@ extern "C" int std_verify_attn_collect_ex(const void* q, void* k_cache, void* v_
                               vis_end, vis_mask, vis_rank, n_visual, scores, scores_head_stride, workspace,
                               workspace_bytes, stream);
 }
+
+#if STD_PHASE_STAMPS
+// Timing build only: copies the stamp rows (which = 0, n words) or the merge
+// stamps (which = 1) to host memory.
+extern "C" int std_phase_stamps(void* host, int which, size_t n) {
+  if (which == 0)
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(phase_stamps),
+                                    std::min(n, (size_t)kStampWgs * kStampSlots) * 8, 0, hipMemcpyDeviceToHost);
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(merge_stamps), std::min(n, (size_t)kStampMerge * 2) * 8, 0,
+                                  hipMemcpyDeviceToHost);
+}
+#endif
