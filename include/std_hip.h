@@ -53,6 +53,19 @@ enum {
   STD_E_RANGE = -6        /* length or index past the cache capacity */
 };
 
+/* Device status word. The device-length entry points (std_kv_append,
+ * std_rope_append, std_qkv_rope_append, std_attn_devlen,
+ * std_gqa_decode_indexed with a device length, std_verify_attn_collect_ex
+ * with a device length) take an optional int32_t* status in device memory.
+ * Where the device length places a row, or the attended keys, past the cache
+ * capacity, the kernel leaves that memory alone (rows past the capacity are
+ * not written; an attention with an out-of-range length reads nothing and
+ * writes NaN outputs) and ORs STD_STATUS_CACHE_OVERFLOW into *status, so
+ * that a step replayed from a graph reports it with its next readback (the
+ * reference's KVCache.cat raises instead, kv_cache.py:54-69). The word is
+ * never cleared by the library. */
+enum { STD_STATUS_CACHE_OVERFLOW = 1 };
+
 /* Human-readable text for a status code (static storage). */
 const char* std_status_string(int status);
 
@@ -261,7 +274,7 @@ int std_compact_kv(const void* dense_k, const void* dense_v, void* sparse_k, voi
 int std_kv_append(void* cache_k, void* cache_v, const void* new_k, const void* new_v,
                   int n_kv, int rows, int d,
                   long long cache_head_stride, long long new_head_stride, long long new_row_stride,
-                  int capacity, const int32_t* len_dev, int dtype, void* stream);
+                  int capacity, const int32_t* len_dev, int dtype, int32_t* status, void* stream);
 
 /* len[i] += delta for i < n (device int32). */
 int std_len_add(int32_t* len_dev, int n, int delta, void* stream);
@@ -288,7 +301,7 @@ int std_len_add(int32_t* len_dev, int n, int delta, void* stream);
 int std_rope_append(const void* qkv, long long qkv_row_stride, void* q_out, void* cache_k, void* cache_v,
                     int n_rows, int n_q, int n_kv, int d, long long cache_head_stride, int capacity,
                     const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
-                    const float* inv_freq, int dtype, void* stream);
+                    const float* inv_freq, int dtype, int32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------
  * Offset-causal GQA attention at a device length (decode when q_len == 1).
@@ -306,7 +319,7 @@ int std_rope_append(const void* qkv, long long qkv_row_stride, void* q_out, void
 int std_attn_devlen(const void* q, const void* k_cache, const void* v_cache, void* out,
                     int n_q, int n_kv, int q_len, const int32_t* len_dev, int max_kv_len, int d,
                     long long k_head_stride, long long v_head_stride, float scale, int dtype,
-                    void* workspace, size_t workspace_bytes, void* stream);
+                    void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sparse draft decode with index-addressed prompt keys (no compaction copy).
@@ -335,7 +348,7 @@ int std_gqa_decode_indexed(const void* q, const void* dense_k, const void* dense
                            const void* k_cache, const void* v_cache, long long k_head_stride,
                            long long v_head_stride, void* out, int n_q, int n_kv, int kv_len,
                            const int32_t* len_dev, int d, float scale, int dtype, void* workspace,
-                           size_t workspace_bytes, void* stream);
+                           size_t workspace_bytes, int32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------
  * Greedy acceptance plus cache rollback on the device.
@@ -437,7 +450,8 @@ int std_qkv_rope_append(const void* x, long long x_row_stride, int n_rows, int K
                         long long w_row_stride, const void* bias, int n_q, int n_kv, int d, void* q_out,
                         void* cache_k, void* cache_v, long long cache_head_stride, int capacity,
                         const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
-                        const float* inv_freq, const void* norm_weight, float eps, int dtype, void* stream);
+                        const float* inv_freq, const void* norm_weight, float eps, int dtype,
+                        int32_t* status, void* stream);
 
 int std_greedy_accept(const void* logits, long long logits_row_stride, int q_rows, int vocab,
                       int dtype, const int32_t* draft, int n_draft, int has_pending,
@@ -501,7 +515,7 @@ int std_verify_attn_collect_ex(const void* q, void* k_cache, void* v_cache,
                                float scale, int dtype, int vis_begin, int vis_end,
                                const uint32_t* vis_mask, const int32_t* vis_rank, int n_visual,
                                float* scores, long long scores_head_stride,
-                               void* workspace, size_t workspace_bytes, void* stream);
+                               void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------
  * Streaming-read ceiling (measurement helper; no counterpart in the

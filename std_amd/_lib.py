@@ -17,6 +17,8 @@ STD_F32 = 0
 STD_BF16 = 1
 STD_F16 = 2
 
+STD_STATUS_CACHE_OVERFLOW = 1    # device status word bit: a row or length past the cache capacity
+
 STATUS_NAMES = {
     -1: "STD_E_NULL",
     -2: "STD_E_DTYPE",
@@ -56,7 +58,7 @@ SIGNATURES = {
     "std_verify_attn_collect_ex": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                            c_int, c_int, c_void_p, c_int, c_longlong, c_longlong, c_longlong,
                                            c_longlong, c_float, c_int, c_int, c_int, c_void_p, c_void_p, c_int,
-                                           c_void_p, c_longlong, c_void_p, c_size_t, c_void_p]),
+                                           c_void_p, c_longlong, c_void_p, c_size_t, c_void_p, c_void_p]),
     "std_select_topk_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "std_select_topk": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_longlong, c_int,
                                 c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
@@ -67,12 +69,12 @@ SIGNATURES = {
     "std_compact_kv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                c_longlong, c_int, c_longlong, c_int, c_int, c_void_p]),
     "std_kv_append": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_longlong,
-                              c_longlong, c_longlong, c_int, c_void_p, c_int, c_void_p]),
+                              c_longlong, c_longlong, c_int, c_void_p, c_int, c_void_p, c_void_p]),
     "std_len_add": (c_int, [c_void_p, c_int, c_int, c_void_p]),
     "std_gqa_decode_indexed": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_longlong, c_longlong, c_void_p,
                                        c_longlong, c_int, c_void_p, c_void_p, c_longlong, c_longlong, c_void_p,
                                        c_int, c_int, c_int, c_void_p, c_int, c_float, c_int, c_void_p, c_size_t,
-                                       c_void_p]),
+                                       c_void_p, c_void_p]),
     "std_gemv_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "std_gemv": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_int, c_int,
                          c_int, c_int, c_void_p, c_size_t, c_void_p]),
@@ -80,14 +82,14 @@ SIGNATURES = {
                             c_longlong, c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "std_qkv_rope_append": (c_int, [c_void_p, c_longlong, c_int, c_int, c_void_p, c_longlong, c_void_p, c_int, c_int,
                                     c_int, c_void_p, c_void_p, c_void_p, c_longlong, c_int, c_void_p, c_void_p, c_int,
-                                    c_void_p, c_void_p, c_float, c_int, c_void_p]),
+                                    c_void_p, c_void_p, c_float, c_int, c_void_p, c_void_p]),
     "std_argmax_rows": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "std_rms_norm": (c_int, [c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_int, c_int, c_float, c_int,
                              c_void_p]),
     "std_rope_append": (c_int, [c_void_p, c_longlong, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
-                                c_longlong, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p]),
+                                c_longlong, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p]),
     "std_attn_devlen": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_int,
-                                c_longlong, c_longlong, c_float, c_int, c_void_p, c_size_t, c_void_p]),
+                                c_longlong, c_longlong, c_float, c_int, c_void_p, c_size_t, c_void_p, c_void_p]),
     "std_greedy_accept_workspace_bytes": (c_size_t, [c_int, c_int]),
     "std_stream_read": (c_int, [c_void_p, c_size_t, c_int, c_int, c_void_p, c_void_p]),
     "std_greedy_accept": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_int, c_int, c_void_p,

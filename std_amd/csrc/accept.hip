@@ -181,14 +181,17 @@ rms_norm_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __restrict_
 __global__ void __launch_bounds__(256)
 kv_append_kernel(char* __restrict__ ck, char* __restrict__ cv, const char* __restrict__ nk,
                  const char* __restrict__ nv, int rows, int row_bytes, long long chs_bytes, long long nhs_bytes,
-                 long long nrs_bytes, int capacity, const int32_t* __restrict__ len_dev) {
+                 long long nrs_bytes, int capacity, const int32_t* __restrict__ len_dev, int32_t* status) {
   const int g = blockIdx.y, kv = blockIdx.z;
   const int cpr = row_bytes / 16;
   const int c = blockIdx.x * 256 + threadIdx.x;
   const int s = c / cpr, col = c - s * cpr;
   if (s >= rows) return;
   const int pos = *len_dev + s;
-  if (pos < 0 || pos >= capacity) return;
+  if (pos < 0 || pos >= capacity) {                     // not written: marks the status word
+    if (g == 0 && kv == 0 && col == 0) flag_overflow(status);
+    return;
+  }
   const char* src = (kv ? nv : nk) + g * nhs_bytes + s * nrs_bytes + col * 16;
   char* dst = (kv ? cv : ck) + g * chs_bytes + (long long)pos * row_bytes + col * 16;
   *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
@@ -261,7 +264,7 @@ extern "C" int std_greedy_accept(const void* logits, long long logits_row_stride
 
 extern "C" int std_kv_append(void* cache_k, void* cache_v, const void* new_k, const void* new_v, int n_kv, int rows,
                              int d, long long cache_head_stride, long long new_head_stride, long long new_row_stride,
-                             int capacity, const int32_t* len_dev, int dtype, void* stream) {
+                             int capacity, const int32_t* len_dev, int dtype, int32_t* status, void* stream) {
   if (!cache_k || !cache_v || !new_k || !new_v || !len_dev) return STD_E_NULL;
   if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_kv < 1 || rows < 1 || capacity < 1) return STD_E_SHAPE;
@@ -272,7 +275,7 @@ extern "C" int std_kv_append(void* cache_k, void* cache_v, const void* new_k, co
   hipLaunchKernelGGL(kv_append_kernel, dim3((rows * cpr + 255) / 256, n_kv, 2), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<char*>(cache_k), static_cast<char*>(cache_v),
                      static_cast<const char*>(new_k), static_cast<const char*>(new_v), rows, row_bytes,
-                     cache_head_stride * es, new_head_stride * es, new_row_stride * es, capacity, len_dev);
+                     cache_head_stride * es, new_head_stride * es, new_row_stride * es, capacity, len_dev, status);
   return launch_status();
 }
 

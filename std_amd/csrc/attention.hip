@@ -132,9 +132,26 @@ struct BatchStrides {
 // idx[g * idx_hs + j] of the dense cache (k, v with head strides k_hs, v_hs
 // and dense_rows rows per head; an index outside [0, dense_rows) is clamped),
 // keys j >= n_idx are rows j of the launch's own cache, as without indices.
-// idx == nullptr: no gather.
+// idx == nullptr: no gather. status: the optional device status word that a
+// device length outside the launch's range marks (host side; the kernels
+// receive GatherDev, with the index array as a separate argument).
 struct GatherArgs {
   const int32_t* idx;
+  long long idx_hs;
+  int n_idx;
+  int dense_rows;
+  const bf16_t* k;
+  const bf16_t* v;
+  long long k_hs, v_hs;
+  int32_t* status;
+};
+
+// The kernel-side auxiliary arguments of the non-collector kernels: the
+// status word and GatherArgs' index parameters (same size as the index
+// pointer it replaces: the argument block of these latency-bound launches
+// stays at 248 bytes).
+struct GatherDev {
+  int32_t* status;
   long long idx_hs;
   int n_idx;
   int dense_rows;
@@ -162,10 +179,11 @@ struct CollArgs {
   int vis_begin, vis_end;
   const uint32_t* vmask;
   int len_off;
+  int32_t* status;
 };
 
 template <bool COLL>
-using AuxArgs = typename std::conditional<COLL, CollArgs, GatherArgs>::type;
+using AuxArgs = typename std::conditional<COLL, CollArgs, GatherDev>::type;
 
 struct WsLayout {
   size_t o_off, ml_off, total;
@@ -702,6 +720,7 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
       device_length(len_dev, q_len, kv_len, ntiles_total, causal_off, ga.len_off);
     else
       device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
+    if (kv_len == 0 && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) flag_overflow(ga.status);
   }
   const int ntiles = split_ntiles(split, ntiles_total, n_split);
   bf16_t* kh = kc + (long long)g * k_hs;
@@ -1367,7 +1386,8 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
                 float* __restrict__ out, float* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
                 int kv_len, int group, long long k_hs, long long v_hs, float scale_log2, int ntiles_total,
                 int n_split, int causal_off, const float* __restrict__ new_k, const float* __restrict__ new_v,
-                long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev) {
+                long long n_hs, long long n_rs, int n_new, BatchStrides bs, const int32_t* __restrict__ len_dev,
+                int32_t* status) {
   using F = F32Frag;
   using S = F32Smem<NT>;
   constexpr int CPR = D / 4;                    // 16-byte chunks per fp32 row
@@ -1391,7 +1411,10 @@ attn_f32_kernel(const float* __restrict__ q, float* __restrict__ kc, float* __re
       ws_ml += b * bs.w;
     }
   }
-  if (len_dev != nullptr) device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
+  if (len_dev != nullptr) {
+    device_length(len_dev, q_len, kv_len, ntiles_total, causal_off);
+    if (kv_len == 0 && threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) flag_overflow(status);
+  }
   const int ntiles = split_ntiles(split, ntiles_total, n_split);
   float* kh = kc + (long long)g * k_hs;
   float* vh = vc + (long long)g * v_hs;
@@ -1568,7 +1591,8 @@ void launch_h16(const void* q, void* k, void* v, void* out, int q_len, int kv_le
                      static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                      static_cast<bf16_t*>(out), static_cast<PartT<NT, E>*>(ws_o), ws_ml, q_len, kv_len, group, k_hs,
                      v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len, static_cast<const bf16_t*>(nk),
-                     static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev, ga, ga.idx);
+                     static_cast<const bf16_t*>(nv), n_hs, n_rs, n_new, bs, len_dev,
+                     GatherDev{ga.status, ga.idx_hs, ga.n_idx, ga.dense_rows, ga.k, ga.v, ga.k_hs, ga.v_hs}, ga.idx);
 }
 
 template <int NT>
@@ -1597,7 +1621,8 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
                        static_cast<float*>(k), static_cast<float*>(v), static_cast<float*>(out),
                        static_cast<float*>(ws_o), ws_ml, q_len,
                        kv_len, group, k_hs, v_hs, scale_log2, p.ntiles, p.n_split, kv_len - q_len,
-                       static_cast<const float*>(nk), static_cast<const float*>(nv), n_hs, n_rs, n_new, bs, len_dev);
+                       static_cast<const float*>(nk), static_cast<const float*>(nv), n_hs, n_rs, n_new, bs, len_dev,
+                       ga.status);
   }
   int s = launch_status();
   if (s != 0 || p.n_split == 1) return s;
@@ -1643,7 +1668,7 @@ int attn_entry(const void* q, void* k, void* v, void* out, int n_q, int n_kv, in
                long long k_hs, long long v_hs, float scale, int dtype, void* ws, size_t ws_bytes, const void* nk,
                const void* nv, long long n_hs, long long n_rs, int n_new, void* stream, int n_batch = 1,
                BatchStrides bs = BatchStrides{0, 0, 0, 0}, const int32_t* len_dev = nullptr,
-               GatherArgs ga = GatherArgs{nullptr, 0, 0, 0, nullptr, nullptr, 0, 0}) {
+               GatherArgs ga = GatherArgs{nullptr, 0, 0, 0, nullptr, nullptr, 0, 0, nullptr}) {
   if (!q || !k || !v || !out) return STD_E_NULL;
   if (ga.idx != nullptr) {
     // Gathered keys: one bf16 decode problem; indices padded to 16 per row of
@@ -1734,7 +1759,7 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
                          const int32_t* len_dev, int d, long long k_hs, long long v_hs, float scale, int dtype,
                          const void* nk, const void* nv, long long n_hs, long long n_rs, int vis_begin, int vis_end,
                          const uint32_t* vmask, const int32_t* vrank, int n_visual, float* scores, long long score_hs,
-                         void* ws, size_t ws_bytes, void* stream) {
+                         void* ws, size_t ws_bytes, int32_t* status, void* stream) {
   if (!q || !k || !v || !out || !scores) return STD_E_NULL;
   if ((nk == nullptr) != (nv == nullptr)) return STD_E_NULL;
   if ((vmask == nullptr) != (vrank == nullptr)) return STD_E_NULL;
@@ -1767,7 +1792,7 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
     void* ws_o = p.n_split > 1 ? static_cast<void*>(base + wl.o_off) : nullptr;
     float2* ws_ml = p.n_split > 1 ? reinterpret_cast<float2*>(base + wl.ml_off) : nullptr;
     const CollArgs ca{reinterpret_cast<float*>(base + cl.logits_off), reinterpret_cast<float2*>(base + cl.stats_off),
-                      cl.n_vtiles, vis_begin, vis_end, vmask, a};
+                      cl.n_vtiles, vis_begin, vis_end, vmask, a, status};
     const CollOut co{scores, n_kv > 1 ? score_hs : 0LL, vmask, vrank, n_visual, len_dev, a, a > 0 ? 1 : 0};
     const void* qa = q;
     void* oa = out;
@@ -1938,11 +1963,12 @@ extern "C" int std_verify_attn_append(const void* q, void* k_cache, void* v_cach
 extern "C" int std_attn_devlen(const void* q, const void* k_cache, const void* v_cache, void* out, int n_q, int n_kv,
                                int q_len, const int32_t* len_dev, int max_kv_len, int d, long long k_head_stride,
                                long long v_head_stride, float scale, int dtype, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+                               size_t workspace_bytes, int32_t* status, void* stream) {
   if (!len_dev) return STD_E_NULL;
   return attn_entry(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), out, n_q, n_kv, q_len, max_kv_len, d,
                     k_head_stride, v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0, 0,
-                    stream, 1, BatchStrides{0, 0, 0, 0}, len_dev);
+                    stream, 1, BatchStrides{0, 0, 0, 0}, len_dev,
+                    GatherArgs{nullptr, 0, 0, 0, nullptr, nullptr, 0, 0, status});
 }
 
 extern "C" int std_gqa_decode_indexed(const void* q, const void* dense_k, const void* dense_v, int dense_rows,
@@ -1951,10 +1977,10 @@ extern "C" int std_gqa_decode_indexed(const void* q, const void* dense_k, const 
                                       const void* k_cache, const void* v_cache, long long k_head_stride,
                                       long long v_head_stride, void* out, int n_q, int n_kv, int kv_len,
                                       const int32_t* len_dev, int d, float scale, int dtype, void* workspace,
-                                      size_t workspace_bytes, void* stream) {
+                                      size_t workspace_bytes, int32_t* status, void* stream) {
   if (!index) return STD_E_NULL;
   const GatherArgs ga{index, index_head_stride, n_index, dense_rows, static_cast<const bf16_t*>(dense_k),
-                      static_cast<const bf16_t*>(dense_v), dense_k_head_stride, dense_v_head_stride};
+                      static_cast<const bf16_t*>(dense_v), dense_k_head_stride, dense_v_head_stride, status};
   return attn_entry(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), out, n_q, n_kv, 1, kv_len, d,
                     k_head_stride, v_head_stride, scale, dtype, workspace, workspace_bytes, nullptr, nullptr, 0, 0,
                     0, stream, 1, BatchStrides{0, 0, 0, 0}, len_dev, ga);
@@ -1996,7 +2022,7 @@ extern "C" int std_verify_attn_collect(const void* q, void* k_cache, void* v_cac
   return verify_collect_entry(q, k_cache, v_cache, out, n_q, n_kv, q_len, kv_len, nullptr, d, k_head_stride,
                               v_head_stride, scale, dtype, new_k, new_v, new_head_stride, new_row_stride, vis_begin,
                               vis_end, nullptr, nullptr, vis_end - vis_begin, scores, scores_head_stride, workspace,
-                              workspace_bytes, stream);
+                              workspace_bytes, nullptr, stream);
 }
 
 extern "C" int std_verify_attn_collect_ex(const void* q, void* k_cache, void* v_cache, const void* new_k,
@@ -2006,11 +2032,11 @@ extern "C" int std_verify_attn_collect_ex(const void* q, void* k_cache, void* v_
                                           long long new_row_stride, float scale, int dtype, int vis_begin,
                                           int vis_end, const uint32_t* vis_mask, const int32_t* vis_rank,
                                           int n_visual, float* scores, long long scores_head_stride, void* workspace,
-                                          size_t workspace_bytes, void* stream) {
+                                          size_t workspace_bytes, int32_t* status, void* stream) {
   return verify_collect_entry(q, k_cache, v_cache, out, n_q, n_kv, q_len, kv_len, len_dev, d, k_head_stride,
                               v_head_stride, scale, dtype, new_k, new_v, new_head_stride, new_row_stride, vis_begin,
                               vis_end, vis_mask, vis_rank, n_visual, scores, scores_head_stride, workspace,
-                              workspace_bytes, stream);
+                              workspace_bytes, status, stream);
 }
 
 #if STD_PHASE_STAMPS

@@ -96,6 +96,13 @@ __device__ __forceinline__ T rms_scale(T x, T weight, float inv) {
   return from_f32<T>(__fmul_rn(to_f32<T>(weight), n));
 }
 
+// Marks the device status word (optional) with a cache overflow; called by
+// one thread per detection. A vector atomic, so concurrent markers need no
+// ordering among themselves.
+__device__ __forceinline__ void flag_overflow(int32_t* status) {
+  if (status != nullptr) atomicOr(status, (int32_t)STD_STATUS_CACHE_OVERFLOW);
+}
+
 // Status of the most recent launch on this thread (0 or a positive hipError_t).
 inline int launch_status() {
   hipError_t e = hipGetLastError();

@@ -300,7 +300,8 @@ namespace {
 // inv_freq[j], cos / sin rounded to bf16, lo = x1 c - x2 s and hi = x2 c + x1 s
 // with each product and the sum rounded. Query heads go to q_out
 // [n_q][M][128]; key heads, rotated, and value heads, as projected, go to cache
-// row len + m of their KV head (rows at or past the capacity are not written).
+// row len + m of their KV head (rows at or past the capacity are not written;
+// they mark the status word).
 //
 // NORM (one row, K <= kQkvNormMaxK): x is the layer's input before its
 // RMSNorm (weight nw): the workgroup forms the row statistic in the order of
@@ -316,6 +317,7 @@ struct RopeArgs {
   bf16_t* cv;
   long long chs;                  // cache head stride (elements)
   int n_q, n_kv, capacity, pos_offset;
+  int32_t* status;                // optional device status word (cache overflow)
 };
 
 template <bool NORM>
@@ -392,7 +394,10 @@ gemv_qkv_rope_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t*
     dst = ra.q_out + ((long long)head * M + ln) * kHeadDim;
   } else {
     const int crow = *len_dev + ln;
-    if (crow < 0 || crow >= ra.capacity) return;
+    if (crow < 0 || crow >= ra.capacity) {            // not written: marks the status word
+      flag_overflow(ra.status);
+      return;
+    }
     dst = (kv_head < ra.n_kv ? ra.ck + (long long)kv_head * ra.chs : ra.cv + (long long)(kv_head - ra.n_kv) * ra.chs) +
           (long long)crow * kHeadDim;
   }
@@ -498,7 +503,7 @@ extern "C" int std_qkv_rope_append(const void* x, long long x_row_stride, int n_
                                    void* cache_k, void* cache_v, long long cache_head_stride, int capacity,
                                    const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
                                    const float* inv_freq, const void* norm_weight, float eps, int dtype,
-                                   void* stream) {
+                                   int32_t* status, void* stream) {
   if (!x || !w || !q_out || !cache_k || !cache_v || !len_dev || !pos_dev || !inv_freq) return STD_E_NULL;
   if (norm_weight && (n_rows != 1 || K > kQkvNormMaxK)) return STD_E_SHAPE;
   if (dtype != STD_BF16) return STD_E_DTYPE;
@@ -509,7 +514,7 @@ extern "C" int std_qkv_rope_append(const void* x, long long x_row_stride, int n_
   if (!aligned16(x) || !aligned16(w) || (x_row_stride * 2) % 16 || (w_row_stride * 2) % 16) return STD_E_ALIGN;
   static_assert((kShortMaxK / 4) / 32 <= kShortSteps, "four waves cover K in kShortSteps steps each");
   const RopeArgs ra{static_cast<bf16_t*>(q_out), static_cast<bf16_t*>(cache_k), static_cast<bf16_t*>(cache_v),
-                    cache_head_stride, n_q, n_kv, capacity, pos_offset};
+                    cache_head_stride, n_q, n_kv, capacity, pos_offset, status};
   auto kern = norm_weight ? gemv_qkv_rope_kernel<true> : gemv_qkv_rope_kernel<false>;
   hipLaunchKernelGGL(kern, dim3((n_q + 2 * n_kv) * 16), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const bf16_t*>(w), w_row_stride, static_cast<const bf16_t*>(x), x_row_stride,

@@ -22,13 +22,14 @@ __device__ __forceinline__ float rnd(float x) { return to_f32<T>(from_f32<T>(x))
 // grid (n_rows, n_q + n_kv), block HALF: thread j rotates the pair (j, j + 64)
 // of one head of one row. Query heads go to q_out [n_q][n_rows][D]; key heads
 // are rotated into the cache row len + row, and the matching value row is
-// copied there. Rows at or past the capacity are not written.
+// copied there. Rows at or past the capacity are not written; they mark the
+// status word.
 template <typename T>
 __global__ void __launch_bounds__(HALF)
 rope_append_kernel(const T* __restrict__ qkv, long long qkv_rs, T* __restrict__ q_out, T* __restrict__ ck,
                    T* __restrict__ cv, int n_rows, int n_q, int n_kv, long long chs, int capacity,
                    const int32_t* __restrict__ len_dev, const int32_t* __restrict__ pos_dev, int pos_offset,
-                   const float* __restrict__ inv_freq) {
+                   const float* __restrict__ inv_freq, int32_t* status) {
   // Every product is rounded to the dtype before the sum, as torch evaluates
   // it: plain operators (round to nearest even) with multiply-add
   // contraction off -- for fp16 the compiler would otherwise fuse x * cos
@@ -50,7 +51,10 @@ rope_append_kernel(const T* __restrict__ qkv, long long qkv_rs, T* __restrict__ 
   }
   const int g = head - n_q;
   const int crow = *len_dev + row;
-  if (crow < 0 || crow >= capacity) return;
+  if (crow < 0 || crow >= capacity) {
+    if (g == 0 && j == 0) flag_overflow(status);
+    return;
+  }
   T* kd = ck + (long long)g * chs + (long long)crow * D;
   kd[j] = from_f32<T>(lo);
   kd[j + HALF] = from_f32<T>(hi);
@@ -68,7 +72,7 @@ using namespace stdhip;
 extern "C" int std_rope_append(const void* qkv, long long qkv_row_stride, void* q_out, void* cache_k, void* cache_v,
                                int n_rows, int n_q, int n_kv, int d, long long cache_head_stride, int capacity,
                                const int32_t* len_dev, const int32_t* pos_dev, int pos_offset,
-                               const float* inv_freq, int dtype, void* stream) {
+                               const float* inv_freq, int dtype, int32_t* status, void* stream) {
   if (!qkv || !q_out || !cache_k || !cache_v || !len_dev || !pos_dev || !inv_freq) return STD_E_NULL;
   if (dtype != STD_F32 && dtype != STD_BF16 && dtype != STD_F16) return STD_E_DTYPE;
   if (d != D || n_rows < 1 || n_rows > 65535 || n_q < 1 || n_kv < 1 || n_q % n_kv != 0 || capacity < 1)
@@ -81,16 +85,16 @@ extern "C" int std_rope_append(const void* qkv, long long qkv_row_stride, void* 
     hipLaunchKernelGGL(rope_append_kernel<bf16_t>, grid, dim3(HALF), 0, st, static_cast<const bf16_t*>(qkv),
                        qkv_row_stride, static_cast<bf16_t*>(q_out), static_cast<bf16_t*>(cache_k),
                        static_cast<bf16_t*>(cache_v), n_rows, n_q, n_kv, cache_head_stride, capacity, len_dev, pos_dev,
-                       pos_offset, inv_freq);
+                       pos_offset, inv_freq, status);
   else if (dtype == STD_F16)
     hipLaunchKernelGGL(rope_append_kernel<f16_t>, grid, dim3(HALF), 0, st, static_cast<const f16_t*>(qkv),
                        qkv_row_stride, static_cast<f16_t*>(q_out), static_cast<f16_t*>(cache_k),
                        static_cast<f16_t*>(cache_v), n_rows, n_q, n_kv, cache_head_stride, capacity, len_dev, pos_dev,
-                       pos_offset, inv_freq);
+                       pos_offset, inv_freq, status);
   else
     hipLaunchKernelGGL(rope_append_kernel<float>, grid, dim3(HALF), 0, st, static_cast<const float*>(qkv),
                        qkv_row_stride, static_cast<float*>(q_out), static_cast<float*>(cache_k),
                        static_cast<float*>(cache_v), n_rows, n_q, n_kv, cache_head_stride, capacity, len_dev, pos_dev,
-                       pos_offset, inv_freq);
+                       pos_offset, inv_freq, status);
   return launch_status();
 }

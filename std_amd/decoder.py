@@ -114,6 +114,12 @@ class RandomDecoder:
         self.verify_collector = None      # set by VerificationCollectorV3.install()
         self.capture_text_queries = False
         self.captured_queries: List[Optional[torch.Tensor]] = [None] * c.num_hidden_layers
+        # Device status word of the decode steps: the appends and attention
+        # launches OR ops' cache-overflow bit into it when a device length would
+        # place a row, or the attended keys, past a cache's capacity (nothing is
+        # written there). The generate loops clear it and read it back with
+        # each round.
+        self.decode_status = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     # -- pieces ---------------------------------------------------------------
     def _hip_rows(self, x: torch.Tensor, max_rows: int) -> bool:
@@ -202,17 +208,18 @@ class RandomDecoder:
         if self.fused_rows(n) and self._hip_rows(x, 1) and width <= ops.QKV_ROPE_NORM_MAX_K:
             # one bf16 row: the norm, projection, rotary embedding and K/V append in one launch
             q = ops.qkv_rope_append(x, p["qkv_w"], p["qkv_b"], hq, kc.data, vc.data, state[0:1], state[1:2],
-                                    self.inv_freq, norm_weight=p["ln1"], eps=c.rms_norm_eps)
+                                    self.inv_freq, norm_weight=p["ln1"], eps=c.rms_norm_eps, status=self.decode_status)
         else:
             h = self._rms_norm(x, p["ln1"])
             if self.fused_rows(n) and self._hip_rows(h, 1) and width <= ops.QKV_ROPE_MAX_K:
                 q = ops.qkv_rope_append(h, p["qkv_w"], p["qkv_b"], hq, kc.data, vc.data, state[0:1], state[1:2],
-                                        self.inv_freq)
+                                        self.inv_freq, status=self.decode_status)
             else:
                 qkv = self._linear(h, p["qkv_w"], p["qkv_b"])                # [1, n, (hq + 2hkv) d]
         if self.fused_rows(n):
             if qkv is not None:
-                q = ops.rope_append(qkv, hq, kc.data, vc.data, state[0:1], state[1:2], self.inv_freq)
+                q = ops.rope_append(qkv, hq, kc.data, vc.data, state[0:1], state[1:2], self.inv_freq,
+                                    status=self.decode_status)
             if self.capture_text_queries:
                 self.captured_queries[li] = q
             gather = controller.gather_for(li) if controller is not None and controller.enabled else None
@@ -222,14 +229,15 @@ class RandomDecoder:
                 # (planned for the cache capacity, as attention_devlen: the same attention rows)
                 out, _ = ops.verify_attention_collect(q, kc.data, vc.data, visual=collector.visual,
                                                       kv_len=kc.capacity, length=state[0:1],
-                                                      scores=collector.scores_out(li))
+                                                      scores=collector.scores_out(li), status=self.decode_status)
                 collector.record(li)
             elif gather is not None:      # index-addressed sparse cache: prompt keys read from the dense cache
                 dk, dv, index, n_index = gather
                 out = ops.gqa_decode_indexed(q, dk, dv, index, n_index, kc.data, vc.data, length=state[0:1],
-                                             max_kv_len=kc.capacity)
+                                             max_kv_len=kc.capacity, status=self.decode_status)
             else:
-                out = ops.attention_devlen(q, kc.data, vc.data, state[0:1], max_kv_len=kc.capacity)
+                out = ops.attention_devlen(q, kc.data, vc.data, state[0:1], max_kv_len=kc.capacity,
+                                           status=self.decode_status)
             if host_lengths:
                 kc.advance(n)
                 vc.advance(n)
@@ -245,6 +253,14 @@ class RandomDecoder:
         if not host_lengths:
             raise ValueError("a device-state step must have at most 96 query rows per KV head")
         out = self._prefill_attention(q, k, v, kc, vc)
+        collector = self.verify_collector
+        if collector is not None and collector.collecting and n > 1 and q.dtype in (torch.bfloat16, torch.float16):
+            # a verify longer than the fused launches serve (more than 96 query rows per KV head): the
+            # collector's scores from its own launch over the cache these rows were just appended to (in
+            # chunks of positions); its attention output is not used
+            ops.verify_attention_collect(q, kc.data, vc.data, visual=collector.visual, kv_len=kc.length,
+                                         scores=collector.scores_out(li))
+            collector.record(li)
         out = out.transpose(1, 2).reshape(1, n, hq * d)
         return residual + F.linear(out, p["o_w"])
 

@@ -16,6 +16,7 @@ import torch
 from . import _lib
 
 HEAD_DIM = 128
+STATUS_CACHE_OVERFLOW = _lib.STD_STATUS_CACHE_OVERFLOW   # device status word bit (see _status_ptr)
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -393,11 +394,23 @@ def compact_kv(dense_k: torch.Tensor, dense_v: torch.Tensor, sparse_k: torch.Ten
               sparse_k.stride(1), sparse_k.shape[2], code, _stream(dev))
 
 
+def _status_ptr(status: Optional[torch.Tensor], dev: torch.device):
+    """The device status word's address (or None): an int32 tensor of at least
+    one element on the op's device; kernels OR STD_STATUS_CACHE_OVERFLOW into
+    element 0 when a row or length falls past the cache capacity."""
+    if status is None:
+        return None
+    if status.dtype != torch.int32 or status.numel() < 1 or not status.is_contiguous() or status.device != dev:
+        raise TypeError("status must be a contiguous int32 tensor on the op's device")
+    return status.data_ptr()
+
+
 def kv_append(cache_k: torch.Tensor, cache_v: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor,
-              length: torch.Tensor) -> None:
+              length: torch.Tensor, status: Optional[torch.Tensor] = None) -> None:
     """Write new rows at positions length[0] + r (KVCache.cat, kv_cache.py:54-69,
     with the length on the device). cache_* [1, n_kv, capacity, D] buffers;
-    new_* [1, n_kv, rows, D] with contiguous rows (any head/row stride)."""
+    new_* [1, n_kv, rows, D] with contiguous rows (any head/row stride). Rows
+    that would land past the capacity are not written and mark ``status``."""
     dev = _check_device(cache_k, cache_v, new_k, new_v, length)
     code = _dtype_code(cache_k)
     _check_cache_view("cache_k", cache_k)
@@ -416,7 +429,7 @@ def kv_append(cache_k: torch.Tensor, cache_v: torch.Tensor, new_k: torch.Tensor,
     rows = new_k.shape[2]
     _lib.call("std_kv_append", cache_k.data_ptr(), cache_v.data_ptr(), new_k.data_ptr(), new_v.data_ptr(),
               cache_k.shape[1], rows, HEAD_DIM, cache_k.stride(1), new_k.stride(1), new_k.stride(2),
-              cache_k.shape[2], length.data_ptr(), code, _stream(dev))
+              cache_k.shape[2], length.data_ptr(), code, _status_ptr(status, dev), _stream(dev))
 
 
 def _check_dev_scalar(name: str, t: torch.Tensor) -> None:
@@ -426,7 +439,7 @@ def _check_dev_scalar(name: str, t: torch.Tensor) -> None:
 
 def rope_append(qkv: torch.Tensor, n_q: int, key_cache: torch.Tensor, value_cache: torch.Tensor,
                 length: torch.Tensor, position: torch.Tensor, inv_freq: torch.Tensor, pos_offset: int = 0,
-                q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                q_out: Optional[torch.Tensor] = None, status: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Rotary embedding of this step's rows plus the K/V cache append, with
     the length and the position read on the device (one launch).
 
@@ -435,7 +448,9 @@ def rope_append(qkv: torch.Tensor, n_q: int, key_cache: torch.Tensor, value_cach
     + r; its rotated keys and its values go to cache row length[0] + r.
     Returns the rotated queries [1, n_q, n, D] (q_out if given). Restates
     apply_multimodal_rotary_pos_emb (modeling_qwen2_5_vl.py:690-732) for text
-    positions and KVCache.cat (kv_cache.py:54-69); the length is not advanced."""
+    positions and KVCache.cat (kv_cache.py:54-69); the length is not advanced.
+    Rows that would land past the capacity are not written and mark
+    ``status`` (see _status_ptr)."""
     dev = _check_device(qkv, key_cache, value_cache, length, position, inv_freq)
     code = _dtype_code(qkv)
     if qkv.dim() != 3 or qkv.shape[0] != 1 or qkv.stride(2) != 1:
@@ -460,7 +475,8 @@ def rope_append(qkv: torch.Tensor, n_q: int, key_cache: torch.Tensor, value_cach
         raise ValueError("q_out must be a contiguous [1, n_q, n, D] tensor of the qkv dtype")
     _lib.call("std_rope_append", qkv.data_ptr(), qkv.stride(1), q_out.data_ptr(), key_cache.data_ptr(),
               value_cache.data_ptr(), n, n_q, n_kv, HEAD_DIM, key_cache.stride(1), key_cache.shape[2],
-              length.data_ptr(), position.data_ptr(), int(pos_offset), inv_freq.data_ptr(), code, _stream(dev))
+              length.data_ptr(), position.data_ptr(), int(pos_offset), inv_freq.data_ptr(), code,
+              _status_ptr(status, dev), _stream(dev))
     return q_out
 
 
@@ -471,7 +487,8 @@ QKV_ROPE_NORM_MAX_K = 3584     # ... and normalises rows up to this width in the
 def qkv_rope_append(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], n_q: int,
                     key_cache: torch.Tensor, value_cache: torch.Tensor, length: torch.Tensor,
                     position: torch.Tensor, inv_freq: torch.Tensor, pos_offset: int = 0,
-                    norm_weight: Optional[torch.Tensor] = None, eps: float = 0.0) -> torch.Tensor:
+                    norm_weight: Optional[torch.Tensor] = None, eps: float = 0.0,
+                    status: Optional[torch.Tensor] = None) -> torch.Tensor:
     """rope_append(linear(x, weight, bias), ...) in one launch for up to four
     bf16 rows: x [1, n, K] (K <= 4096), weight [(n_q + 2 n_kv) D, K] the
     stacked q|k|v projection, bias [(n_q + 2 n_kv) D] or None. Same outputs,
@@ -479,7 +496,7 @@ def qkv_rope_append(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.
     rotated queries [1, n_q, n, D]; rotated keys and the values go to cache
     row length[0] + r. The length is not advanced. With norm_weight (one row,
     K <= 3584) x is normalised first in the same launch, exactly as
-    rms_norm(x, norm_weight, eps)."""
+    rms_norm(x, norm_weight, eps). Rows past the capacity mark ``status``."""
     dev = _check_device(x, weight, key_cache, value_cache, length, position, inv_freq)
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise TypeError("qkv_rope_append: bf16 only")
@@ -511,19 +528,21 @@ def qkv_rope_append(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.
               bias.data_ptr() if bias is not None else None, n_q, n_kv, HEAD_DIM, q_out.data_ptr(),
               key_cache.data_ptr(), value_cache.data_ptr(), key_cache.stride(1), key_cache.shape[2],
               length.data_ptr(), position.data_ptr(), int(pos_offset), inv_freq.data_ptr(),
-              norm_weight.data_ptr() if norm_weight is not None else None, float(eps), _lib.STD_BF16, _stream(dev))
+              norm_weight.data_ptr() if norm_weight is not None else None, float(eps), _lib.STD_BF16,
+              _status_ptr(status, dev), _stream(dev))
     return q_out
 
 
 def attention_devlen(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
                      length: torch.Tensor, max_kv_len: int, scale: Optional[float] = None,
-                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     out: Optional[torch.Tensor] = None, status: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Offset-causal GQA attention with the cache length read on the device:
     keys [0, length[0] + q_len) are valid (this step's q_len rows last) and
     query row i sees keys [0, length[0] + i]; q_len == 1 is the decode. The
     launch is planned for max_kv_len (<= the cache capacity), so one captured
     graph serves every length up to it; a device length past
-    max_kv_len - q_len yields NaN outputs. query [1, n_q, q_len, D]."""
+    max_kv_len - q_len yields NaN outputs and marks ``status``. query
+    [1, n_q, q_len, D]."""
     dev = _check_device(query, key_cache, value_cache, length)
     code = _dtype_code(query)
     if query.dim() != 4 or query.shape[0] != 1:
@@ -553,7 +572,7 @@ def attention_devlen(query: torch.Tensor, key_cache: torch.Tensor, value_cache: 
     ws_ptr = _attn_workspace(ws_bytes, dev)
     _lib.call("std_attn_devlen", query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), out.data_ptr(), n_q,
               n_kv, q_len, length.data_ptr(), int(max_kv_len), d, key_cache.stride(1), value_cache.stride(1),
-              float(scale), code, ws_ptr, ws_bytes, _stream(dev))
+              float(scale), code, ws_ptr, ws_bytes, _status_ptr(status, dev), _stream(dev))
     return out
 
 
@@ -602,7 +621,8 @@ def pad_index(index: torch.Tensor) -> torch.Tensor:
 def gqa_decode_indexed(query: torch.Tensor, dense_k: torch.Tensor, dense_v: torch.Tensor, index: torch.Tensor,
                        n_index: int, key_cache: torch.Tensor, value_cache: torch.Tensor, kv_len: Optional[int] = None,
                        length: Optional[torch.Tensor] = None, max_kv_len: Optional[int] = None,
-                       scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                       status: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Draft decode whose first n_index keys per KV head are rows
     index[g, j] of the dense cache (no compaction copy); keys j >= n_index
     are rows j of the sparse cache key_cache / value_cache.
@@ -610,7 +630,8 @@ def gqa_decode_indexed(query: torch.Tensor, dense_k: torch.Tensor, dense_v: torc
     query [1, n_q, 1, D] bf16; dense_* and key/value caches [1, n_kv, capacity, D]
     views with contiguous rows; index int32 [n_kv, >= n_index rounded up to 16]
     (see pad_index). Host length: kv_len keys. Device length: length[0] + 1
-    keys (this step's row written at length[0]), planned for max_kv_len."""
+    keys (this step's row written at length[0]), planned for max_kv_len; a
+    length past it marks ``status``."""
     dev = _check_device(query, dense_k, dense_v, index, key_cache, value_cache)
     if query.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError("gqa_decode_indexed: bf16 or fp16")
@@ -656,7 +677,7 @@ def gqa_decode_indexed(query: torch.Tensor, dense_k: torch.Tensor, dense_v: torc
               dense_k.stride(1), dense_v.stride(1), index.data_ptr(), index.stride(0), n_index, key_cache.data_ptr(),
               value_cache.data_ptr(), key_cache.stride(1), value_cache.stride(1), out.data_ptr(), n_q, n_kv, plan,
               length.data_ptr() if length is not None else None, d, float(scale), _dtype_code(query), ws_ptr, ws_bytes,
-              _stream(dev))
+              _status_ptr(status, dev), _stream(dev))
     return out
 
 
@@ -861,8 +882,8 @@ def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value
                              new_key: Optional[torch.Tensor] = None, new_value: Optional[torch.Tensor] = None,
                              kv_len: Optional[int] = None, scale: Optional[float] = None,
                              out: Optional[torch.Tensor] = None, scores: Optional[torch.Tensor] = None,
-                             visual: Optional[VisualKeys] = None,
-                             length: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                             visual: Optional[VisualKeys] = None, length: Optional[torch.Tensor] = None,
+                             status: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Dense verify attention plus the visual-attention collector in one pass
     (VerificationCollectorV3._hook, dynamic_selection.py:504-519, riding the
     verify forward at modeling_qwen2_5_vl.py:1063-1067).
@@ -947,5 +968,5 @@ def verify_attention_collect(query: torch.Tensor, key_cache: torch.Tensor, value
               new_key.stride(2) if appending else 0, float(scale), _dtype_code(query), visual.begin, visual.end,
               visual.mask.data_ptr() if visual.mask is not None else None,
               visual.rank.data_ptr() if visual.rank is not None else None, visual.n, scores.data_ptr(),
-              scores.stride(0), ws_ptr, ws_bytes, _stream(dev))
+              scores.stride(0), ws_ptr, ws_bytes, _status_ptr(status, dev), _stream(dev))
     return out, scores

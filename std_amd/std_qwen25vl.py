@@ -441,6 +441,24 @@ def math_reverify_count(verify_attn_backend: str, accept_len: int, draft_len: in
     return int(verify_attn_backend == "math_on_full_accept" and accept_len == draft_len)
 
 
+def _decode_status(model, dev) -> torch.Tensor:
+    """The model's device status word (cleared), or a zero stand-in for a
+    model without one."""
+    status = getattr(model, "decode_status", None)
+    if status is None:
+        return torch.zeros(1, dtype=torch.int32, device=dev)
+    status.zero_()
+    return status
+
+
+def _check_decode_status(value: int) -> None:
+    """Raise as the reference's KVCache.cat does (kv_cache.py:54-69) when a
+    device-length step reported a cache overflow."""
+    if int(value) & ops.STATUS_CACHE_OVERFLOW:
+        raise RuntimeError("KV cache overflow: a decode step's device length placed rows past a cache's capacity "
+                           "(nothing was written there; the cache was sized too small for this decode)")
+
+
 def _token_argmax(logits: torch.Tensor) -> torch.Tensor:
     """[1, 1] int64 next token of the last row (graph-capture safe argmax)."""
     return ops.argmax_rows(logits[0, -1:, :]).view(1, 1)
@@ -548,6 +566,7 @@ def ar_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id:
     prefill_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
 
     generated: List[torch.Tensor] = []
+    status = _decode_status(model, model.device)
     step = None
     if use_graphs and max_new_tokens > 1:
         state = torch.tensor([prompt_len, prompt_len], dtype=torch.int32).to(model.device)   # (length, position)
@@ -582,6 +601,7 @@ def ar_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id:
         fill_cache_length(lengths, prompt_len + len(generated) - 1)
     torch.cuda.synchronize()
     end = time.time()
+    _check_decode_status(int(status[0]))
     gen = torch.cat(generated) if generated else torch.empty(0, dtype=torch.long, device=model.device)
     out = torch.cat([prompt_ids, gen.reshape(1, -1)], dim=1)
     return GenerateResult(out, end - decode_start, end - start, int(gen.numel()), cache_init_time=cache_init_time,
@@ -790,6 +810,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         # the verify graphs' logits buffers: plain, and with the collector (or None)
         return caps, holder["draft"], holder["res"], (holder["logits"], holder.get("coll_logits"))
 
+    status = _decode_status(model, dev)
     torch.cuda.synchronize()
     decode_start = time.time()
     while len(generated) < max_new_tokens:
@@ -852,8 +873,9 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
                                     dense_next=None if dense_pending else dense_next_i32)
         if trace is not None:
             trace.end_verification()
-        host = torch.cat([res[:2], draft_dev.to(torch.int32)]).tolist()     # the round's one readback
-        accept_len, bonus_token, draft = host[0], host[1], host[2:]
+        host = torch.cat([res[:2], status, draft_dev.to(torch.int32)]).tolist()     # the round's one readback
+        accept_len, bonus_token, draft = host[0], host[1], host[3:]
+        _check_decode_status(host[2])
         verify_time += _profile_mark(profile_decode) - stage
         accept_lengths.append(accept_len)
         accepted_total += accept_len

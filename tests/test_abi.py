@@ -172,7 +172,7 @@ def test_verify_collect_ex_validation():
     hs = 4106 * 128
     args = dict(q=16, k=16, v=16, nk=NULL, nv=NULL, out=16, nq=28, nkv=4, ql=10, kv=4106, len_dev=NULL, d=128,
                 khs=hs, vhs=hs, nhs=0, nrs=0, scale=0.088, dt=1, vb=0, ve=3968, mask=NULL, rank=NULL, nvis=3968,
-                sc=16, schs=3968, ws=16, wsb=1 << 30, st=NULL)
+                sc=16, schs=3968, ws=16, wsb=1 << 30, status=NULL, st=NULL)
 
     def call(**kw):
         a = dict(args, **kw)
@@ -228,7 +228,8 @@ def test_indexed_decode_validation():
     hs = 128 * 4096
     # fp32 is not served; the index must be present, aligned and padded to 16 entries per row
     args = dict(q=16, dk=16, dv=16, rows=4096, dks=hs, dvs=hs, idx=16, ihs=1024, n=1024, k=16, v=16, ks=hs, vs=hs,
-                out=16, nq=28, nkv=4, kv=1100, ld=NULL, d=128, scale=0.088, dt=1, ws=16, wsb=1 << 30, st=NULL)
+                out=16, nq=28, nkv=4, kv=1100, ld=NULL, d=128, scale=0.088, dt=1, ws=16, wsb=1 << 30, status=NULL,
+                st=NULL)
 
     def call(**kw):
         a = dict(args, **kw)
@@ -253,8 +254,8 @@ def test_gemv_validation():
     assert lib.std_gemv(NULL, 128, 16, 128, NULL, 16, 64, 1, 64, 128, 1, NULL, 0, NULL) == -1
     # the fused q|k|v projection: bf16 only
     qkv = [16, 3584, 1, 3584, 16, 3584, NULL, 28, 4, 128, 16, 16, 16, 128 * 1024, 1024, 16, 16, 0, 16, NULL, 1e-6]
-    assert lib.std_qkv_rope_append(*qkv, 2, NULL) == -2
-    assert lib.std_qkv_rope_append(*qkv, 0, NULL) == -2
+    assert lib.std_qkv_rope_append(*qkv, 2, NULL, NULL) == -2
+    assert lib.std_qkv_rope_append(*qkv, 0, NULL, NULL) == -2
 
 
 def test_accept_and_append_validation():
@@ -263,8 +264,8 @@ def test_accept_and_append_validation():
     assert lib.std_greedy_accept(16, 152064, 9, 152064, 1, 16, 9, 1, NULL, 16, NULL, 0, 16, 1 << 20, NULL) == -3
     # dense_next is required without a pending token
     assert lib.std_greedy_accept(16, 152064, 9, 152064, 1, 16, 9, 0, NULL, 16, NULL, 0, 16, 1 << 20, NULL) == -1
-    assert lib.std_kv_append(16, 16, 16, 16, 4, 1, 128, 128 * 100, 128, 512, 100, NULL, 1, NULL) == -1
-    assert lib.std_kv_append(16, 16, 16, 16, 4, 1, 128, 128 * 100, 128, 3, 100, 16, 1, NULL) == -5  # row stride
+    assert lib.std_kv_append(16, 16, 16, 16, 4, 1, 128, 128 * 100, 128, 512, 100, NULL, 1, NULL, NULL) == -1
+    assert lib.std_kv_append(16, 16, 16, 16, 4, 1, 128, 128 * 100, 128, 3, 100, 16, 1, NULL, NULL) == -5  # row stride
     assert lib.std_compact_kv(16, 16, 16, 16, 16, 4, 2000, 128, 128 * 4096, 4096, 128 * 1024, 1024, 1, NULL) == -6
 
 

@@ -100,15 +100,29 @@ def test_kv_append_at_device_length_and_len_add():
     assert torch.count_nonzero(ck[:, :, :10]) == 0 and torch.count_nonzero(ck[:, :, 14:]) == 0
 
 
-def test_kv_append_past_capacity_is_skipped():
-    ck = torch.zeros(1, 2, 8, 128, device=dev())
-    cv = torch.zeros_like(ck)
+def test_kv_append_past_capacity_is_skipped_and_reported():
+    """Rows that would land at or past the capacity are not written (the
+    memory after the cache is left alone) and mark the device status word;
+    an append that fits leaves the word as it was."""
+    buf = torch.full((1, 2, 12, 128), -7.0, device=dev())
+    buf_v = torch.full_like(buf, -7.0)
+    ck, cv = buf[:, :, :8], buf_v[:, :, :8]              # rows 8..11 of the buffers lie past the caches' capacity
     nk = torch.ones(1, 2, 3, 128, device=dev())
-    length = torch.tensor([6], dtype=torch.int32, device=dev())
-    announce("kv_append past capacity")
-    ops.kv_append(ck, cv, nk, nk, length)
+    status = torch.zeros(1, dtype=torch.int32, device=dev())
+    announce("kv_append past capacity, status word")
+    ops.kv_append(ck, cv, nk[:, :, :2], nk[:, :, :2], torch.tensor([0], dtype=torch.int32, device=dev()),
+                  status=status)
     torch.cuda.synchronize()
-    assert torch.all(ck[:, :, 6:] == 1) and torch.all(ck[:, :, :6] == 0)
+    assert int(status) == 0
+    ops.kv_append(ck, cv, nk, nk, torch.tensor([6], dtype=torch.int32, device=dev()), status=status)
+    torch.cuda.synchronize()
+    assert int(status) == ops.STATUS_CACHE_OVERFLOW
+    assert torch.all(ck[:, :, 6:] == 1) and torch.all(ck[:, :, 2:6] == -7) and torch.all(ck[:, :, :2] == 1)
+    assert torch.all(buf[:, :, 8:] == -7) and torch.all(buf_v[:, :, 8:] == -7), "an append wrote past the cache"
+    status.zero_()
+    ops.kv_append(ck, cv, nk, nk, torch.tensor([-2], dtype=torch.int32, device=dev()), status=status)
+    torch.cuda.synchronize()
+    assert int(status) == ops.STATUS_CACHE_OVERFLOW
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

@@ -325,3 +325,32 @@ def test_collector_in_graph_replayed_rounds(gamma):
         assert torch.equal(a, b), f"round {r}: graph-replayed scores differ from the eager round's"
         q_rows = graph.proposed_lengths[r] + graph.pending_lengths[r]
         np.testing.assert_allclose(b.double().sum(-1).numpy(), q_rows, rtol=1e-4)
+
+
+def test_collector_records_every_round_of_a_long_verify():
+    """gamma = 13 at seven query heads per KV head: fourteen verify positions
+    (98 query rows per KV head) take the decoder's unfused verify path; the
+    collector still records one round per verification (the reference's hook
+    runs in every verify forward), each summing to the round's positions."""
+    from std_amd.std_qwen25vl import VerificationCollectorV3, set_trace_collector, std_generate_qwen25vl
+    from std_amd.decoder import DecoderConfig, RandomDecoder
+
+    cfg = DecoderConfig.tiny(layers=2)
+    model = RandomDecoder(cfg, dev(), torch.bfloat16, seed=5006)
+    inputs = _two_segment_inputs(cfg, 37)
+    positions = torch.nonzero(inputs["input_ids"][0] == cfg.video_token_id).flatten().cpu()
+    announce("collector rounds, gamma=13, eager")
+    coll = VerificationCollectorV3(model, positions)
+    coll.install()
+    set_trace_collector(coll)
+    try:
+        res, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=30,
+                                       gamma=13, target_k_plus_text=256, ignore_eos=True)
+    finally:
+        set_trace_collector(None)
+        coll.uninstall()
+    assert len(coll.rounds) == res.decode_rounds >= 2
+    for r, sc in enumerate(coll.rounds):
+        q_rows = res.proposed_lengths[r] + res.pending_lengths[r]
+        assert sc.shape == (cfg.num_hidden_layers, cfg.num_key_value_heads, positions.numel())
+        np.testing.assert_allclose(sc.double().sum(-1).numpy(), q_rows, rtol=1e-4)

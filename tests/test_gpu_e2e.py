@@ -256,3 +256,26 @@ def test_trace_collector_brackets_prefill_and_each_verify(tiny32, use_graphs):
     std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=4, gamma=2,
                           target_k_plus_text=TARGET, ignore_eos=True, use_graphs=use_graphs)
     assert events == []
+
+
+@pytest.mark.parametrize("use_graphs", [False, True])
+def test_cache_overflow_raises_instead_of_dropping_rows(tiny32, monkeypatch, use_graphs):
+    """Caches sized too small for the decode: the reference's KVCache.cat
+    raises (kv_cache.py:54-69). Here the device-length appends skip the rows
+    past the capacity and mark the model's status word, which the round's
+    readback turns into the same RuntimeError (with graphs), or the host
+    length check raises it first (eager)."""
+    import std_amd.std_qwen25vl as stdq
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 13, n_visual=300, n_text=20)
+    announce(f"e2e cache overflow reported, graphs={use_graphs}")
+    monkeypatch.setattr(stdq, "_cache_capacity", lambda p, n, g: p + 12)
+    with pytest.raises(RuntimeError, match="KV cache overflow"):
+        std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=40, gamma=5,
+                              target_k_plus_text=TARGET, ignore_eos=True, use_graphs=use_graphs)
+    torch.cuda.synchronize()
+    monkeypatch.undo()
+    # the status word is cleared by the next call, which runs normally
+    std, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=12, gamma=5,
+                                   target_k_plus_text=TARGET, ignore_eos=True, use_graphs=use_graphs)
+    assert std.generate_len == 12 and int(model.decode_status) == 0

@@ -116,13 +116,54 @@ def test_attention_devlen_small_cache_matches_oracle(dtype, cap, kv):
 
 
 def test_attention_devlen_rejects_length_past_plan_with_nan():
+    """A device length outside [0, max_kv_len - q_len] reads nothing, writes NaN
+    outputs and marks the status word; a valid one leaves the word alone."""
     announce("attention_devlen with a device length past max_kv_len - q_len")
     k = torch.randn(1, NKV, 512, D, device=dev()).to(torch.bfloat16)
     q = torch.randn(1, NQ, 4, D, device=dev()).to(torch.bfloat16)
+    status = torch.zeros(1, dtype=torch.int32, device=dev())
+    ops.attention_devlen(q, k, k, _scalar(296), max_kv_len=300, status=status)
+    torch.cuda.synchronize()
+    assert int(status) == 0
     for bad in (300, -1):
-        out = ops.attention_devlen(q, k, k, _scalar(bad), max_kv_len=300)
+        status.zero_()
+        out = ops.attention_devlen(q, k, k, _scalar(bad), max_kv_len=300, status=status)
         torch.cuda.synchronize()
         assert torch.isnan(out.float()).all()
+        assert int(status) == ops.STATUS_CACHE_OVERFLOW
+    for dt in (torch.float32, torch.float16):          # the fp32 kernel and the fp16 instances report it too
+        status.zero_()
+        out = ops.attention_devlen(q.to(dt), k.to(dt), k.to(dt), _scalar(-5), max_kv_len=300, status=status)
+        torch.cuda.synchronize()
+        assert torch.isnan(out.float()).all() and int(status) == ops.STATUS_CACHE_OVERFLOW
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_rope_append_past_capacity_is_skipped_and_reported(fused):
+    """rope_append / qkv_rope_append with rows at or past the capacity: the
+    rows that fit are written, the others are not (memory after the cache is
+    untouched), the queries are still produced, and the status word is set."""
+    announce(f"rope append past capacity, status word, fused={fused}")
+    g = torch.Generator().manual_seed(71)
+    cap, n = 20, 3
+    buf_k = torch.full((1, NKV, cap + 8, D), -3.0, device=dev()).to(torch.bfloat16)
+    buf_v = torch.full((1, NKV, cap + 8, D), -3.0, device=dev()).to(torch.bfloat16)
+    kc, vc = buf_k[:, :, :cap], buf_v[:, :, :cap]
+    inv = (1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float64) / D))).float().to(dev())
+    status = torch.zeros(1, dtype=torch.int32, device=dev())
+    if fused:
+        K = 256
+        x = torch.randn(1, n, K, generator=g).to(torch.bfloat16).to(dev())
+        w = (0.05 * torch.randn((NQ + 2 * NKV) * D, K, generator=g)).to(torch.bfloat16).to(dev())
+        q = ops.qkv_rope_append(x, w, None, NQ, kc, vc, _scalar(cap - 1), _scalar(500), inv, status=status)
+    else:
+        qkv = torch.randn(1, n, (NQ + 2 * NKV) * D, generator=g).to(torch.bfloat16).to(dev())
+        q = ops.rope_append(qkv, NQ, kc, vc, _scalar(cap - 1), _scalar(500), inv, status=status)
+    torch.cuda.synchronize()
+    assert int(status) == ops.STATUS_CACHE_OVERFLOW
+    assert torch.isfinite(q.float()).all()
+    assert not torch.all(kc[:, :, cap - 1] == -3.0) and torch.all(kc[:, :, :cap - 1] == -3.0)
+    assert torch.all(buf_k[:, :, cap:] == -3.0) and torch.all(buf_v[:, :, cap:] == -3.0)
 
 
 @pytest.mark.parametrize("n,K,n_q,n_kv,length,pos,off,cap",
