@@ -245,10 +245,22 @@ def main():
     lengths = lengths0.clone()
     dense_len, sparse_len = lengths[0:1], lengths[1:2]
 
+    # A 1 GiB read that evicts the Infinity Cache (clean lines), as a model's
+    # weight stream between two draft steps does.
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    rflush = flush.view(torch.int32)
+    rsink = torch.zeros(1024, dtype=torch.int32, device=dev)
+
+    def read_flush():
+        ops.stream_read(rflush, 0, 1024, rsink)
+
     # Each layer call appends its new K/V row(s) and attends in one launch
     # (KVCache.cat + attention); the device lengths advance once per step.
-    def draft_phase():
+    # With evict, the caches are evicted before each draft step.
+    def draft_phase(evict=None):
         for t in range(G):
+            if evict is not None:
+                evict()
             S = S0 + t + 1
             for l in range(L):
                 ops.gqa_decode_append(q_draft[l], sparse_k[l], sparse_v[l], new_k_draft[l], new_v_draft[l], S,
@@ -262,11 +274,18 @@ def main():
                                         out=verify_out[l])
         ops.len_add(dense_len, Q)
 
-    def round_kernels():
+    def round_kernels(evict=None):
         lengths.copy_(lengths0)                          # steady state: same shapes every round
-        draft_phase()
+        draft_phase(evict)
         verify_phase()
         return ops.greedy_accept(logits, draft, True, rollback_lengths=lengths)
+
+    def round_kernels_cold():
+        return round_kernels(read_flush)
+
+    def evictions_only():
+        for _ in range(G):
+            read_flush()
 
     def capture(fn):
         """Capture fn into a HIP graph (after one eager warm-up on a side stream)."""
@@ -288,27 +307,57 @@ def main():
     a_eager = int(res_eager[0])
     draft_eager, verify_eager = draft_out.clone(), verify_out.clone()
     assert a_eager == 6, f"acceptance length {a_eager} != 6"
-    round_graph, res_graph = capture(round_kernels)
+    # The timed round evicts the caches before each draft step (the compact
+    # cache is then read cold, as in a model's decode); the evictions' own
+    # time, from a graph of the evictions alone, is subtracted. The same round
+    # without evictions (compact cache warm in the Infinity Cache between
+    # steps) is timed as well and reported beside it.
+    round_graph, res_graph = capture(round_kernels_cold)
+    warm_graph, res_warm = capture(round_kernels)
+    evict_graph, _ = capture(evictions_only)
 
-    def step():
-        round_graph.replay()
-        return int(res_graph[0].item())                  # the one readback per round
+    def step(graph=round_graph, res=res_graph):
+        graph.replay()
+        return int(res[0].item())                        # the one readback per round
 
     for _ in range(args.warmup):
         a = step()
+        a_warm = step(warm_graph, res_warm)
     torch.cuda.synchronize()
     # every replay must reproduce the eager round exactly (same kernels, same inputs)
     assert a == a_eager and torch.equal(draft_out, draft_eager) and torch.equal(verify_out, verify_eager), \
         "graph replay differs from the eager round"
+    assert a_warm == a_eager
 
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    def timed(graph, res):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step(graph, res)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    def timed_evictions():
+        """The evictions of one round: median of event-timed replays."""
+        stream = torch.cuda.current_stream()
+        times = []
+        for _ in range(max(5, args.steps)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            evict_graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e-3)
+        return statistics.median(times)
+
+    evict_s = timed_evictions()
+    elapsed_with_evictions = timed(round_graph, res_graph)
+    elapsed = elapsed_with_evictions - args.steps * evict_s
     ms_per_step = elapsed * 1e3 / args.steps
-    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
+    elapsed_warm = timed(warm_graph, res_warm)
+    ms_per_step_warm = elapsed_warm * 1e3 / args.steps
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (cold draft steps; evictions "
+        f"{evict_s * 1e3:.3f} ms/round subtracted), {ms_per_step_warm:.3f} ms/step warm")
 
     # ---- per-kernel timing: graphs of one phase's attention calls, HIP events on the replay stream ----
     kv = P + Q
@@ -408,13 +457,14 @@ def main():
 
     # Streaming-read ceiling on this device, in the same process: 256 MiB reads
     # over 8 distinct buffers in the fastest patterns of the stream workload
-    # (the verify kernel's LDS DMA ring, the decode key split's, and vector
-    # loads, all dealing tiles round-robin); the attention kernels are also
-    # reported as a fraction of it.
+    # (the verify kernel's LDS DMA ring, the decode key split's, with the
+    # default and the non-temporal load policy, and vector loads, all dealing
+    # tiles round-robin); the attention kernels are also reported as a
+    # fraction of it.
     sbufs = [torch.ones((256 << 20) // 4, dtype=torch.int32, device=dev) for _ in range(8)]
     ssink = torch.zeros(4096, dtype=torch.int32, device=dev)
     ceiling = {}
-    for mode, n_wg in ((3, 256), (3, 208), (5, 256), (5, 192), (1, 1024)):
+    for mode, n_wg in ((3, 256), (3, 208), (5, 256), (5, 192), (1, 1024), (6, 256), (7, 256), (7, 192)):
         def reads(mode=mode, n_wg=n_wg):
             for b in sbufs:
                 ops.stream_read(b, mode, n_wg, ssink)
@@ -428,15 +478,8 @@ def main():
     # caches full of dirty lines, so the copy also pays for their write-back;
     # a decode's weight stream evicts with clean lines, which the second form,
     # a 1 GiB read before each copy, reproduces.
-    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    rflush = flush.view(torch.int32)
-    rsink = torch.zeros(1024, dtype=torch.int32, device=dev)
-
     def write_flush():
         flush.fill_(1)
-
-    def read_flush():
-        ops.stream_read(rflush, 0, 1024, rsink)
 
     cold = {}
     for kind, evict in (("write", write_flush), ("read", read_flush)):
@@ -447,7 +490,6 @@ def main():
         cold[kind] = (time_graph(step_cold_graph, args.cold_iters, rep) - flush_us,
                       time_graph(all_cold_graph, args.cold_iters, rep) - flush_us)
         del flush_graph, step_cold_graph, all_cold_graph
-    del flush, rflush, rsink
     draft_step_cold_us, draft_all_cold_us = cold["write"]
     draft_step_rcold_us, draft_all_rcold_us = cold["read"]
     d_bytes = draft_bytes(Hq, Hkv, S0, D, es)
@@ -456,6 +498,7 @@ def main():
     draft_step_cold_gbps = L * d_bytes / (draft_step_cold_us * 1e-6) / 1e9
 
     draft_tokens_per_s = G * args.steps / elapsed
+    draft_tokens_per_s_warm = G * args.steps / elapsed_warm
     traffic = None
     # counter passes are per element type (the committed ones are bf16)
     tsuffix = "_fp16" if w.dtype == torch.float16 else ""
@@ -481,9 +524,14 @@ def main():
             "workload": f"{w.name}: {L}-layer attention stack, {Hq}q/{Hkv}kv heads, d={D}, context {P} "
                         f"({P - T} visual + {T} text), K+text={w.k_plus_text}, gamma={G}, vocab={w.vocab}",
             "step": "gamma draft decode steps over the compact cache + dense verify (q=gamma+1) + greedy "
-                    "accept/rollback, all layers; replayed as one HIP graph plus one 8-byte readback",
+                    "accept/rollback, all layers; replayed as one HIP graph plus one 8-byte readback; the caches "
+                    "are evicted by a 1 GiB read before each draft step (a model's weight stream between steps) "
+                    "and the evictions' own time, from a graph of them alone, is subtracted",
             "parallelism": "single GPU",
         },
+        "value_warm_draft_steps": round(draft_tokens_per_s_warm, 2),
+        "ms_per_step_warm_draft_steps": round(ms_per_step_warm, 4),
+        "evictions_ms_per_step_subtracted": round(evict_s * 1e3, 4),
         "draft_attn_us_per_step": round(draft_call_us * L, 2),
         "draft_attn_us_per_layer": round(draft_call_us, 3),
         "draft_hbm_gbps_warm": round(d_bytes / (draft_call_us * 1e-6) / 1e9, 1),
@@ -491,8 +539,8 @@ def main():
         # In a model's decode the layers' weights stream between two draft steps
         # and evict the compact cache from the Infinity Cache: the round's rate
         # with each of its draft steps at the measured cold step time instead.
-        "value_with_cold_draft_steps": round(G / ((ms_per_step + G * (draft_step_cold_us - draft_call_us * L) / 1e3)
-                                                  * 1e-3), 2),
+        "value_with_cold_draft_steps": round(G / ((ms_per_step_warm + G * (draft_step_cold_us - draft_call_us * L)
+                                                   / 1e3) * 1e-3), 2),
         "draft_hbm_gbps_cold_step": round(draft_step_cold_gbps, 1),
         "draft_pct_peak_cold_step": round(100 * draft_step_cold_gbps / HBM_PEAK_GBPS, 2),
         "draft_attn_us_per_step_one_launch_cold": round(draft_all_cold_us, 2),
@@ -503,7 +551,7 @@ def main():
         # The same cold figures with the caches evicted by a 1 GiB read (clean lines).
         "draft_attn_us_per_step_cold_read_evicted": round(draft_step_rcold_us, 2),
         "value_with_cold_draft_steps_read_evicted": round(
-            G / ((ms_per_step + G * (draft_step_rcold_us - draft_call_us * L) / 1e3) * 1e-3), 2),
+            G / ((ms_per_step_warm + G * (draft_step_rcold_us - draft_call_us * L) / 1e3) * 1e-3), 2),
         "draft_attn_us_per_step_one_launch_cold_read_evicted": round(draft_all_rcold_us, 2),
         "draft_one_launch_pct_peak_cold_read_evicted": round(
             100 * L * d_bytes / (draft_all_rcold_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2),
@@ -870,7 +918,7 @@ def run_stream(args) -> None:
     configs += [(m, n) for m in (2, 4) for n in (256, 512)]
     # round-robin rings also with fewer workgroups than CUs (contiguous chunks
     # need a workgroup count that divides the 8192 tiles)
-    configs += [(m, n) for m in (3, 5) for n in (192, 208, 224, 256, 512)]
+    configs += [(m, n) for m in (3, 5, 6, 7) for n in (192, 208, 224, 256, 512)]
     for mode, n_wg in configs:
         def body():
             for i in range(reads):
@@ -947,7 +995,10 @@ def cpu_baseline(w, L):
     verify, argmax + prefix for the accept), timed on one layer's inputs of
     the workload (bf16 values upcast): 3 warm-ups then the median of 10 calls
     with torch's thread count, and 1 warm-up then the median of 3 with one
-    thread; one round = L x (verify + gamma draft steps) + one accept."""
+    thread; one round = L x (verify + gamma draft steps) + one accept. The
+    verify and the selection are timed on bounded key samples (scaled by the
+    key count) and once each at the full size with all threads; the round
+    (`value`) uses the full-size verify call."""
     import torch
 
     from oracle import torch_cpu
@@ -1003,6 +1054,16 @@ def cpu_baseline(w, L):
     threads = torch.get_num_threads()
     t0 = time.perf_counter()
     r_all, v_all, d_all, a_all = round_seconds("", 3, 10, 8.0)
+    # One full-size call each of the verify (all kv_len keys) and, below, the
+    # selection: the scale factors of the samples, measured.
+    kf_full = torch.cat([x["k"], x["new_k"]], 2).float()
+    vf_full = torch.cat([x["v"], x["new_v"]], 2).float()
+    torch_cpu.verify_attention(qv[:, :, :1], kf_full[:, :, :w.prompt_len + 1], vf_full[:, :, :w.prompt_len + 1])
+    t1 = time.perf_counter()
+    torch_cpu.verify_attention(qv, kf_full, vf_full)
+    v_full = time.perf_counter() - t1
+    del kf_full, vf_full
+    r_full = L * (v_full + w.gamma * d_all) + a_all
     # Selection (once per prompt, outside the round): one layer's text rows over
     # the first visual keys and the text keys of a bounded prompt, scaled to the
     # full prompt (the work is linear in the key count).
@@ -1013,6 +1074,11 @@ def cpu_baseline(w, L):
     t_sel = (w.prompt_len / p_sel) * median_time(
         "select", lambda: torch_cpu.select_topk(qt, k_sel, p_sel - w.text_len, min(w.k, p_sel - w.text_len)),
         3, 10, 8.0)
+    k_full = x["k"].float()
+    t1 = time.perf_counter()
+    torch_cpu.select_topk(qt, k_full, w.prompt_len - w.text_len, w.k)
+    t_sel_full = time.perf_counter() - t1
+    del k_full
     torch.set_num_threads(1)
     try:
         r_one, v_one, d_one, _ = round_seconds("_1_thread", 1, 3, 4.0)
@@ -1020,24 +1086,28 @@ def cpu_baseline(w, L):
         torch.set_num_threads(threads)
     sample_s = time.perf_counter() - t0
     return {
-        "value": round(w.gamma / r_all, 3),
+        "value": round(w.gamma / r_full, 3),
         "unit": "draft tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"one layer of the workload (verify q={Q} over {kv_len} keys, timed over {kv_sample} of them and "
-                  f"scaled x{verify_scale:.3f}; one draft step over {w.compact_len} keys; one accept over {Q} x "
-                  f"{w.vocab} logits), torch "
-                  f"fp32 on the CPU, 3 warm-ups + median of 10 ({threads} threads) and 1 + median of 3 (1 thread), "
-                  f"fewer where one call would overrun the leg's time budget (see warmups_reps); "
-                  f"round = {L} x (verify + {w.gamma} draft steps) + accept",
+        "sample": f"one layer of the workload, torch fp32 on the CPU: one full-size verify call (q={Q} over {kv_len} "
+                  f"keys, after a one-row warm-up over the same keys), one draft step over {w.compact_len} keys and "
+                  f"one accept over {Q} x {w.vocab} logits (3 warm-ups + median of 10, {threads} threads); "
+                  f"round = {L} x (verify + {w.gamma} draft steps) + accept. Also: the verify over {kv_sample} keys "
+                  f"scaled x{verify_scale:.3f} (value_scaled_sample), and the legs with 1 thread",
+        "value_scaled_sample": round(w.gamma / r_all, 3),
+        "verify_ms_per_layer_full_call": round(v_full * 1e3, 1),
+        "verify_full_over_scaled_sample": round(v_full / v_all, 3),
+        "select_ms_per_layer_full_call": round(t_sel_full * 1e3, 1),
+        "select_full_over_scaled_sample": round(t_sel_full / t_sel, 3),
         "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
         "threads": threads,
         "value_1_thread": round(w.gamma / r_one, 3),
-        "verify_ms_per_layer": round(v_all * 1e3, 3),
+        "verify_ms_per_layer_scaled_sample": round(v_all * 1e3, 3),
         "draft_ms_per_layer_step": round(d_all * 1e3, 4),
         "accept_ms": round(a_all * 1e3, 3),
-        "select_ms_per_layer": round(t_sel * 1e3, 2),
+        "select_ms_per_layer_scaled_sample": round(t_sel * 1e3, 2),
         "select_sample": f"{p_sel} of {w.prompt_len} keys, scaled x{w.prompt_len / p_sel:.3f}; all threads only",
         "verify_ms_per_layer_1_thread": round(v_one * 1e3, 3),
         "draft_ms_per_layer_step_1_thread": round(d_one * 1e3, 4),

@@ -526,9 +526,11 @@ int std_verify_attn_collect_ex(const void* q, void* k_cache, void* v_cache,
  *             thread per 32 KiB tile;
  *   mode 2/3: the verify kernel's LDS DMA ring (eight waves, two tiles in
  *             flight), each tile 16 KiB from either half of the buffer;
- *   mode 4/5: the decode key split's ring (four waves, three in flight).
- * Even modes give each workgroup one contiguous chunk (the tile count must
- * divide by n_workgroups), odd modes deal tiles round-robin.
+ *   mode 4/5: the decode key split's ring (four waves, three in flight);
+ *   mode 6/7: modes 3 and 5 with non-temporal loads (the policy the attention
+ *             kernels use for key ranges of 8192 keys and more).
+ * Modes 0, 2 and 4 give each workgroup one contiguous chunk (the tile count
+ * must divide by n_workgroups); modes 1, 3, 5, 6 and 7 deal tiles round-robin.
  * ------------------------------------------------------------------------ */
 int std_stream_read(const void* src, size_t bytes, int mode, int n_workgroups, uint32_t* sink, void* stream);
 

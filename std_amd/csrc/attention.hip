@@ -203,6 +203,13 @@ WsLayout ws_layout(int n_kv, int rows, const SplitPlan& p, int part_bytes) {
   return l;
 }
 
+// A problem of at least kStreamTiles key tiles (8192 keys: 4 MiB of K and V
+// per KV head, a dense cache rather than the draft's compact one) is read once
+// per launch and not again before other data has passed through the caches:
+// its tiles are loaded non-temporally.
+constexpr int kStreamTiles = 128;
+inline bool stream_keys(int ntiles) { return ntiles >= kStreamTiles; }
+
 // Tiles are dealt to the splits of a head round-robin: split s streams tiles
 // s, s + n_split, s + 2 n_split, ... so that at every step the workgroups of a
 // head read neighbouring 16 KiB tiles, spread over the HBM channels. (One
@@ -660,7 +667,7 @@ struct Bf16Cfg {
 template <int NT, typename E>
 using PartT = typename std::conditional<(NT > 1) && std::is_same<E, bf16_t>::value, half_t, float>::type;
 
-template <int NT, bool KS, bool GA, bool COLL = false, typename E = bf16_t>
+template <int NT, bool KS, bool GA, bool COLL = false, typename E = bf16_t, bool STREAM = false>
 __global__ void __launch_bounds__(NT == 1 ? 256 : 512)
 attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* __restrict__ vc,
                  bf16_t* __restrict__ out, PartT<NT, E>* __restrict__ ws_o, float2* __restrict__ ws_ml, int q_len,
@@ -824,8 +831,8 @@ attn_bf16_kernel(const bf16_t* __restrict__ q, bf16_t* __restrict__ kc, bf16_t* 
     for (int j = 0; j < kSegs; ++j) {
       const uint32_t off = (uint32_t)(min(dma_row[j], last) * ROWB + dma_chunk[j]);
       const uint32_t dst = lds_addr(stage) + (w * kSegs + j) * 1024;
-      lds_dma16_sbase(kt, off, dst);
-      lds_dma16_sbase(vt, off, dst + TILEB);
+      lds_dma16_sbase<STREAM>(kt, off, dst);
+      lds_dma16_sbase<STREAM>(vt, off, dst + TILEB);
     }
   };
 
@@ -1581,12 +1588,17 @@ void launch_h16(const void* q, void* k, void* v, void* out, int q_len, int kv_le
                 const int32_t* len_dev, GatherArgs ga, hipStream_t st) {
   // One row tile and at least two tiles per split on average: key split.
   const bool ks = NT == 1 && p.ntiles >= 2 * p.n_split;
+  // Long key ranges stream with non-temporal loads (stream_keys).
+  const bool str = stream_keys(p.ntiles);
   // Gathered keys (decode only): a separate instantiation, so the plain
   // kernels carry none of the gather code or arguments.
-  auto kern = NT == 1 && ga.idx != nullptr ? (ks ? attn_bf16_kernel<NT, NT == 1, NT == 1, false, E>
-                                                 : attn_bf16_kernel<NT, false, NT == 1, false, E>)
-                                           : (ks ? attn_bf16_kernel<NT, NT == 1, false, false, E>
-                                                 : attn_bf16_kernel<NT, false, false, false, E>);
+  auto kern = NT == 1 && ga.idx != nullptr
+                  ? (ks ? attn_bf16_kernel<NT, NT == 1, NT == 1, false, E>
+                        : attn_bf16_kernel<NT, false, NT == 1, false, E>)
+                  : str ? (ks ? attn_bf16_kernel<NT, NT == 1, false, false, E, true>
+                              : attn_bf16_kernel<NT, false, false, false, E, true>)
+                        : (ks ? attn_bf16_kernel<NT, NT == 1, false, false, E>
+                              : attn_bf16_kernel<NT, false, false, false, E>);
   hipLaunchKernelGGL(kern, grid, dim3(Bf16Cfg<NT>::kThreads), 0, st,
                      static_cast<const bf16_t*>(q), static_cast<bf16_t*>(k), static_cast<bf16_t*>(v),
                      static_cast<bf16_t*>(out), static_cast<PartT<NT, E>*>(ws_o), ws_ml, q_len, kv_len, group, k_hs,
@@ -1811,7 +1823,9 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
     auto run = [&](auto elem) -> int {
       using E = decltype(elem);
       using PT = PartT<5, E>;
-      hipLaunchKernelGGL((attn_bf16_kernel<5, false, false, true, E>), dim3(p.n_split, n_kv, 1),
+      auto kern = stream_keys(p.ntiles) ? attn_bf16_kernel<5, false, false, true, E, true>
+                                        : attn_bf16_kernel<5, false, false, true, E, false>;
+      hipLaunchKernelGGL(kern, dim3(p.n_split, n_kv, 1),
                          dim3(Bf16Cfg<5>::kThreads), 0, st, static_cast<const bf16_t*>(qa), static_cast<bf16_t*>(k),
                          static_cast<bf16_t*>(v), static_cast<bf16_t*>(oa), static_cast<PT*>(ws_o), ws_ml, qc, kv_c,
                          group, k_hs, v_hs,

@@ -10,7 +10,8 @@
 // waves, two tiles in flight) or the decode key split's (four waves, three
 // tiles in flight). Tiles go to workgroups either as one contiguous chunk per
 // workgroup (the attention kernels' split of a head's key range) or dealt
-// round-robin. Nothing is written except one word per workgroup under a
+// round-robin, with the default or the non-temporal load policy (the
+// attention kernels stream long key ranges non-temporally). Nothing is written except one word per workgroup under a
 // condition that the data never meets, which keeps the loads live.
 #include <climits>
 
@@ -40,7 +41,7 @@ stream_regs_kernel(const uint4* __restrict__ src, int ntiles, int per, int n_wg,
   if (acc == kNever) sink[b] = acc;
 }
 
-template <int WAVES, int AHEAD, bool RR>
+template <int WAVES, int AHEAD, bool RR, bool NTL = false>
 __global__ void __launch_bounds__(64 * WAVES)
 stream_lds_kernel(const char* __restrict__ ha, const char* __restrict__ hb, int ntiles, int per, int n_wg,
                   uint32_t* __restrict__ sink) {
@@ -63,8 +64,8 @@ stream_lds_kernel(const char* __restrict__ ha, const char* __restrict__ hb, int 
     for (int j = 0; j < kSegs; ++j) {
       const int seg = w * kSegs + j;
       const uint32_t off = (uint32_t)(seg * 1024 + lane * 16);
-      lds_dma16_sbase(a, off, dst0 + seg * 1024);
-      lds_dma16_sbase(c, off, dst0 + kHalf + seg * 1024);
+      lds_dma16_sbase<NTL>(a, off, dst0 + seg * 1024);
+      lds_dma16_sbase<NTL>(c, off, dst0 + kHalf + seg * 1024);
     }
   };
 #pragma unroll
@@ -93,12 +94,12 @@ using namespace stdhip;
 extern "C" int std_stream_read(const void* src, size_t bytes, int mode, int n_workgroups, uint32_t* sink,
                                void* stream) {
   if (!src || !sink) return STD_E_NULL;
-  if (mode < 0 || mode > 5) return STD_E_SHAPE;
+  if (mode < 0 || mode > 7) return STD_E_SHAPE;
   if (bytes == 0 || bytes % kTileBytes != 0 || bytes / kTileBytes > (size_t)INT_MAX) return STD_E_SHAPE;
   if (n_workgroups < 1 || n_workgroups > 65535) return STD_E_SHAPE;
   if (!aligned16(src)) return STD_E_ALIGN;
   const int ntiles = (int)(bytes / kTileBytes);
-  const bool rr = (mode & 1) != 0;
+  const bool rr = (mode & 1) != 0 || mode == 6;
   if (rr ? n_workgroups > ntiles : ntiles % n_workgroups != 0) return STD_E_SHAPE;
   const int per = rr ? 0 : ntiles / n_workgroups;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -126,9 +127,17 @@ extern "C" int std_stream_read(const void* src, size_t bytes, int mode, int n_wo
       hipLaunchKernelGGL((stream_lds_kernel<4, 4, false>), grid, dim3(256), 0, st, a, b, ntiles, per, n_workgroups,
                          sink);
       break;
-    default:
+    case 5:
       hipLaunchKernelGGL((stream_lds_kernel<4, 4, true>), grid, dim3(256), 0, st, a, b, ntiles, per, n_workgroups,
                          sink);
+      break;
+    case 6:
+      hipLaunchKernelGGL((stream_lds_kernel<8, 3, true, true>), grid, dim3(512), 0, st, a, b, ntiles, per,
+                         n_workgroups, sink);
+      break;
+    default:
+      hipLaunchKernelGGL((stream_lds_kernel<4, 4, true, true>), grid, dim3(256), 0, st, a, b, ntiles, per,
+                         n_workgroups, sink);
       break;
   }
   return launch_status();

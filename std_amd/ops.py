@@ -795,6 +795,8 @@ STREAM_MODES = {
     3: "LDS DMA ring (verify schedule), tiles round-robin",
     4: "LDS DMA ring (decode key split: 4 waves, 3 tiles in flight), contiguous chunk per workgroup",
     5: "LDS DMA ring (decode key split), tiles round-robin",
+    6: "LDS DMA ring (verify schedule), tiles round-robin, non-temporal loads",
+    7: "LDS DMA ring (decode key split), tiles round-robin, non-temporal loads",
 }
 
 
