@@ -126,3 +126,48 @@ def test_c5_first_divergence_from_dense_ar(c5):
         div = first_divergence(std_tokens, ar_tokens)
         print(f"[c5] first divergence STD vs AR: {div} (random weights; reported, not asserted)", flush=True)
         assert std_tokens[0] == ar_tokens[0], "both decoders start from the prefill's argmax token"
+
+
+def test_c5_shape_full_selection_accepts_every_draft_under_graph_replay():
+    """The 7B-shaped decoder in fp32 on a 896 visual + 128 text prompt with
+    K+text 1024: the selection keeps every visual position, the compact cache
+    equals the dense cache, so every draft token is accepted. This exercises
+    full-length rollbacks (a = gamma) at the real layer shapes in
+    graph-replayed rounds: each round's acceptance, bonus and rolled-back
+    lengths match the oracle, graph rounds equal eager rounds, and STD equals
+    dense AR token for token."""
+    cfg = DecoderConfig.qwen25vl_7b()
+    model = RandomDecoder(cfg, dev(), torch.float32, seed=5011)
+    gen = torch.Generator().manual_seed(5011)
+    n_vis, n_text, new = 896, 128, 30
+    ids = torch.cat([torch.full((n_vis,), cfg.video_token_id),
+                     torch.randint(0, 151643, (n_text,), generator=gen)]).view(1, -1)
+    inputs = {"input_ids": ids.to(dev()), "visual_embeds": torch.randn(n_vis, cfg.hidden_size, generator=gen).to(dev())}
+    tokens = {}
+    for use_graphs in (False, True):
+        rounds = []
+
+        def hook(info):
+            logits = info["logits"].float().cpu().numpy()
+            a, bonus, _ = ref_accept.verify_accept(logits, info["draft"], info["has_pending"], info["dense_next"])
+            want_len = ref_accept.rollback_lengths(info["dense_cached_len"], info["n_pending"],
+                                                   info["sparse_prev_len"], a)
+            rounds.append(dict(got=(info["accept_len"], info["bonus"], info["lengths"]), want=(a, bonus, want_len),
+                               replayed=info["replayed"]))
+
+        announce(f"c5 shape fp32, full selection, {new} tokens, use_graphs={use_graphs}")
+        res, sel = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=new,
+                                         gamma=GAMMA, target_k_plus_text=TARGET, ignore_eos=True,
+                                         use_graphs=use_graphs, round_hook=hook)
+        assert sel.k == n_vis and sel.compact_len == n_vis + n_text
+        assert res.accept_lengths == res.proposed_lengths and res.acceptance_rate == 1.0
+        _assert_rounds(rounds)
+        assert all(r["got"][0] == GAMMA for r in rounds), "expected full-length accepts"
+        if use_graphs:
+            assert any(r["replayed"] for r in rounds)
+        tokens[use_graphs] = res.output_ids[0, -res.generate_len:].cpu()
+    assert torch.equal(tokens[False], tokens[True])
+    announce("c5 shape fp32: dense AR decode")
+    ar = ar_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=new,
+                              ignore_eos=True, use_graphs=True)
+    assert first_divergence(tokens[True], ar.output_ids[0, -ar.generate_len:].cpu()) is None
