@@ -581,9 +581,11 @@ def main():
         "salient_selected_frac": salient_frac_selected,
         "select_compact_ms_first_call": round(select_ms_first, 3),
         "roofline": {
-            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false, false, {e}> split + "
-                      "attn_merge_kernel<{e}, _Float16> merge)".format(
-                          e="_Float16" if w.dtype == torch.float16 else "unsigned short"),
+            "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false, false, {e}, {nt}> split + "
+                      "attn_merge_kernel<{e}, {pt}> merge)".format(
+                          e="_Float16" if w.dtype == torch.float16 else "unsigned short",
+                          pt="float" if w.dtype == torch.float16 else "_Float16",
+                          nt="true" if (P + Q + 63) // 64 >= 128 else "false"),
             "bound": "hbm",
             "achieved": round(verify_gbps, 1),
             "peak": HBM_PEAK_GBPS,
@@ -782,6 +784,7 @@ def _phase_summary(st, mt, n_wg, n_merge):
     loop_end = us(st[:, 43])
     end = us(np.maximum(st[:, 47], st[:, 45]))
     r = {"workgroups": int(n_wg), "tiles_per_wg": [int(ntl.min()), int(ntl.max())],
+         "slowest_wg": int(np.argmax(end)), "first_tile_slowest_wg": float(first[int(np.argmax(end))]),
          "entry_spread": float(entry.max()), "first_tile_median": float(np.median(first)),
          "first_tile_max": float(first.max()), "step_median": float(np.nanmedian(steps)) if n_wg and (ntl > 2).any()
          else None, "loop_end_median": float(np.median(loop_end)), "output_stores_median": float(np.median(end - loop_end)),
@@ -804,7 +807,9 @@ def run_phases(args) -> None:
     the library (libstdhip_stamps.so: the same kernels with s_memrealtime
     stamps at each workgroup's phases; build it with `python -m std_amd.build
     --stamps`). Each case is 28 launches captured in one HIP graph, as in the
-    c4 bench; after each replay the stamps of its last launch are read. Prints
+    c4 bench (the draft both plain and with the new row appended by the
+    launch, as the round runs it); after each replay the stamps of its last
+    launch are read. Prints
     one JSON line per case (medians over replays, microseconds from the first
     workgroup's entry) and one summary line."""
     import ctypes
@@ -832,6 +837,10 @@ def run_phases(args) -> None:
     qd = torch.randn(L, 1, Hq, 1, D, generator=gen, device=dev).to(torch.bfloat16)
     sk = kc[:, :, :, 5000:5000 + S].contiguous()
     sv = vc[:, :, :, 5000:5000 + S].contiguous()
+    ska = kc[:, :, :, 5000:5000 + S + 64].contiguous()       # room for the appended row
+    sva = vc[:, :, :, 5000:5000 + S + 64].contiguous()
+    nk = torch.randn(L, 1, Hkv, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    nv = torch.randn(L, 1, Hkv, 1, D, generator=gen, device=dev).to(torch.bfloat16)
     vo, do = torch.empty_like(qv), torch.empty_like(qd)
     def n_wg(rows, kv):
         return lib.std_attn_split_count(Hkv, rows, kv, _lib.STD_BF16) * Hkv
@@ -843,6 +852,9 @@ def run_phases(args) -> None:
         "dense_decode": (lambda l: ops.gqa_decode(qd[l], kc[l][:, :, :P], vc[l][:, :, :P], out=do[l]), n_wg(7, P),
                          7 * Hkv),
         "draft": (lambda l: ops.gqa_decode(qd[l], sk[l], sv[l], out=do[l]), n_wg(7, S), 7 * Hkv),
+        # the draft step as the c4 round runs it: the new row appended by the attention launch itself
+        "draft_append": (lambda l: ops.gqa_decode_append(qd[l], ska[l], sva[l], nk[l], nv[l], S, out=do[l]),
+                         n_wg(7, S), 7 * Hkv),
     }
     stream = torch.cuda.current_stream()
     out = {}
