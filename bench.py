@@ -767,10 +767,12 @@ def run_gemv(args) -> None:
                       "results": results}))
 
 
-def _phase_summary(st, mt, n_wg, n_merge):
+def _phase_summary(st, mt, n_wg, n_merge, merge_rows=None):
     """Phases of one split launch and its merge launch from the timing build's
     stamps (100 MHz ticks; see attention.hip): times in us from the first
-    workgroup's entry."""
+    workgroup's entry. merge_rows = (grid x, rows): the merge launch also runs
+    the collector finish, whose blocks are those with x >= rows; their span is
+    reported apart from the row merges'."""
     import numpy as np
 
     st = st.astype(np.int64).reshape(-1, 48)[:n_wg]
@@ -799,6 +801,13 @@ def _phase_summary(st, mt, n_wg, n_merge):
         r["gap_split_end_to_merge"] = float(us(mt[:, 0].min()) - end.max())
         r["merge_span"] = float(us(mt[:, 1].max()) - us(mt[:, 0].min()))
         r["merge_end"] = float(us(mt[:, 1].max()))
+        if merge_rows is not None:
+            gx, rows = merge_rows
+            is_row = (np.arange(n_merge) % gx) < rows
+            r["merge_rows_end"] = float(us(mt[is_row, 1].max()))
+            r["coll_finish_first_entry"] = float(us(mt[~is_row, 0].min()))
+            r["coll_finish_end_median"] = float(np.median(us(mt[~is_row, 1])))
+            r["coll_finish_end"] = float(us(mt[~is_row, 1].max()))
     return r
 
 
@@ -842,13 +851,22 @@ def run_phases(args) -> None:
     nk = torch.randn(L, 1, Hkv, 1, D, generator=gen, device=dev).to(torch.bfloat16)
     nv = torch.randn(L, 1, Hkv, 1, D, generator=gen, device=dev).to(torch.bfloat16)
     vo, do = torch.empty_like(qv), torch.empty_like(qd)
+    V = P - 128                                   # visual keys [0, V): the collector's range at c4
+    cs = torch.empty(L, Hkv, V, dtype=torch.float32, device=dev)
+    n_vtiles = -(-V // 64)                        # 64-key tiles holding visual keys
+    n_coll_blocks = -(-n_vtiles // 16)            # collector finish blocks per KV head (1024 keys each)
+
     def n_wg(rows, kv):
         return lib.std_attn_split_count(Hkv, rows, kv, _lib.STD_BF16) * Hkv
 
-    # (launch of layer l, split workgroups, merge blocks)
+    # (launch of layer l, split workgroups, merge blocks[, (merge grid x, merge rows)])
     cases = {
         "verify": (lambda l: ops.verify_attention(qv[l], kc[l][:, :, :KV], vc[l][:, :, :KV], out=vo[l]),
                    n_wg(7 * Q, KV), 7 * Q * Hkv),
+        # the same verify carrying the visual-attention collector (its merge launch also finishes the scores)
+        "verify_collect": (lambda l: ops.verify_attention_collect(qv[l], kc[l][:, :, :KV], vc[l][:, :, :KV], 0, V,
+                                                                  kv_len=KV, out=vo[l], scores=cs[l]),
+                           n_wg(7 * Q, KV), (7 * Q + n_coll_blocks) * Hkv, (7 * Q + n_coll_blocks, 7 * Q)),
         "dense_decode": (lambda l: ops.gqa_decode(qd[l], kc[l][:, :, :P], vc[l][:, :, :P], out=do[l]), n_wg(7, P),
                          7 * Hkv),
         "draft": (lambda l: ops.gqa_decode(qd[l], sk[l], sv[l], out=do[l]), n_wg(7, S), 7 * Hkv),
@@ -858,7 +876,7 @@ def run_phases(args) -> None:
     }
     stream = torch.cuda.current_stream()
     out = {}
-    for name, (fn, n_wg, n_merge) in cases.items():
+    for name, (fn, n_wg, n_merge, *mrows) in cases.items():
         def body():
             for l in range(L):
                 fn(l)
@@ -884,7 +902,7 @@ def run_phases(args) -> None:
             mt = np.zeros(8192 * 2, dtype=np.uint64)
             _lib.check("std_phase_stamps", lib.std_phase_stamps(st.ctypes.data, 0, st.size))
             _lib.check("std_phase_stamps", lib.std_phase_stamps(mt.ctypes.data, 1, mt.size))
-            r = _phase_summary(st, mt, n_wg, n_merge if n_wg > Hkv else 0)
+            r = _phase_summary(st, mt, n_wg, n_merge if n_wg > Hkv else 0, mrows[0] if mrows else None)
             r["per_launch_us"] = e0.elapsed_time(e1) * 1e3 / L
             reps.append(r)
         med = {}
@@ -900,8 +918,9 @@ def run_phases(args) -> None:
         print(json.dumps({"case": name, **med}), flush=True)
         del graph
     print(json.dumps({"metric": "per-phase timing of the c4 attention launches (timing build)", "n_gpus": 1,
-                      "config": {"workload": "c4 shapes: verify 70 rows x 131082 keys, dense decode 7 rows x 131072 "
-                                             "keys, draft 7 rows x 1034 keys; 28 launches per graph"},
+                      "config": {"workload": "c4 shapes: verify 70 rows x 131082 keys (also with the collector over 130944 "
+                                             "visual keys), dense decode 7 rows x 131072 keys, draft 7 rows x 1034 "
+                                             "keys; 28 launches per graph"},
                       "cases": sorted(out)}), flush=True)
 
 

@@ -10,6 +10,9 @@ namespace stdhip {
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory
 // operations of this wave are outstanding, leaving the other counters alone.
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// s_waitcnt immediate that waits for this wave's LDS (and scalar memory)
+// operations only, leaving vector-memory loads such as the DMA ring in flight.
+constexpr int waitcnt_lgkm0() { return 15 | (3 << 14) | (7 << 4); }
 
 // One wave-wide global_load_lds_dwordx4: lane i copies 16 bytes from
 // sbase + voff (a wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane
