@@ -855,6 +855,8 @@ def run_phases(args) -> None:
     cs = torch.empty(L, Hkv, V, dtype=torch.float32, device=dev)
     n_vtiles = -(-V // 64)                        # 64-key tiles holding visual keys
     n_coll_blocks = -(-n_vtiles // 16)            # collector finish blocks per KV head (1024 keys each)
+    # its row-merge blocks per KV head: one per row beyond 32 splits per head, else four rows each
+    n_row_blocks = 7 * Q if lib.std_attn_split_count(Hkv, 7 * Q, KV, _lib.STD_BF16) > 32 else -(-7 * Q // 4)
 
     def n_wg(rows, kv):
         return lib.std_attn_split_count(Hkv, rows, kv, _lib.STD_BF16) * Hkv
@@ -866,7 +868,8 @@ def run_phases(args) -> None:
         # the same verify carrying the visual-attention collector (its merge launch also finishes the scores)
         "verify_collect": (lambda l: ops.verify_attention_collect(qv[l], kc[l][:, :, :KV], vc[l][:, :, :KV], 0, V,
                                                                   kv_len=KV, out=vo[l], scores=cs[l]),
-                           n_wg(7 * Q, KV), (7 * Q + n_coll_blocks) * Hkv, (7 * Q + n_coll_blocks, 7 * Q)),
+                           n_wg(7 * Q, KV), (n_row_blocks + n_coll_blocks) * Hkv, (n_row_blocks + n_coll_blocks,
+                                                                                   n_row_blocks)),
         "dense_decode": (lambda l: ops.gqa_decode(qd[l], kc[l][:, :, :P], vc[l][:, :, :P], out=do[l]), n_wg(7, P),
                          7 * Hkv),
         "draft": (lambda l: ops.gqa_decode(qd[l], sk[l], sv[l], out=do[l]), n_wg(7, S), 7 * Hkv),

@@ -307,18 +307,38 @@ __device__ __forceinline__ f32x4 load_part(const half_t* p) {
   return __builtin_convertvector(*reinterpret_cast<const half4_t*>(p), f32x4);
 }
 
-// Standalone merge: grid (R, n_kv), block kMergeThreads = 8 split groups x
-// 32 float4 lanes of the head dim. Every load is issued up front (a thread's
-// first kMergePrefetch partials together with the (m, l) statistics), so the
-// kernel costs about one memory round trip. Group sg sums splits sg, sg + 8,
-// ... in order and the eight group sums are added in group order, so the
-// result is deterministic.
+// Cross-lane max and sum of lanes l and l ^ 16 (xor16) or l and l ^ 32
+// (xor32) through v_permlane16/32_swap: both lanes get (the value of the one
+// with the bit clear) op (the value of the one with the bit set).
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+
+// Merge of the split partials, block form (more than kWaveMergeMax splits):
+// one 256-thread block per row, 8 split groups x 32 float4 lanes of the head
+// dim. Every load is issued up front (a thread's first kMergePrefetch
+// partials together with the (m, l) statistics), so the kernel costs about
+// one memory round trip. Group sg sums splits sg, sg + 8, ... in order and the
+// eight group sums are added in group order, so the result is deterministic.
 constexpr int kMergeGroups = 8;
 constexpr int kMergeThreads = kMergeGroups * (D / 4);
 constexpr int kMergePrefetch = 8;
 
 template <typename T, typename PT>
-__device__ __forceinline__ void merge_row(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
+__device__ __forceinline__ void merge_row_block(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
                                           T* __restrict__ out, int n_split, int q_len, int group, long long out_bs,
                                           int n_kv, int r, int g) {
   __shared__ float wts[kMaxSplit];
@@ -403,14 +423,90 @@ __device__ __forceinline__ void merge_row(const PT* __restrict__ ws_o, const flo
   }
 }
 
-template <typename T, typename PT>
-__global__ void __launch_bounds__(kMergeThreads)
+// Merge, wave form (at most kWaveMergeMax splits: the draft's one-tile
+// splits, short verifies): one wave per row. Lane (c, h) = (lane & 31,
+// lane >> 5) owns columns 4c .. 4c + 3 and the splits h, h + 2, ..., h + 2(J-1)
+// and issues all of their loads before the first use; loads past the last
+// split fall outside a buffer resource bounded at it, which returns zeros
+// without a memory access (re-reading the last split instead made the loads of
+// one line wait on each other: 17 splits at J = 16 took the 1034-key draft from
+// 7.4 to 7.8 us per layer). The two half-waves combine through one lane swap:
+// no LDS, no barrier (1024-key draft, 16 splits: 7.19 -> 6.49 us per layer
+// against the block form). Each half adds its splits in ascending order and
+// the row is half 0's sum plus half 1's, so the result is deterministic.
+constexpr int kWaveMergeMax = 32;
+// J = splits per half-wave: ceil(n_split / 2) rounded up to an instantiated
+// count (the draft's 1024-1033 keys give 16 or 17 splits: J = 8 or 9).
+inline int merge_j(int n_split) {
+  return n_split <= 8 ? 4 : n_split <= 16 ? 8 : n_split <= 18 ? 9 : n_split <= 24 ? 12 : 16;
+}
+constexpr int kBufWord3 = 0x00020000;     // raw buffer resource word 3 (gfx9 family)
+
+template <typename T, typename PT, int J>
+__device__ __forceinline__ void merge_row_wave(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
+                                               T* __restrict__ out, int n_split, int q_len, int group,
+                                               long long out_bs, int n_kv, int r, int g, int bz, int lane) {
+  static_assert(2 * J <= kWaveMergeMax, "one pass covers every split");
+  const int c = lane & 31, h = lane >> 5;
+  const int R = group * q_len;
+  out += bz * out_bs;
+  const long long base = ((long long)bz * n_kv + g) * n_split * R + r;
+  const uint32_t step_b = (uint32_t)(R * D * sizeof(PT));
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(ws_o + base * D), (short)0, (int)((n_split - 1) * step_b + D * sizeof(PT)), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(ws_ml + base), (short)0, (int)((n_split - 1) * R * 8 + 8), kBufWord3);
+  float2 ml[J];
+  f32x4 pv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t sp = h + 2 * j;
+    ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, sp * R * 8, 0, 0));
+    if constexpr (sizeof(PT) == 4)
+      pv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, sp * step_b + 16 * c, 0, 0));
+    else
+      pv[j] = __builtin_convertvector(
+          __builtin_bit_cast(half4_t, __builtin_amdgcn_raw_buffer_load_b64(ro, sp * step_b + 8 * c, 0, 0)), f32x4);
+  }
+  float M = -1e30f, L = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    if (h + 2 * j < n_split) M = fmaxf(M, ml[j].x);
+  M = xor32_max(M);
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    if (h + 2 * j < n_split) {
+      const float e = fast_exp2(ml[j].x - M);
+      L += ml[j].y * e;
+      o += pv[j] * e;
+    }
+  L = xor32_sum(L);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = xor32_sum(o[e]);
+  if (h == 0) {
+    const int hl = r / q_len, i = r - hl * q_len;
+    T* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(o[e] / L);
+  }
+}
+
+// grid (R, n_kv, n_batch): block (r, g, b) merges row r of KV head g of
+// problem b; J == 0: the block form (kMergeThreads threads), otherwise the
+// wave form (one wave).
+template <typename T, typename PT, int J>
+__global__ void __launch_bounds__(J == 0 ? kMergeThreads : 64)
 attn_merge_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
                   int n_split, int q_len, int group, long long out_bs, int n_kv) {
 #if STD_PHASE_STAMPS
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
 #endif
-  merge_row<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y);
+  if constexpr (J == 0)
+    merge_row_block<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y);
+  else
+    merge_row_wave<T, PT, J>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y,
+                             blockIdx.z, threadIdx.x);
 #if STD_PHASE_STAMPS
   const int b = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
   if (threadIdx.x == 0 && b < kStampMerge) {
@@ -531,9 +627,12 @@ __device__ __forceinline__ void coll_finish(const float* __restrict__ logits, co
 }
 
 // The verify merge and the collector finish in one launch: grid
-// (n_rows + n_col_blocks, n_kv); blocks x < n_rows merge attention row x (none
-// when the verify ran as one split), the others finish 1024 visual keys each.
-template <typename T, typename PT>
+// (n_row_blocks + n_col_blocks, n_kv). The first n_row_blocks blocks merge
+// the attention rows (none when the verify ran as one split): one row per
+// block in the block form (J == 0, n_row_blocks = n_rows), otherwise one per
+// wave (n_row_blocks = (n_rows + 3) / 4, row 4x + w). The other blocks finish
+// 1024 visual keys each.
+template <typename T, typename PT, int J>
 __global__ void __launch_bounds__(kMergeThreads)
 merge_coll_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml, T* __restrict__ out,
                   int n_split, int q_len, int group, int n_rows, const float* __restrict__ logits,
@@ -542,10 +641,20 @@ merge_coll_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
 #if STD_PHASE_STAMPS
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
 #endif
-  if ((int)blockIdx.x < n_rows)
-    merge_row<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
-  else
-    coll_finish(logits, stats, co, q_len, n_split, n_vtiles, vis_begin, vis_end, blockIdx.x - n_rows, blockIdx.y);
+  const int n_row_blocks = J == 0 ? n_rows : (n_rows + 3) / 4;
+  if ((int)blockIdx.x < n_row_blocks) {
+    if constexpr (J == 0) {
+      merge_row_block<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
+    } else {
+      const int r = 4 * blockIdx.x + (threadIdx.x >> 6);
+      if (r < n_rows)
+        merge_row_wave<T, PT, J>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, r, blockIdx.y, 0,
+                                 threadIdx.x & 63);
+    }
+  } else {
+    coll_finish(logits, stats, co, q_len, n_split, n_vtiles, vis_begin, vis_end, blockIdx.x - n_row_blocks,
+                blockIdx.y);
+  }
 #if STD_PHASE_STAMPS
   const int b = blockIdx.y * gridDim.x + blockIdx.x;
   if (threadIdx.x == 0 && b < kStampMerge) {
@@ -638,22 +747,6 @@ template <> struct Elem<f16_t> {
   }
 };
 
-__device__ __forceinline__ float xor16_max(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-}
-__device__ __forceinline__ float xor32_max(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-}
-__device__ __forceinline__ float xor16_sum(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
-}
-__device__ __forceinline__ float xor32_sum(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
-}
 
 // Row-owner layout: compute wave w < NT owns query rows [16w, 16w + 16) of the
 // launch's R rows and processes all 64 keys of every tile, so at the end of
@@ -1639,6 +1732,26 @@ void launch_h16(const void* q, void* k, void* v, void* out, int q_len, int kv_le
                      GatherDev{ga.status, ga.idx_hs, ga.n_idx, ga.dense_rows, ga.k, ga.v, ga.k_hs, ga.v_hs}, ga.idx);
 }
 
+// The merge launch: the wave form up to kWaveMergeMax splits, the block
+// form beyond.
+template <typename T, typename PT>
+void launch_merge(const void* ws_o, const float2* ws_ml, void* out, int n_split, int q_len, int group, long long out_bs,
+                  int n_kv, int R, int n_batch, hipStream_t st) {
+  const dim3 grid(R, n_kv, n_batch);
+  const PT* o = static_cast<const PT*>(ws_o);
+  T* y = static_cast<T*>(out);
+  if (n_split > kWaveMergeMax) {
+    hipLaunchKernelGGL((attn_merge_kernel<T, PT, 0>), grid, dim3(kMergeThreads), 0, st, o, ws_ml, y, n_split, q_len,
+                       group, out_bs, n_kv);
+    return;
+  }
+  const int j = merge_j(n_split);
+  auto kern = j == 4 ? attn_merge_kernel<T, PT, 4> : j == 8 ? attn_merge_kernel<T, PT, 8>
+            : j == 9 ? attn_merge_kernel<T, PT, 9> : j == 12 ? attn_merge_kernel<T, PT, 12>
+                     : attn_merge_kernel<T, PT, 16>;
+  hipLaunchKernelGGL(kern, grid, dim3(64), 0, st, o, ws_ml, y, n_split, q_len, group, out_bs, n_kv);
+}
+
 template <int NT>
 int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, int kv_len, int group,
               long long k_hs, long long v_hs, float scale, int dtype, void* ws, const void* nk, const void* nv,
@@ -1671,17 +1784,11 @@ int launch_nt(const void* q, void* k, void* v, void* out, int n_kv, int q_len, i
   int s = launch_status();
   if (s != 0 || p.n_split == 1) return s;
   if (dtype == STD_BF16)
-    hipLaunchKernelGGL((attn_merge_kernel<bf16_t, PartT<NT, bf16_t>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0,
-                       st, static_cast<const PartT<NT, bf16_t>*>(ws_o), ws_ml, static_cast<bf16_t*>(out), p.n_split, q_len,
-                       group, bs.o, n_kv);
+    launch_merge<bf16_t, PartT<NT, bf16_t>>(ws_o, ws_ml, out, p.n_split, q_len, group, bs.o, n_kv, R, n_batch, st);
   else if (dtype == STD_F16)
-    hipLaunchKernelGGL((attn_merge_kernel<f16_t, PartT<NT, f16_t>>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0,
-                       st, static_cast<const PartT<NT, f16_t>*>(ws_o), ws_ml, static_cast<f16_t*>(out), p.n_split, q_len,
-                       group, bs.o, n_kv);
+    launch_merge<f16_t, PartT<NT, f16_t>>(ws_o, ws_ml, out, p.n_split, q_len, group, bs.o, n_kv, R, n_batch, st);
   else
-    hipLaunchKernelGGL((attn_merge_kernel<float, float>), dim3(R, n_kv, n_batch), dim3(kMergeThreads), 0, st,
-                       static_cast<const float*>(ws_o), ws_ml, static_cast<float*>(out), p.n_split, q_len, group,
-                       bs.o, n_kv);
+    launch_merge<float, float>(ws_o, ws_ml, out, p.n_split, q_len, group, bs.o, n_kv, R, n_batch, st);
   return launch_status();
 }
 
@@ -1865,9 +1972,15 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
                          BatchStrides{0, 0, 0, 0, 0}, len_dev, ca, nullptr);
       const int s = launch_status();
       if (s != 0) return s;
-      hipLaunchKernelGGL((merge_coll_kernel<E, PT>), dim3(n_rows + (cl.n_vtiles + 15) / 16, n_kv),
-                         dim3(kMergeThreads), 0, st, static_cast<const PT*>(ws_o), ws_ml, static_cast<E*>(oa), p.n_split, qc, group, n_rows, ca.logits, ca.stats, co,
-                         cl.n_vtiles, vis_begin, vis_end);
+      const bool wave = p.n_split <= kWaveMergeMax;
+      const int mj = wave ? merge_j(p.n_split) : 0;
+      const dim3 mgrid((wave ? (n_rows + 3) / 4 : n_rows) + (cl.n_vtiles + 15) / 16, n_kv);
+      auto mkern = mj == 0 ? merge_coll_kernel<E, PT, 0> : mj == 4 ? merge_coll_kernel<E, PT, 4>
+                 : mj == 8 ? merge_coll_kernel<E, PT, 8> : mj == 9 ? merge_coll_kernel<E, PT, 9>
+                 : mj == 12 ? merge_coll_kernel<E, PT, 12> : merge_coll_kernel<E, PT, 16>;
+      hipLaunchKernelGGL(mkern, mgrid, dim3(kMergeThreads), 0, st, static_cast<const PT*>(ws_o), ws_ml,
+                         static_cast<E*>(oa), p.n_split, qc, group, n_rows, ca.logits, ca.stats, co, cl.n_vtiles,
+                         vis_begin, vis_end);
       return launch_status();
     };
     const int s = dtype == STD_BF16 ? run(bf16_t{}) : run(f16_t{});
