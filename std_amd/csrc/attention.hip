@@ -327,102 +327,6 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(a[0]) + __uint_as_float(a[1]);
 }
 
-// Merge of the split partials, block form (more than kWaveMergeMax splits):
-// one 256-thread block per row, 8 split groups x 32 float4 lanes of the head
-// dim. Every load is issued up front (a thread's first kMergePrefetch
-// partials together with the (m, l) statistics), so the kernel costs about
-// one memory round trip. Group sg sums splits sg, sg + 8, ... in order and the
-// eight group sums are added in group order, so the result is deterministic.
-constexpr int kMergeGroups = 8;
-constexpr int kMergeThreads = kMergeGroups * (D / 4);
-constexpr int kMergePrefetch = 8;
-
-template <typename T, typename PT>
-__device__ __forceinline__ void merge_row_block(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
-                                          T* __restrict__ out, int n_split, int q_len, int group, long long out_bs,
-                                          int n_kv, int r, int g) {
-  __shared__ float wts[kMaxSplit];
-  __shared__ float red[2][kMergeThreads / 64];
-  __shared__ f32x4 part[kMergeGroups][D / 4];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int d4 = tid & (D / 4 - 1), sg = tid / (D / 4);
-  const int R = group * q_len;
-  out += blockIdx.z * out_bs;
-  const long long base = ((long long)blockIdx.z * n_kv + g) * n_split * R + r;
-  const PT* col = ws_o + base * D + 4 * d4;
-  const long long step = (long long)R * D;
-  // Every load below is issued before the first use: splits past n_split
-  // re-read the last one and are masked after the load (a load under a
-  // condition would compile to a branch that waits for it).
-  f32x4 pre[kMergePrefetch];
-#pragma unroll
-  for (int j = 0; j < kMergePrefetch; ++j) pre[j] = load_part(col + min(sg + j * kMergeGroups, n_split - 1) * step);
-  constexpr int kMlPerThread = kMaxSplit / kMergeThreads;
-  float2 mls[kMlPerThread];
-#pragma unroll
-  for (int i = 0; i < kMlPerThread; ++i) mls[i] = ws_ml[base + (long long)min(tid + i * kMergeThreads, n_split - 1) * R];
-  float m = -1e30f;
-#pragma unroll
-  for (int i = 0; i < kMlPerThread; ++i) {
-    if (tid + i * kMergeThreads >= n_split) mls[i] = make_float2(-1e30f, 0.f);
-    m = fmaxf(m, mls[i].x);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-  if (lane == 0) red[0][wv] = m;
-  __syncthreads();
-  float M = red[0][0];
-#pragma unroll
-  for (int i = 1; i < kMergeThreads / 64; ++i) M = fmaxf(M, red[0][i]);
-  float l = 0.f;
-#pragma unroll
-  for (int i = 0; i < kMlPerThread; ++i) {
-    const int sp = tid + i * kMergeThreads;
-    if (sp < n_split) {
-      const float e = fast_exp2(mls[i].x - M);
-      wts[sp] = e;
-      l += mls[i].y * e;
-    }
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
-  if (lane == 0) red[1][wv] = l;
-  __syncthreads();
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < kMergePrefetch; ++j) {
-    const int sp = sg + j * kMergeGroups;
-    if (sp < n_split) o += pre[j] * wts[sp];
-  }
-  for (int s0 = kMergePrefetch * kMergeGroups; s0 < n_split; s0 += 4 * kMergeGroups) {
-    f32x4 v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int sp = s0 + sg + j * kMergeGroups;
-      v[j] = sp < n_split ? load_part(col + sp * step) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int sp = s0 + sg + j * kMergeGroups;
-      if (sp < n_split) o += v[j] * wts[sp];
-    }
-  }
-  part[sg][d4] = o;
-  __syncthreads();
-  if (sg == 0) {
-    float L = 0.f;
-#pragma unroll
-    for (int i = 0; i < kMergeThreads / 64; ++i) L += red[1][i];
-    f32x4 t = part[0][d4];
-#pragma unroll
-    for (int k = 1; k < kMergeGroups; ++k) t += part[k][d4];
-    const int hl = r / q_len, i = r - hl * q_len;
-    T* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * d4;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(t[e] / L);
-  }
-}
-
 // Merge, wave form (at most kWaveMergeMax splits: the draft's one-tile
 // splits, short verifies): one wave per row. Lane (c, h) = (lane & 31,
 // lane >> 5) owns columns 4c .. 4c + 3 and the splits h, h + 2, ..., h + 2(J-1)
@@ -489,6 +393,93 @@ __device__ __forceinline__ void merge_row_wave(const PT* __restrict__ ws_o, cons
     T* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(o[e] / L);
+  }
+}
+
+// Merge, block form (more than kWaveMergeMax splits: long verifies and dense
+// decodes): four waves per row, wave w taking the splits [w per, (w + 1) per)
+// with per = ceil(n_split / 4), in passes of 16 laid out as in the wave form
+// (buffer resources bounded at the wave's last split). Every wave first forms
+// the row's maximum over all splits from one (m, l) load per lane and a
+// 64-lane butterfly, so the four waves' sums share one scale; they are added
+// in wave order through LDS after a single barrier. All of a wave's first
+// pass goes out before the maximum is formed. (The previous form, eight split
+// groups sharing weights through LDS with three barriers, spanned 3.1 us for
+// the 128k verify's 280 rows.)
+constexpr int kMergeThreads = 256;
+
+template <typename T, typename PT>
+__device__ __forceinline__ void merge_row_block(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
+                                                T* __restrict__ out, int n_split, int q_len, int group,
+                                                long long out_bs, int n_kv, int r, int g) {
+  __shared__ f32x4 part[4][D / 4];
+  __shared__ float lpart[4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, h = lane >> 5;
+  const int R = group * q_len;
+  out += blockIdx.z * out_bs;
+  const long long base = ((long long)blockIdx.z * n_kv + g) * n_split * R + r;
+  const uint32_t step_b = (uint32_t)(R * D * sizeof(PT));
+  const int per = (n_split + 3) / 4;
+  const int s_beg = min(n_split, w * per), s_end = min(n_split, s_beg + per);
+  const int n_w = s_end - s_beg;
+  // this wave's splits (empty range: a resource of no records, every load zero)
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(ws_o + (base + (long long)s_beg * R) * D), (short)0,
+      n_w > 0 ? (int)((n_w - 1) * step_b + D * sizeof(PT)) : 0, kBufWord3);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(ws_ml + base + (long long)s_beg * R), (short)0, n_w > 0 ? (n_w - 1) * R * 8 + 8 : 0, kBufWord3);
+  // all of the row's (m, l) pairs, for the maximum
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)(ws_ml + base), (short)0,
+                                                                      (n_split - 1) * R * 8 + 8, kBufWord3);
+  constexpr int J = 8;
+  float2 ml[J];
+  f32x4 pv[J];
+  auto load = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t sp = s0 + h + 2 * j;           // relative to s_beg
+      ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, sp * R * 8, 0, 0));
+      if constexpr (sizeof(PT) == 4)
+        pv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, sp * step_b + 16 * c, 0, 0));
+      else
+        pv[j] = __builtin_convertvector(
+            __builtin_bit_cast(half4_t, __builtin_amdgcn_raw_buffer_load_b64(ro, sp * step_b + 8 * c, 0, 0)), f32x4);
+    }
+  };
+  load(0);
+  float M = -1e30f;
+  for (int s = lane; s < n_split; s += 64)
+    M = fmaxf(M, __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(ra, s * R * 8, 0, 0)).x);
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+  M = xor32_max(xor16_max(M));
+  float L = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < n_w; s0 += 2 * J) {
+    if (s0 > 0) load(s0);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (s0 + h + 2 * j < n_w) {
+        const float e = fast_exp2(ml[j].x - M);
+        L += ml[j].y * e;
+        o += pv[j] * e;
+      }
+  }
+  L = xor32_sum(L);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = xor32_sum(o[e]);
+  if (h == 0) part[w][c] = o;
+  if (lane == 0) lpart[w] = L;
+  __syncthreads();
+  if (w == 0 && h == 0) {
+    const f32x4 t = ((part[0][c] + part[1][c]) + part[2][c]) + part[3][c];
+    const float Lt = ((lpart[0] + lpart[1]) + lpart[2]) + lpart[3];
+    const int hl = r / q_len, i = r - hl * q_len;
+    T* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 4 * c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(t[e] / Lt);
   }
 }
 
