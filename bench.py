@@ -129,7 +129,7 @@ def main():
         sys.exit(2)
     import torch
 
-    from std_amd import ops
+    from std_amd import _lib, ops
     from std_amd.workloads import WORKLOADS, non_visual_positions, visual_positions
 
     if args.workload == "c5":
@@ -499,6 +499,11 @@ def main():
 
     draft_tokens_per_s = G * args.steps / elapsed
     draft_tokens_per_s_warm = G * args.steps / elapsed_warm
+    # the merge kernel's form: 0 = one block per row (more than 32 splits per KV head), else the one-wave
+    # form's splits per half-wave
+    n_split_verify = _lib.load_library().std_attn_split_count(Hkv, (Hq // Hkv) * Q, P + Q, _lib.STD_BF16)
+    merge_form = 0 if n_split_verify > 32 else next(j for j, top in ((4, 8), (8, 16), (9, 18), (12, 24), (16, 32))
+                                                     if n_split_verify <= top)
     traffic = None
     # counter passes are per element type (the committed ones are bf16)
     tsuffix = "_fp16" if w.dtype == torch.float16 else ""
@@ -582,10 +587,10 @@ def main():
         "select_compact_ms_first_call": round(select_ms_first, 3),
         "roofline": {
             "kernel": "verify attention, one layer (attn_bf16_kernel<5, false, false, false, {e}, {nt}> split + "
-                      "attn_merge_kernel<{e}, {pt}> merge)".format(
+                      "attn_merge_kernel<{e}, {pt}, {j}> merge)".format(
                           e="_Float16" if w.dtype == torch.float16 else "unsigned short",
                           pt="float" if w.dtype == torch.float16 else "_Float16",
-                          nt="true" if (P + Q + 63) // 64 >= 128 else "false"),
+                          nt="true" if (P + Q + 63) // 64 >= 128 else "false", j=merge_form),
             "bound": "hbm",
             "achieved": round(verify_gbps, 1),
             "peak": HBM_PEAK_GBPS,
