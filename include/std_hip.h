@@ -528,7 +528,7 @@ int std_verify_attn_collect_ex(const void* q, void* k_cache, void* v_cache,
  *             flight), each tile 16 KiB from either half of the buffer;
  *   mode 4/5: the decode key split's ring (four waves, three in flight);
  *   mode 6/7: modes 3 and 5 with non-temporal loads (the policy the attention
- *             kernels use for key ranges of 8192 keys and more).
+ *             kernels use for key ranges of 4096 keys and more).
  * Modes 0, 2 and 4 give each workgroup one contiguous chunk (the tile count
  * must divide by n_workgroups); modes 1, 3, 5, 6 and 7 deal tiles round-robin.
  * ------------------------------------------------------------------------ */

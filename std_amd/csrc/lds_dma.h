@@ -30,7 +30,7 @@ constexpr int waitcnt_lgkm0() { return 15 | (3 << 14) | (7 << 4); }
 // once, the lines are not kept for reuse in the caches, which leaves them to the
 // data that is (measured on MI355X: the 128k verify 55.9 -> 51.7 us, the 128k
 // dense decode 50.6 -> 46.1 us per layer); a cache that is read again soon
-// (the draft's compact cache between steps) keeps the default policy.
+// (the draft's 1024-key compact cache between steps) keeps the default policy.
 template <bool NTL = false>
 __device__ __forceinline__ void lds_dma16_sbase(const void* sbase, uint32_t voff, uint32_t lds_base) {
   // readfirstlane pins the wave-uniform operands to SGPRs even where the
