@@ -16,6 +16,7 @@
 // epilogue can also add the decoder's residual or apply the MLP's
 // silu(gate) * up, so those elementwise ops cost no launch of their own.
 #include "common.h"
+#include "lds_dma.h"
 
 namespace stdhip {
 namespace {
@@ -158,6 +159,138 @@ gemv_bf16_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __r
     for (int j = 0; j < kMat; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ld16(wr[j] + k), bv, acc[j], 0, 0, 0);
   }
   gemv_finish<WK, GATED, 16>(red, acc, wave, lane, n0, bias, residual, r_rs, y, y_rs, M, N);
+}
+
+// Weight streaming through LDS for one activation row and large weights (the
+// decode steps' gate/up, down and lm_head): each wave streams its K range of
+// the workgroup's 16 (gated: 2 x 16) weight rows HBM -> LDS through a private
+// ring of global_load_lds_dwordx4 with the non-temporal policy. The register
+// kernels' 16-byte lanes fetch each 128-byte line of a row in two load
+// instructions; a DMA instruction here moves whole lines of several rows, and
+// the stream read once leaves the caches to the data read again. No wave
+// waits for another until the epilogue: each issues, waits for and reads only
+// its own stages. Where the register kernels run four waves (gate/up,
+// lm_head) this kernel keeps their K split, MFMA order and epilogue and equals
+// them bit for bit; where they run two (down: 224 column blocks), two waves
+// per CU could not keep enough bytes in flight (33 us against 27.6 us even
+// with seven 4 KiB stages each), so eight waves split K here instead.
+// Measured at one row, graph-replayed on the 7B shapes: gate/up 50.7 -> 43.6
+// us, down 27.6 -> 24.0 us, lm_head 179 -> 161 us (a plain 271 MB read
+// through this kind of ring: 39.6-40.3 us).
+//
+// Stage: 16 rows x KS k (2 KS bytes per row) per weight row set; a DMA
+// instruction covers 1 KiB = 64 / C rows of C 16-byte chunks (C = KS / 8); the
+// chunk c of row r lives at chunk c ^ (r % C), so that the MFMA operand reads
+// (row ln, chunk 4u + lg) spread over the banks. NSTG ring slots per wave keep
+// NSTG - 1 stages in flight. The wave's slice of the activation row goes to
+// LDS by DMA ahead of the first stages.
+template <int WK> struct DmaCfg;
+template <> struct DmaCfg<4> { static constexpr int KS = 64, NSTG = 4; };
+template <> struct DmaCfg<8> { static constexpr int KS = 128, NSTG = 3; };
+
+// The activation slices of the WK waves (dynamic LDS; the rings are static).
+inline int gemv_dma_xs_bytes(int WK, int K) {
+  const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;
+  return WK * ((kw * 2 + 1023) / 1024) * 1024;
+}
+
+// s_waitcnt until at most n * PER vector-memory operations are outstanding
+// (n < MAXN, a run-time count turned into the instruction's immediate).
+template <int PER, int MAXN>
+__device__ __forceinline__ void wait_vm_stages(int n) {
+  if constexpr (MAXN > 0) {
+    if (n >= MAXN - 1) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((MAXN - 1) * PER));
+      return;
+    }
+    wait_vm_stages<PER, MAXN - 1>(n);
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+}
+
+template <int WK, bool GATED>
+__global__ void __launch_bounds__(64 * WK)
+gemv_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x,
+                const bf16_t* __restrict__ bias, const bf16_t* __restrict__ residual, long long r_rs,
+                bf16_t* __restrict__ y, int N, int K) {
+  constexpr int KS = DmaCfg<WK>::KS, NSTG = DmaCfg<WK>::NSTG;
+  constexpr int C = KS / 8;                      // 16-byte chunks per row of a stage
+  constexpr int RPI = 64 / C;                    // rows per DMA instruction
+  constexpr int IPM = 16 / RPI;                  // DMA instructions per row set and stage
+  constexpr int kMat = GATED ? 2 : 1;
+  constexpr int kMatB = 16 * KS * 2;
+  constexpr int kStageB = kMat * kMatB;
+  constexpr int kPer = kMat * IPM;               // DMA instructions per stage
+  __shared__ __align__(16) char rings[WK * NSTG * kStageB];
+  extern __shared__ __align__(16) char xs_all[];
+  __shared__ f32x4 red[kMat][WK][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;
+  const int k_begin = min(K, wave * kw), k_end = min(K, k_begin + kw);
+  const int nk = k_end - k_begin;               // a multiple of 32
+  const int nst = (nk + KS - 1) / KS;
+  const int xs_b = ((kw * 2 + 1023) / 1024) * 1024;
+  char* ring = rings + wave * NSTG * kStageB;
+  char* xs = xs_all + wave * xs_b;
+  // DMA lane roles: instruction i of a row set covers rows RPI i + lane / C;
+  // the lane's 16 bytes are physical chunk lane % C of that row, i.e. logical
+  // chunk lc[i] = (lane % C) ^ (row % C) (k 8 lc .. 8 lc + 7 of the stage);
+  // rows past N re-read row N - 1.
+  int row_b[IPM], lc[IPM];
+#pragma unroll
+  for (int i = 0; i < IPM; ++i) {
+    const int r = RPI * i + lane / C;
+    lc[i] = (lane % C) ^ (r % C);
+    row_b[i] = (min(n0 + r, N - 1) - n0) * (int)(w_rs * 2);
+  }
+  const char* wb = reinterpret_cast<const char*>(w + (long long)n0 * w_rs + k_begin);
+  auto issue = [&](int s) {
+    const uint32_t dst = lds_addr(ring + (s % NSTG) * kStageB);
+#pragma unroll
+    for (int j = 0; j < kMat; ++j)
+#pragma unroll
+      for (int i = 0; i < IPM; ++i) {
+        // k positions past the wave's range re-read its last 8 k (never used)
+        const int kk = min(s * KS + 8 * lc[i], nk - 8);
+        lds_dma16_sbase<true>(wb + (long long)j * N * w_rs * 2, (uint32_t)(row_b[i] + kk * 2),
+                              dst + j * kMatB + i * 1024);
+      }
+  };
+  // the activation slice [k_begin, k_end) of row 0, in 1 KiB DMA pieces
+  if (nk > 0) {
+    const char* xb = reinterpret_cast<const char*>(x + k_begin);
+    for (int b = 0; b < xs_b; b += 1024)
+      lds_dma16_sbase<false>(xb, (uint32_t)min(b + lane * 16, nk * 2 - 16), lds_addr(xs + b));
+  }
+  f32x4 acc[kMat];
+#pragma unroll
+  for (int j = 0; j < kMat; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < NSTG - 1 && s < nst; ++s) issue(s);
+  for (int s = 0; s < nst; ++s) {
+    // stages issued: 0 .. min(s + NSTG - 2, nst - 1); stage s must have landed
+    wait_vm_stages<kPer, NSTG - 1>(min(NSTG - 2, nst - 1 - s));
+    // slot (s + NSTG - 1) % NSTG last held stage s - 1, whose operands are in registers
+    if (s + NSTG - 1 < nst) issue(s + NSTG - 1);
+    const char* st = ring + (s % NSTG) * kStageB;
+#pragma unroll
+    for (int u = 0; u < KS / 32; ++u) {
+      const int kk = s * KS + 32 * u;
+      if (kk < nk) {
+        const bf16x8_t b = ln == 0 ? *reinterpret_cast<const bf16x8_t*>(xs + (kk + 8 * lg) * 2) : bf16x8_t{};
+#pragma unroll
+        for (int j = 0; j < kMat; ++j) {
+          const bf16x8_t a =
+              *reinterpret_cast<const bf16x8_t*>(st + j * kMatB + ln * (KS * 2) + (((4 * u + lg) ^ (ln % C)) << 4));
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+        }
+      }
+    }
+  }
+  gemv_finish<WK, GATED, 16>(red, acc, wave, lane, n0, bias, residual, r_rs, y, 0, 1, N);
 }
 
 // The gated projection at more than four rows (the ten-row verify step): one
@@ -438,6 +571,23 @@ inline int gemv_waves(int M, int n_rows, int K) {
   return K <= kShortMaxK && (n_rows + 15) / 16 >= 256 ? 4 : 2;
 }
 
+// One row over a weight of at least kDmaMinBytes goes through the LDS ring
+// (gemv_dma_kernel, four waves where gemv_waves picks four, else eight): the
+// decode steps' gate/up (271 MB), down (136 MB) and lm_head (1.09 GB) at the
+// 7B shapes; smaller weights (o, 26 MB) keep the register kernels, whose
+// single load round trip suits them. The waves' activation slices must fit
+// the dynamic LDS, and a wave's slice pieces plus its stages in flight the 63
+// outstanding vector-memory operations it can count.
+constexpr long long kDmaMinBytes = 64ll << 20;
+inline bool use_dma(int n_rows, int K, int wk, bool gated) {
+  if (wk == 2 && gated) return false;          // eight waves of two row sets would crowd the LDS
+  const int dk = wk == 4 ? 4 : 8;
+  const int kw = (((K + dk - 1) / dk) + 31) / 32 * 32;
+  const int in_flight = dk == 4 ? (DmaCfg<4>::NSTG - 1) * (gated ? 2 : 1) * 2 : (DmaCfg<8>::NSTG - 1) * 4;
+  return (long long)n_rows * K * 2 >= kDmaMinBytes && gemv_dma_xs_bytes(dk, K) <= (48 << 10) &&
+         (kw * 2 + 1023) / 1024 + in_flight <= 63;
+}
+
 template <bool GATED>
 int launch_gemv(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias, const void* residual,
                 long long r_rs, void* y, long long y_rs, int M, int N, int K, hipStream_t st) {
@@ -449,6 +599,18 @@ int launch_gemv(const void* x, long long x_rs, const void* w, long long w_rs, co
                        static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
   };
   static_assert((kShortMaxK / 4) / 32 <= kShortSteps, "four waves cover K in kShortSteps steps each");
+  if (M == 1 && use_dma(GATED ? 2 * N : N, K, wk, GATED)) {
+    const int dk = wk == 4 ? 4 : 8;                // use_dma admits a gated launch at four waves only
+    void (*kern)(const bf16_t*, long long, const bf16_t*, const bf16_t*, const bf16_t*, long long, bf16_t*, int,
+                 int);
+    if constexpr (GATED) kern = gemv_dma_kernel<4, true>;
+    else kern = dk == 4 ? gemv_dma_kernel<4, false> : gemv_dma_kernel<8, false>;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * dk), gemv_dma_xs_bytes(dk, K), st,
+                       static_cast<const bf16_t*>(w), w_rs, static_cast<const bf16_t*>(x),
+                       static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(residual), r_rs,
+                       static_cast<bf16_t*>(y), N, K);
+    return launch_status();
+  }
   if constexpr (GATED) {
     if (wk == 4) launch(gemv_bf16_kernel<4, true>, blocks, 4);
     else if (wk == 2) launch(gemv_bf16_kernel<2, true>, blocks, 2);

@@ -127,3 +127,35 @@ def test_gemv_ring_with_few_steps_per_wave(M, N, K, gated):
     torch.cuda.synchronize()
     torch.testing.assert_close(got.float(), ref, rtol=2e-2, atol=2e-3)
     assert torch.equal(got, again)
+
+
+@pytest.mark.parametrize("N,K,gated", [(20000, 3584, False), (9470, 3552, True), (8200, 8224, False),
+                                        (3584, 18944, False)])
+def test_gemv_lds_ring_one_row(N, K, gated):
+    """One activation row over a weight of 64 MiB or more streams through the
+    LDS ring (four waves with 64-k stages, or two waves with 128-k stages):
+    ragged column counts and K ranges that end inside a stage, against a
+    float32 reference; the gated sums equal the plain projection of the
+    stacked weight bit for bit, with a residual the plain result plus it, and
+    repeated calls are bit-identical."""
+    announce(f"gemv lds ring N={N} K={K} gated={gated}")
+    g = torch.Generator(device=dev()).manual_seed(N + K)
+    x = torch.randn(1, K, generator=g, device=dev()).to(torch.bfloat16)
+    NW = 2 * N if gated else N
+    w = (torch.randn(NW, K, generator=g, device=dev()) * 0.02).to(torch.bfloat16)
+    if gated:
+        got = ops.gated_linear(x, w)
+        gate, up = ops.linear(x, w).chunk(2, dim=-1)
+        want = F.silu(gate) * up
+        diff = (got.float() - want.float()).abs()
+        assert (diff <= _bf16_ulp(want)).all()
+        ref = F.silu(F.linear(x.float(), w[:N].float())) * F.linear(x.float(), w[N:].float())
+        torch.testing.assert_close(got.float(), ref, rtol=2e-2, atol=2e-3)
+    else:
+        got = ops.linear(x, w)
+        torch.testing.assert_close(got.float(), F.linear(x.float(), w.float()), rtol=1e-2, atol=2e-3)
+        r = (torch.randn(1, N, generator=g, device=dev()) * 4).to(torch.bfloat16)
+        assert torch.equal(ops.linear(x, w, residual=r), r + got)
+    again = ops.gated_linear(x, w) if gated else ops.linear(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
