@@ -705,7 +705,8 @@ def run_gemv(args) -> None:
     """The Qwen2.5-VL-7B decoder's projections through the HIP GEMV at one
     (draft / AR / bonus step) and ten (verify step) rows: q/k/v with bias, o
     and down with the residual epilogue, gate/up with the activation epilogue,
-    lm_head. Weights ~ N(0, 0.02) bf16 in enough copies (>= 768 MB) that the
+    lm_head, and at one row the decode steps' fused q/k/v launch (input
+    RMSNorm, projection, rotary embedding, K/V append). Weights ~ N(0, 0.02) bf16 in enough copies (>= 768 MB) that the
     256 MB last-level cache holds none of them between launches; 24 launches
     cycling the copies are captured in one HIP graph and replayed (the graph
     launch is amortised over the 24), timed with events. Prints one JSON line."""
@@ -720,8 +721,14 @@ def run_gemv(args) -> None:
               ("down", H, I, "residual"), ("lm_head", V, H, None)]
     g = torch.Generator(device=dev).manual_seed(7)
     results = []
+    # the decode steps' q/k/v launch: input RMSNorm, projection with bias, rotary
+    # embedding of the 28 query and 4 key heads, K/V append at row 32768
+    caches = [torch.zeros(1, 4, 32800, 128, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    length = torch.full((1,), 32768, dtype=torch.int32, device=dev)
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))).float().to(dev)
+    norm_w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
     for rows in (1, 10):
-        for name, N, K, kind in shapes:
+        for name, N, K, kind in shapes + ([("q/k/v fused", QKV, H, "norm+rotary+append")] if rows == 1 else []):
             NW = 2 * N if kind == "gated" else N
             nbytes = NW * K * 2
             copies = max(2, -(-768 * 2 ** 20 // nbytes))
@@ -730,9 +737,15 @@ def run_gemv(args) -> None:
             b = (torch.randn(NW, generator=g, device=dev) * 0.02).to(torch.bfloat16) if kind == "bias" else None
             r = torch.randn(1, rows, N, generator=g, device=dev).to(torch.bfloat16) if kind == "residual" else None
 
+            if kind == "norm+rotary+append":
+                b = (torch.randn(NW, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
             def one(w):
                 if kind == "gated":
                     return ops.gated_linear(x, w)
+                if kind == "norm+rotary+append":
+                    return ops.qkv_rope_append(x, w, b, 28, caches[0], caches[1], length, length, inv_freq,
+                                               norm_weight=norm_w, eps=1e-6)
                 return ops.linear(x, w, b, residual=r)
 
             def body():

@@ -22,12 +22,14 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
 }
 
 // Round-to-nearest-even float -> bf16, quieting NaNs (same rounding as
-// torch's float -> bfloat16 conversion).
+// torch's float -> bfloat16 conversion). Both results are formed and one
+// selected: a select, where an early return for NaN compiles to a branch
+// that saves and restores the execution mask around each conversion.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (u >> 16) | 0x40u;
+  return (u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded;
 }
 
 // fp16 is carried as the compiler's half type (its conversions from float

@@ -453,6 +453,64 @@ struct RopeArgs {
   int32_t* status;                // optional device status word (cache overflow)
 };
 
+// Where columns p..p+3 of half `half` (half 0: columns p.., half 1: p + 64..)
+// of head `head`, row m of M, go: query heads to q_out [n_q][M][128]; key and
+// value heads to cache row len + m of their KV head (len: the cache length).
+// nullptr for a cache row at or past the capacity (not written; it marks the
+// status word).
+__device__ __forceinline__ bf16_t* qkv_dest(int head, int half, int p, int m, int M, const RopeArgs& ra, int len) {
+  const int kv_head = head - ra.n_q;
+  bf16_t* dst;
+  if (head < ra.n_q) {
+    dst = ra.q_out + ((long long)head * M + m) * kHeadDim;
+  } else {
+    const int crow = len + m;
+    if (crow < 0 || crow >= ra.capacity) {
+      flag_overflow(ra.status);
+      return nullptr;
+    }
+    dst = (kv_head < ra.n_kv ? ra.ck + (long long)kv_head * ra.chs : ra.cv + (long long)(kv_head - ra.n_kv) * ra.chs) +
+          (long long)crow * kHeadDim;
+  }
+  return dst + half * (kHeadDim / 2) + p;
+}
+
+// rope_append_kernel's rotation factors at position pos and frequency freq:
+// angle = float(pos) * freq, cos and sin each rounded to bf16.
+__device__ __forceinline__ float2 rope_factors(int pos, float freq) {
+  const float ang = __fmul_rn((float)pos, freq);
+  return make_float2(round_bf16(cosf(ang)), round_bf16(sinf(ang)));
+}
+
+// The rotated element of half `half` of the pair (x1, x2) (the first and the
+// second half's column), each product and the sum rounded to bf16:
+// lo = x1 c - x2 s, hi = x2 c + x1 s.
+__device__ __forceinline__ float rope_rotate(float x1, float x2, float2 f, int half) {
+  return half ? round_bf16(__fadd_rn(round_bf16(__fmul_rn(x2, f.x)), round_bf16(__fmul_rn(x1, f.y))))
+              : round_bf16(__fadd_rn(round_bf16(__fmul_rn(x1, f.x)), round_bf16(__fmul_rn(-x2, f.y))));
+}
+
+// The register kernel's epilogue: v holds columns p..p+3 of half `half` of
+// row m (bias added, rounded to bf16), partner the same columns of the other
+// half; query and key heads are rotated, value heads stored as projected.
+__device__ __forceinline__ void qkv_rope_store(const float* v, const float* partner, int head, int half, int p, int m,
+                                               int M, const RopeArgs& ra, const int32_t* __restrict__ len_dev,
+                                               const int32_t* __restrict__ pos_dev,
+                                               const float* __restrict__ inv_freq) {
+  bf16_t* dst = qkv_dest(head, half, p, m, M, ra, *len_dev);
+  if (!dst) return;
+  if (head - ra.n_q >= ra.n_kv) {              // value heads: the projection as is
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = from_f32<bf16_t>(v[i]);
+    return;
+  }
+  const int pos = *pos_dev + ra.pos_offset + m;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    dst[i] = from_f32<bf16_t>(rope_rotate(half ? partner[i] : v[i], half ? v[i] : partner[i],
+                                          rope_factors(pos, inv_freq[p + i]), half));
+}
+
 template <bool NORM>
 __global__ void __launch_bounds__(256, 3)    // three waves a SIMD: a 7B q/k/v launch in one wave of workgroups
 gemv_qkv_rope_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
@@ -521,35 +579,166 @@ gemv_qkv_rope_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t*
 #pragma unroll
   for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(v[i], 16);
   if (!xm || lg >= 2) return;
-  const int kv_head = head - ra.n_q;
-  bf16_t* dst;
-  if (head < ra.n_q) {
-    dst = ra.q_out + ((long long)head * M + ln) * kHeadDim;
-  } else {
-    const int crow = *len_dev + ln;
-    if (crow < 0 || crow >= ra.capacity) {            // not written: marks the status word
-      flag_overflow(ra.status);
-      return;
+  qkv_rope_store(v, partner, head, half, p, ln, M, ra, len_dev, pos_dev, inv_freq);
+}
+
+// One decode row over a q|k|v weight of at least kDmaMinBytes (the 7B q/k/v,
+// 33 MB): the weight streams HBM -> LDS through gemv_dma_kernel's four-wave
+// ring (non-temporal whole-line DMA, 64-k stages, four slots per wave), with
+// its K split and MFMA order, so the sums equal gemv_dma_kernel<4, false>'s
+// and gemv_short_kernel's bit for bit. A workgroup owns 16 weight rows: eight
+// rotary pairs p..p+7 of one head, p = 8 (block % 8), head = block / 8, tile
+// row r holding column p + (r & 7) of half r / 8; the two halves of a pair
+// meet 32 lanes apart. Nothing the ring has in flight is waited for before its
+// turn: what the kernel reads besides the weight arrives by DMA ahead of the
+// first stages (the activation slices; with NORM the x row and the norm
+// weight; wave 0 the workgroup's bias) or by scalar loads after the first
+// stages (the cache length, the position and the frequencies, whose rotation
+// factors lanes 0 and 1 of each wave form while those stages are in flight,
+// one pair a lane), and the norm's barriers are bare
+// (__syncthreads would wait for every load in flight). With NORM the
+// workgroup forms the RMSNorm row from LDS in the order of the rms_* helpers
+// (rms_norm_kernel's output bit for bit) and writes it whole to LDS.
+// Measured at the 7B shape, weights cold, graph-replayed: 8.7 us without the
+// norm (the plain projection: 8.5 us) and 10.1 us with it, against 10.6 and
+// 12.7 us with the rotation factors formed in the epilogue, the scalar loads
+// ahead of the first stages and the norm's plain loads and __syncthreads
+// draining the ring (13.8 us in the register kernel). Six ring slots instead
+// of four measured slower with the norm (10.6 us).
+template <bool NORM>
+__global__ void __launch_bounds__(256)
+gemv_qkv_rope_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x,
+                         const bf16_t* __restrict__ bias, int K, RopeArgs ra, const int32_t* __restrict__ len_dev,
+                         const int32_t* __restrict__ pos_dev, const float* __restrict__ inv_freq,
+                         const bf16_t* __restrict__ nw, float eps) {
+  constexpr int WK = 4, KS = DmaCfg<WK>::KS, NSTG = DmaCfg<WK>::NSTG, HALF = kHeadDim / 2;
+  constexpr int C = KS / 8, RPI = 64 / C, IPM = 16 / RPI;
+  constexpr int kStageB = 16 * KS * 2;
+  constexpr int kXsB = ((kShortMaxK / WK) * 2 + 1023) / 1024 * 1024;   // one wave's slice region
+  constexpr int kRowB = NORM ? kQkvNormMaxK * 2 : 16;                   // the x row, the norm weight
+  static_assert(!NORM || (kQkvNormMaxK <= kRmsMaxOneBatch && kRowB % 1024 == 0), "one load batch, whole pieces");
+  __shared__ __align__(16) char rings[WK * NSTG * kStageB];
+  __shared__ __align__(16) char xs_all[WK * kXsB];
+  __shared__ __align__(16) char rows[2][kRowB];
+  __shared__ __align__(16) char bias_s[1024];
+  __shared__ f32x4 red[WK][64];
+  __shared__ float rms_red[WK];
+  __shared__ float2 cs[8];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int head = blockIdx.x / 8, p = (blockIdx.x % 8) * 8;
+  const bool rotated = head < ra.n_q + ra.n_kv;          // query and key heads
+  const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;   // <= kShortMaxK / WK (checked on the host)
+  const int k_begin = min(K, wave * kw), k_end = min(K, k_begin + kw);
+  const int nk = k_end - k_begin;
+  const int nst = (nk + KS - 1) / KS;
+  char* ring = rings + wave * NSTG * kStageB;
+  // without NORM each wave's slice arrives in whole 1 KiB DMA pieces, so the
+  // waves' regions are padded to whole pieces; with NORM the normalised row is
+  // written whole, element i at byte 2 i, and each wave reads its K range of it
+  char* xs = NORM ? xs_all + k_begin * 2 : xs_all + wave * kXsB;
+  int row_b[IPM], lc[IPM];
+#pragma unroll
+  for (int i = 0; i < IPM; ++i) {
+    const int r = RPI * i + lane / C;
+    lc[i] = (lane % C) ^ (r % C);
+    row_b[i] = ((r >> 3) * HALF + (r & 7)) * (int)(w_rs * 2);
+  }
+  const char* wb = reinterpret_cast<const char*>(w + (long long)(head * kHeadDim + p) * w_rs + k_begin);
+  auto issue = [&](int s) {
+    const uint32_t dst = lds_addr(ring + (s % NSTG) * kStageB);
+#pragma unroll
+    for (int i = 0; i < IPM; ++i) {
+      const int kk = min(s * KS + 8 * lc[i], nk - 8);
+      lds_dma16_sbase<true>(wb, (uint32_t)(row_b[i] + kk * 2), dst + i * 1024);
     }
-    dst = (kv_head < ra.n_kv ? ra.ck + (long long)kv_head * ra.chs : ra.cv + (long long)(kv_head - ra.n_kv) * ra.chs) +
-          (long long)crow * kHeadDim;
+  };
+  // bias columns p..p+7 and p+64..p+71: two 16-byte pieces (lanes past 1 re-read the second)
+  if (bias && wave == 0)
+    lds_dma16_sbase<false>(bias + head * kHeadDim + p, (uint32_t)(min(lane, 1) * HALF * 2), lds_addr(bias_s));
+  if constexpr (NORM) {                          // the rows' 1 KiB pieces, spread over the waves
+    const int np = (K * 2 + 1023) / 1024;
+    for (int q = wave; q < 2 * np; q += WK) {
+      const int r = q >= np ? 1 : 0, b = (q - r * np) * 1024;
+      lds_dma16_sbase<false>(r ? nw : x, (uint32_t)min(b + lane * 16, K * 2 - 16), lds_addr(rows[r] + b));
+    }
+  } else if (nk > 0) {                           // the wave's activation slice
+    const char* xb = reinterpret_cast<const char*>(x + k_begin);
+    for (int b = 0; b < nk * 2; b += 1024)
+      lds_dma16_sbase<false>(xb, (uint32_t)min(b + lane * 16, nk * 2 - 16), lds_addr(xs + b));
   }
-  dst += half * HALF + p;
-  if (kv_head >= ra.n_kv) {                    // value heads: the projection as is
+  const int pre = min(NSTG - 1, nst);
+  for (int s = 0; s < pre; ++s) issue(s);
+  // The cache length, the position and the frequencies are uniform: read as
+  // constant memory they are scalar loads, counted apart from the ring's
+  // vector-memory operations, and read after the first stages are issued, since
+  // waiting for any scalar load waits for all of them.
+  typedef const __attribute__((address_space(4))) int32_t* cint_p;
+  typedef const __attribute__((address_space(4))) float* cfloat_p;
+  const int len = head >= ra.n_q ? *(cint_p)len_dev : 0;
+  if (rotated) {
+    const int pos = *(cint_p)pos_dev + ra.pos_offset;
+    const float f0 = ((cfloat_p)inv_freq)[p + 2 * wave], f1 = ((cfloat_p)inv_freq)[p + 2 * wave + 1];
+    if (lane < 2) cs[2 * wave + lane] = rope_factors(pos, lane ? f1 : f0);
+  }
+  if constexpr (NORM) {
+    wait_vm_stages<IPM, NSTG>(pre);              // this wave's row pieces have landed, its stages may not
+    wg_barrier();
+    bf16_t nx[kRmsBatch], ng[kRmsBatch];
+    rms_load<bf16_t>(reinterpret_cast<const bf16_t*>(rows[0]), nx, 0, K, threadIdx.x);
+    rms_load<bf16_t>(reinterpret_cast<const bf16_t*>(rows[1]), ng, 0, K, threadIdx.x);
+    const float ss = rms_wave_sum(rms_add_squares<bf16_t>(0.f, nx, 0, K, threadIdx.x));
+    if (lane == 0) rms_red[wave] = ss;
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0());
+    wg_barrier();
+    const float inv = rms_inv(rms_red, K, eps);
+    // all kRmsBatch elements, those past K too (never read): 256 kRmsBatch
+    // elements fill the slice regions exactly
+    static_assert(256 * kRmsBatch * 2 == WK * kXsB, "the batch fits the slice regions");
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = from_f32<bf16_t>(v[i]);
-    return;
+    for (int j = 0; j < kRmsBatch; ++j)
+      *reinterpret_cast<bf16_t*>(xs_all + (threadIdx.x + 256 * j) * 2) = rms_scale<bf16_t>(nx[j], ng[j], inv);
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0());
+    wg_barrier();
   }
-  const int pos = *pos_dev + ra.pos_offset + ln;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < nst; ++s) {
+    wait_vm_stages<IPM, NSTG - 1>(min(NSTG - 2, nst - 1 - s));
+    if (s + NSTG - 1 < nst) issue(s + NSTG - 1);
+    const char* st = ring + (s % NSTG) * kStageB;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float ang = __fmul_rn((float)pos, inv_freq[p + i]);
-    const float c = round_bf16(cosf(ang)), s = round_bf16(sinf(ang));
-    const float x1 = half ? partner[i] : v[i], x2 = half ? v[i] : partner[i];
-    const float r = half ? round_bf16(__fadd_rn(round_bf16(__fmul_rn(x2, c)), round_bf16(__fmul_rn(x1, s))))
-                         : round_bf16(__fadd_rn(round_bf16(__fmul_rn(x1, c)), round_bf16(__fmul_rn(-x2, s))));
-    dst[i] = from_f32<bf16_t>(r);
+    for (int u = 0; u < KS / 32; ++u) {
+      const int kk = s * KS + 32 * u;
+      if (kk < nk) {
+        const bf16x8_t b = ln == 0 ? *reinterpret_cast<const bf16x8_t*>(xs + (kk + 8 * lg) * 2) : bf16x8_t{};
+        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(st + ln * (KS * 2) + (((4 * u + lg) ^ (ln % C)) << 4));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+      }
+    }
   }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));     // wave 0's bias piece (older than every stage; a no-op)
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 t = red[0][lane];
+#pragma unroll
+  for (int i = 1; i < WK; ++i) t += red[i][lane];
+  // lane (0, lg): tile rows 4 lg .. 4 lg + 3 = columns pp .. pp + 3 of half lg / 2
+  const int half = lg >> 1, q4 = 4 * (lg & 1), pp = p + q4;
+  const bf16_t* bl = reinterpret_cast<const bf16_t*>(bias_s + half * 16) + q4;
+  float v[4], partner[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = round_bf16(bias ? t[i] + to_f32<bf16_t>(bl[i]) : t[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) partner[i] = __shfl_xor(v[i], 32);
+  if (ln != 0) return;
+  bf16_t* dst = qkv_dest(head, half, pp, 0, 1, ra, len);
+  if (!dst) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    dst[i] = from_f32<bf16_t>(rotated ? rope_rotate(half ? partner[i] : v[i], half ? v[i] : partner[i], cs[q4 + i], half)
+                                      : v[i]);
 }
 
 // Waves per workgroup (the K split), from kernel durations at one and ten
@@ -572,13 +761,15 @@ inline int gemv_waves(int M, int n_rows, int K) {
 }
 
 // One row over a weight of at least kDmaMinBytes goes through the LDS ring
-// (gemv_dma_kernel, four waves where gemv_waves picks four, else eight): the
-// decode steps' gate/up (271 MB), down (136 MB) and lm_head (1.09 GB) at the
-// 7B shapes; smaller weights (o, 26 MB) keep the register kernels, whose
-// single load round trip suits them. The waves' activation slices must fit
-// the dynamic LDS, and a wave's slice pieces plus its stages in flight the 63
-// outstanding vector-memory operations it can count.
-constexpr long long kDmaMinBytes = 64ll << 20;
+// (gemv_dma_kernel, four waves where gemv_waves picks four, else eight): every
+// projection of a 7B decode step -- q/k/v (33 MB: 8.5 us against 11.6 us in
+// the short kernel), o (26 MB: 7.4 against 7.9 us), gate/up (271 MB), down
+// (136 MB) and lm_head (1.09 GB). Smaller weights keep the register kernels,
+// whose single load round trip suits a launch of a few microseconds. The
+// waves' activation slices must fit the dynamic LDS, and a wave's slice pieces
+// plus its stages in flight the 63 outstanding vector-memory operations it can
+// count.
+constexpr long long kDmaMinBytes = 16ll << 20;
 inline bool use_dma(int n_rows, int K, int wk, bool gated) {
   if (wk == 2 && gated) return false;          // eight waves of two row sets would crowd the LDS
   const int dk = wk == 4 ? 4 : 8;
@@ -677,6 +868,15 @@ extern "C" int std_qkv_rope_append(const void* x, long long x_row_stride, int n_
   static_assert((kShortMaxK / 4) / 32 <= kShortSteps, "four waves cover K in kShortSteps steps each");
   const RopeArgs ra{static_cast<bf16_t*>(q_out), static_cast<bf16_t*>(cache_k), static_cast<bf16_t*>(cache_v),
                     cache_head_stride, n_q, n_kv, capacity, pos_offset, status};
+  if (n_rows == 1 && (long long)(n_q + 2 * n_kv) * kHeadDim * K * 2 >= kDmaMinBytes &&
+      (!bias || aligned16(bias)) && (!norm_weight || aligned16(norm_weight))) {
+    auto kern = norm_weight ? gemv_qkv_rope_dma_kernel<true> : gemv_qkv_rope_dma_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3((n_q + 2 * n_kv) * 8), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const bf16_t*>(w), w_row_stride, static_cast<const bf16_t*>(x),
+                       static_cast<const bf16_t*>(bias), K, ra, len_dev, pos_dev, inv_freq,
+                       static_cast<const bf16_t*>(norm_weight), eps);
+    return launch_status();
+  }
   auto kern = norm_weight ? gemv_qkv_rope_kernel<true> : gemv_qkv_rope_kernel<false>;
   hipLaunchKernelGGL(kern, dim3((n_q + 2 * n_kv) * 16), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const bf16_t*>(w), w_row_stride, static_cast<const bf16_t*>(x), x_row_stride,

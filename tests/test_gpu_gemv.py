@@ -130,13 +130,15 @@ def test_gemv_ring_with_few_steps_per_wave(M, N, K, gated):
 
 
 @pytest.mark.parametrize("N,K,gated", [(20000, 3584, False), (9470, 3552, True), (8200, 8224, False),
-                                        (3584, 18944, False)])
+                                        (3584, 18944, False), (4608, 3584, False), (3584, 3584, False),
+                                        (2350, 3616, False)])
 def test_gemv_lds_ring_one_row(N, K, gated):
-    """One activation row over a weight of 64 MiB or more streams through the
-    LDS ring (four waves with 64-k stages, or two waves with 128-k stages):
-    ragged column counts and K ranges that end inside a stage, against a
-    float32 reference; the gated sums equal the plain projection of the
-    stacked weight bit for bit, with a residual the plain result plus it, and
+    """One activation row over a weight of 16 MiB or more streams through the
+    LDS ring (four waves with 64-k stages, or eight waves with 128-k stages):
+    the 7B q/k/v and o shapes, ragged column counts and K ranges that end
+    inside a stage, against a float32 reference; the gated sums equal the plain
+    projection of the stacked weight bit for bit, with a residual the plain
+    result plus it, with a bias the float32 reference plus the bias, and
     repeated calls are bit-identical."""
     announce(f"gemv lds ring N={N} K={K} gated={gated}")
     g = torch.Generator(device=dev()).manual_seed(N + K)
@@ -156,6 +158,9 @@ def test_gemv_lds_ring_one_row(N, K, gated):
         torch.testing.assert_close(got.float(), F.linear(x.float(), w.float()), rtol=1e-2, atol=2e-3)
         r = (torch.randn(1, N, generator=g, device=dev()) * 4).to(torch.bfloat16)
         assert torch.equal(ops.linear(x, w, residual=r), r + got)
+        b = torch.randn(N, generator=g, device=dev()).to(torch.bfloat16)
+        torch.testing.assert_close(ops.linear(x, w, bias=b).float(), F.linear(x.float(), w.float(), b.float()),
+                                   rtol=1e-2, atol=2e-3)
     again = ops.gated_linear(x, w) if gated else ops.linear(x, w)
     torch.cuda.synchronize()
     assert torch.equal(got, again)
