@@ -428,6 +428,25 @@ int std_gemv_ex(const void* x, long long x_row_stride, const void* w, long long 
                 const void* bias, const void* residual, long long residual_row_stride, void* y,
                 long long y_row_stride, int M, int N, int K, int gated, int dtype, void* stream);
 
+/* std_gemv_ex of one row whose input is a hidden state before its RMSNorm:
+ * y = std_gemv_ex(std_rms_norm(x, norm_weight, eps), w, bias, residual,
+ * gated) in one launch (one instead of two at batch 1) -- the decoder
+ * layer's post_attention_layernorm before the MLP's gate/up projection
+ * (modeling_qwen2_5_vl.py:1219-1220) and the final norm before lm_head
+ * (modeling_qwen2_5_vl.py:1454, 2122). Every workgroup forms the norm while
+ * its first weight stages are in flight (7B gate/up: 43.1 us against 46.5 us
+ * for the two launches; lm_head 158.8 against 163.3 us). x, norm_weight [K],
+ * K <= 3584 a
+ * multiple of 32; y, residual (may be NULL) [N]; x, norm_weight, w 16-byte
+ * aligned. The normalised row equals std_rms_norm's bit for bit, and y equals
+ * std_rms_norm followed by std_gemv_ex bit for bit where std_gemv_ex streams
+ * the weight through its LDS ring (one row, weights of 16 MiB and more: every
+ * 7B projection); for smaller weights the K split may differ and elements by
+ * one bf16 rounding. No workspace. */
+int std_gemv_norm(const void* x, const void* norm_weight, float eps, const void* w, long long w_row_stride,
+                  const void* bias, const void* residual, void* y, int N, int K, int gated, int dtype,
+                  void* stream);
+
 /* The q|k|v projection of a decode step fused with std_rope_append (one
  * launch instead of two): x [n_rows][K] (n_rows <= 4, K <= 4096, a multiple
  * of 32) times W [(n_q + 2 n_kv) * 128][K] (the q_proj, k_proj, v_proj rows

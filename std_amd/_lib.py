@@ -80,6 +80,8 @@ SIGNATURES = {
                          c_int, c_int, c_void_p, c_size_t, c_void_p]),
     "std_gemv_ex": (c_int, [c_void_p, c_longlong, c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_void_p,
                             c_longlong, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "std_gemv_norm": (c_int, [c_void_p, c_void_p, c_float, c_void_p, c_longlong, c_void_p, c_void_p, c_void_p, c_int,
+                              c_int, c_int, c_int, c_void_p]),
     "std_qkv_rope_append": (c_int, [c_void_p, c_longlong, c_int, c_int, c_void_p, c_longlong, c_void_p, c_int, c_int,
                                     c_int, c_void_p, c_void_p, c_void_p, c_longlong, c_int, c_void_p, c_void_p, c_int,
                                     c_void_p, c_void_p, c_float, c_int, c_void_p, c_void_p]),

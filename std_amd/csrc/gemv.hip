@@ -194,6 +194,16 @@ inline int gemv_dma_xs_bytes(int WK, int K) {
   return WK * ((kw * 2 + 1023) / 1024) * 1024;
 }
 
+// The input RMSNorm in the launch (NORM, one row): rows up to kGemvNormMaxK
+// elements, one load batch of rms_norm_kernel's 256-thread layout, whose
+// 256 kRmsBatch elements the activation region then holds.
+constexpr int kGemvNormMaxK = 3584;
+constexpr int kNormXsBytes = 256 * kRmsBatch * 2;
+inline int gemv_dma_lds_bytes(int WK, int K, bool norm) {
+  const int b = gemv_dma_xs_bytes(WK, K);
+  return norm && b < kNormXsBytes ? kNormXsBytes : b;
+}
+
 // s_waitcnt until at most n * PER vector-memory operations are outstanding
 // (n < MAXN, a run-time count turned into the instruction's immediate).
 template <int PER, int MAXN>
@@ -209,11 +219,22 @@ __device__ __forceinline__ void wait_vm_stages(int n) {
   }
 }
 
-template <int WK, bool GATED>
+// NORM (one row, K <= kGemvNormMaxK): x is a decoder layer's hidden state
+// before its RMSNorm (weight nw, epsilon eps), normalised in the launch as
+// rms_norm_kernel normalises it, bit for bit. The x row and the norm weight
+// come by DMA ahead of the first stages -- the x row's 1 KiB pieces into the
+// ring slot each wave fills last (piece q in wave q % WK's), the norm weight
+// into the activation region -- and the first four waves (rms_norm_kernel's
+// 256-thread layout) form the statistic and write the normalised row whole
+// to the activation region, element i at byte 2 i, from which each wave reads
+// its K range. The barriers are bare (the stages stay in flight); both
+// stagings are read before the first overwrite (the normalised row after the
+// second barrier, the ring slot by the stage issued after the third).
+template <int WK, bool GATED, bool NORM = false>
 __global__ void __launch_bounds__(64 * WK)
 gemv_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x,
                 const bf16_t* __restrict__ bias, const bf16_t* __restrict__ residual, long long r_rs,
-                bf16_t* __restrict__ y, int N, int K) {
+                bf16_t* __restrict__ y, int N, int K, const bf16_t* __restrict__ nw = nullptr, float eps = 0.f) {
   constexpr int KS = DmaCfg<WK>::KS, NSTG = DmaCfg<WK>::NSTG;
   constexpr int C = KS / 8;                      // 16-byte chunks per row of a stage
   constexpr int RPI = 64 / C;                    // rows per DMA instruction
@@ -222,9 +243,16 @@ gemv_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __re
   constexpr int kMatB = 16 * KS * 2;
   constexpr int kStageB = kMat * kMatB;
   constexpr int kPer = kMat * IPM;               // DMA instructions per stage
+  constexpr int kRowPieces = (kGemvNormMaxK * 2 + 1023) / 1024;
+  static_assert(!NORM || kStageB >= (kRowPieces + WK - 1) / WK * 1024, "the x row fits the last ring slots");
+  static_assert(!NORM || (WK >= 4 && kGemvNormMaxK <= 256 * kRmsBatch), "four statistic waves, one batch");
   __shared__ __align__(16) char rings[WK * NSTG * kStageB];
   extern __shared__ __align__(16) char xs_all[];
   __shared__ f32x4 red[kMat][WK][64];
+  // the norm's four wave sums, in the epilogue's exchange buffer (first used
+  // after the loop): the gated launch takes exactly half a CU's 160 KiB of
+  // LDS, and 16 bytes more would leave one workgroup a CU
+  float* rms_red = reinterpret_cast<float*>(&red[0][0][0]);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15, lg = lane >> 4;
@@ -235,7 +263,9 @@ gemv_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __re
   const int nst = (nk + KS - 1) / KS;
   const int xs_b = ((kw * 2 + 1023) / 1024) * 1024;
   char* ring = rings + wave * NSTG * kStageB;
-  char* xs = xs_all + wave * xs_b;
+  char* xs = NORM ? xs_all + k_begin * 2 : xs_all + wave * xs_b;
+  // the ring slot filled last, where wave q % WK keeps x row piece q
+  auto x_piece = [&](int q) { return rings + (q % WK) * NSTG * kStageB + (NSTG - 1) * kStageB + (q / WK) * 1024; };
   // DMA lane roles: instruction i of a row set covers rows RPI i + lane / C;
   // the lane's 16 bytes are physical chunk lane % C of that row, i.e. logical
   // chunk lc[i] = (lane % C) ^ (row % C) (k 8 lc .. 8 lc + 7 of the stage);
@@ -260,8 +290,17 @@ gemv_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __re
                               dst + j * kMatB + i * 1024);
       }
   };
-  // the activation slice [k_begin, k_end) of row 0, in 1 KiB DMA pieces
-  if (nk > 0) {
+  if constexpr (NORM) {
+    // the x row and the norm weight, 1 KiB pieces spread over the waves
+    const int np = (K * 2 + 1023) / 1024;
+    for (int q = wave; q < 2 * np; q += WK) {
+      const bool is_x = q < np;
+      const int b = (is_x ? q : q - np) * 1024;
+      lds_dma16_sbase<false>(is_x ? x : nw, (uint32_t)min(b + lane * 16, K * 2 - 16),
+                             lds_addr(is_x ? x_piece(q) : xs_all + b));
+    }
+  } else if (nk > 0) {
+    // the activation slice [k_begin, k_end) of row 0, in 1 KiB DMA pieces
     const char* xb = reinterpret_cast<const char*>(x + k_begin);
     for (int b = 0; b < xs_b; b += 1024)
       lds_dma16_sbase<false>(xb, (uint32_t)min(b + lane * 16, nk * 2 - 16), lds_addr(xs + b));
@@ -269,7 +308,35 @@ gemv_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __re
   f32x4 acc[kMat];
 #pragma unroll
   for (int j = 0; j < kMat; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < NSTG - 1 && s < nst; ++s) issue(s);
+  const int pre = min(NSTG - 1, nst);
+  for (int s = 0; s < pre; ++s) issue(s);
+  if constexpr (NORM) {
+    wait_vm_stages<kPer, NSTG>(pre);            // this wave's pieces have landed, its stages may not
+    wg_barrier();
+    const bool stat = threadIdx.x < 256;        // wave-uniform
+    bf16_t nx[kRmsBatch], ng[kRmsBatch];
+    if (stat) {
+      // element e = tid + 256 j: x piece j / 2, norm weight byte 2 e (elements
+      // past K read what the regions hold there and are never used)
+#pragma unroll
+      for (int j = 0; j < kRmsBatch; ++j) {
+        nx[j] = *reinterpret_cast<const bf16_t*>(x_piece(j >> 1) + ((j & 1) * 256 + threadIdx.x) * 2);
+        ng[j] = *reinterpret_cast<const bf16_t*>(xs_all + (threadIdx.x + 256 * j) * 2);
+      }
+      const float ss = rms_wave_sum(rms_add_squares<bf16_t>(0.f, nx, 0, K, threadIdx.x));
+      if (lane == 0) rms_red[wave] = ss;
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0());
+    wg_barrier();
+    if (stat) {
+      const float inv = rms_inv(rms_red, K, eps);
+#pragma unroll
+      for (int j = 0; j < kRmsBatch; ++j)
+        *reinterpret_cast<bf16_t*>(xs_all + (threadIdx.x + 256 * j) * 2) = rms_scale<bf16_t>(nx[j], ng[j], inv);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0());
+    wg_barrier();
+  }
   for (int s = 0; s < nst; ++s) {
     // stages issued: 0 .. min(s + NSTG - 2, nst - 1); stage s must have landed
     wait_vm_stages<kPer, NSTG - 1>(min(NSTG - 2, nst - 1 - s));
@@ -779,6 +846,22 @@ inline bool use_dma(int n_rows, int K, int wk, bool gated) {
          (kw * 2 + 1023) / 1024 + in_flight <= 63;
 }
 
+// One row through gemv_dma_kernel at dk waves (a gated launch at four only).
+template <bool GATED, bool NORM>
+int launch_dma(int dk, const void* x, const void* w, long long w_rs, const void* bias, const void* residual,
+               long long r_rs, void* y, int N, int K, const void* nw, float eps, hipStream_t st) {
+  void (*kern)(const bf16_t*, long long, const bf16_t*, const bf16_t*, const bf16_t*, long long, bf16_t*, int, int,
+               const bf16_t*, float);
+  if constexpr (GATED) kern = gemv_dma_kernel<4, true, NORM>;
+  else kern = dk == 4 ? gemv_dma_kernel<4, false, NORM> : gemv_dma_kernel<8, false, NORM>;
+  if (GATED) dk = 4;
+  hipLaunchKernelGGL(kern, dim3((N + 15) / 16), dim3(64 * dk), gemv_dma_lds_bytes(dk, K, NORM), st,
+                     static_cast<const bf16_t*>(w), w_rs, static_cast<const bf16_t*>(x),
+                     static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(residual), r_rs,
+                     static_cast<bf16_t*>(y), N, K, static_cast<const bf16_t*>(nw), eps);
+  return launch_status();
+}
+
 template <bool GATED>
 int launch_gemv(const void* x, long long x_rs, const void* w, long long w_rs, const void* bias, const void* residual,
                 long long r_rs, void* y, long long y_rs, int M, int N, int K, hipStream_t st) {
@@ -790,18 +873,8 @@ int launch_gemv(const void* x, long long x_rs, const void* w, long long w_rs, co
                        static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
   };
   static_assert((kShortMaxK / 4) / 32 <= kShortSteps, "four waves cover K in kShortSteps steps each");
-  if (M == 1 && use_dma(GATED ? 2 * N : N, K, wk, GATED)) {
-    const int dk = wk == 4 ? 4 : 8;                // use_dma admits a gated launch at four waves only
-    void (*kern)(const bf16_t*, long long, const bf16_t*, const bf16_t*, const bf16_t*, long long, bf16_t*, int,
-                 int);
-    if constexpr (GATED) kern = gemv_dma_kernel<4, true>;
-    else kern = dk == 4 ? gemv_dma_kernel<4, false> : gemv_dma_kernel<8, false>;
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * dk), gemv_dma_xs_bytes(dk, K), st,
-                       static_cast<const bf16_t*>(w), w_rs, static_cast<const bf16_t*>(x),
-                       static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(residual), r_rs,
-                       static_cast<bf16_t*>(y), N, K);
-    return launch_status();
-  }
+  if (M == 1 && use_dma(GATED ? 2 * N : N, K, wk, GATED))
+    return launch_dma<GATED, false>(wk == 4 ? 4 : 8, x, w, w_rs, bias, residual, r_rs, y, N, K, nullptr, 0.f, st);
   if constexpr (GATED) {
     if (wk == 4) launch(gemv_bf16_kernel<4, true>, blocks, 4);
     else if (wk == 2) launch(gemv_bf16_kernel<2, true>, blocks, 2);
@@ -849,6 +922,21 @@ extern "C" int std_gemv_ex(const void* x, long long x_row_stride, const void* w,
                            long long y_row_stride, int M, int N, int K, int gated, int dtype, void* stream) {
   return gemv_entry(x, x_row_stride, w, w_row_stride, bias, residual, residual_row_stride, y, y_row_stride, M, N, K,
                     dtype, gated != 0, stream);
+}
+
+extern "C" int std_gemv_norm(const void* x, const void* norm_weight, float eps, const void* w,
+                             long long w_row_stride, const void* bias, const void* residual, void* y, int N, int K,
+                             int gated, int dtype, void* stream) {
+  if (!x || !norm_weight || !w || !y) return STD_E_NULL;
+  if (dtype != STD_BF16) return STD_E_DTYPE;
+  if (N < 1 || K < 32 || K % 32 != 0 || K > kGemvNormMaxK || w_row_stride < K) return STD_E_SHAPE;
+  if (!aligned16(x) || !aligned16(norm_weight) || !aligned16(w) || (w_row_stride * 2) % 16) return STD_E_ALIGN;
+  // the split std_gemv_ex's ring launch would use for this shape: four waves
+  // where gemv_waves picks four (and for every gated launch), else eight
+  const int dk = gated || gemv_waves(1, N, K) == 4 ? 4 : 8;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return gated ? launch_dma<true, true>(dk, x, w, w_row_stride, bias, residual, 0, y, N, K, norm_weight, eps, st)
+               : launch_dma<false, true>(dk, x, w, w_row_stride, bias, residual, 0, y, N, K, norm_weight, eps, st);
 }
 
 extern "C" int std_qkv_rope_append(const void* x, long long x_row_stride, int n_rows, int K, const void* w,

@@ -264,13 +264,20 @@ class RandomDecoder:
         out = out.transpose(1, 2).reshape(1, n, hq * d)
         return residual + F.linear(out, p["o_w"])
 
-    def _mlp(self, li: int, h: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
-        """residual + down(silu(gate(h)) * up(h)); up to 16 bf16 rows (decode
-        and verify steps) take two HIP launches (activation and residual add in
-        the GEMV epilogues)."""
+    def _mlp(self, li: int, x: torch.Tensor) -> torch.Tensor:
+        """x + down(silu(gate(h)) * up(h)) with h = post_attention_layernorm(x);
+        up to 16 bf16 rows (decode and verify steps) take HIP launches, the
+        activation and the residual add in the GEMV epilogues: at one row two
+        (the norm inside the gate/up launch, std_gemv_norm; 7B: 43.1 us against
+        46.5 us for the norm launch and the projection), else three."""
         p = self.layers[li]
+        if self._hip_rows(x, 1):
+            act = ops.gated_linear(x, p["gate_up_w"], norm_weight=p["ln2"], eps=self.config.rms_norm_eps)
+            return ops.linear(act, p["down_w"], residual=x)
+        h = self._rms_norm(x, p["ln2"])
         if self._hip_rows(h, 16):
-            return ops.linear(ops.gated_linear(h, p["gate_up_w"]), p["down_w"], residual=residual)
+            return ops.linear(ops.gated_linear(h, p["gate_up_w"]), p["down_w"], residual=x)
+        residual = x
         gate, up = F.linear(h, p["gate_up_w"]).chunk(2, dim=-1)
         return residual + F.linear(F.silu(gate) * up, p["down_w"])
 
@@ -316,11 +323,15 @@ class RandomDecoder:
         for li in range(self.config.num_hidden_layers):
             kc, vc = past_key_values[li]
             x = self._attention(li, x, cos, sin, kc, vc, step_state, host_lengths)
-            x = self._mlp(li, self._rms_norm(x, self.layers[li]["ln2"]), residual=x)
+            x = self._mlp(li, x)
         if not host_lengths:
             ops.len_add(step_state, n)
         if not all_logits:
             x = x[:, -1:]
+        if self._hip_rows(x, 1):
+            # the final norm in the lm_head launch (std_gemv_norm; 7B: 158.8 us
+            # against 163.3 us for the norm launch and the projection)
+            return ops.linear(x, self.lm_head, norm_weight=self.norm, eps=self.config.rms_norm_eps)
         return self._linear(self._rms_norm(x, self.norm), self.lm_head)
 
     __call__ = forward

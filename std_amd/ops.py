@@ -577,8 +577,17 @@ def attention_devlen(query: torch.Tensor, key_cache: torch.Tensor, value_cache: 
 
 
 def _gemv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], residual: Optional[torch.Tensor],
-          gated: bool, name: str) -> torch.Tensor:
+          gated: bool, name: str, norm_weight: Optional[torch.Tensor] = None, eps: float = 0.0) -> torch.Tensor:
     dev = _check_device(x, weight)
+    if norm_weight is not None:
+        _check_device(norm_weight)
+        K = x.shape[-1]
+        if norm_weight.dtype != torch.bfloat16 or norm_weight.shape != (K,) or not norm_weight.is_contiguous():
+            raise ValueError(f"{name}: norm_weight must be a contiguous bf16 [{K}]")
+        one_launch = (x.numel() == K and K <= 3584 and x.is_contiguous() and x.data_ptr() % 16 == 0
+                      and norm_weight.data_ptr() % 16 == 0)
+        if not one_launch:      # the norm as its own launch, then the projection
+            return _gemv(rms_norm(x, norm_weight, eps), weight, bias, residual, gated, name)
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise TypeError(f"{name}: bf16 only")
     K = x.shape[-1]
@@ -600,6 +609,12 @@ def _gemv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], r
         if r2.stride(1) != 1:
             raise ValueError(f"{name}: residual rows must be contiguous")
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    if norm_weight is not None:
+        _lib.call("std_gemv_norm", x2.data_ptr(), norm_weight.data_ptr(), float(eps), weight.data_ptr(),
+                  weight.stride(0), bias.data_ptr() if bias is not None else None,
+                  r2.data_ptr() if r2 is not None else None, y.data_ptr(), N, K, int(gated), _lib.STD_BF16,
+                  _stream(dev))
+        return y.view(*x.shape[:-1], N)
     _lib.call("std_gemv_ex", x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0),
               bias.data_ptr() if bias is not None else None, r2.data_ptr() if r2 is not None else None,
               r2.stride(0) if r2 is not None else 0, y.data_ptr(), y.stride(0), M, N, K, int(gated), _lib.STD_BF16,
@@ -682,21 +697,26 @@ def gqa_decode_indexed(query: torch.Tensor, dense_k: torch.Tensor, dense_v: torc
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
-           residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+           residual: Optional[torch.Tensor] = None, norm_weight: Optional[torch.Tensor] = None,
+           eps: float = 0.0) -> torch.Tensor:
     """torch.nn.functional.linear for at most 16 bf16 rows: the HIP
     weight-streaming projection (weight [N, K] read once, fp32 accumulation,
     deterministic). x [..., K] with at most 16 rows in total. With residual
     ([..., N] bf16) it returns residual + linear(x, weight, bias), the
-    decoder's residual add, rounded as torch rounds the two ops."""
-    return _gemv(x, weight, bias, residual, False, "linear")
+    decoder's residual add, rounded as torch rounds the two ops. With
+    norm_weight x is first normalised as rms_norm(x, norm_weight, eps) (one
+    launch for one row of at most 3584 elements: std_gemv_norm)."""
+    return _gemv(x, weight, bias, residual, False, "linear", norm_weight, eps)
 
 
-def gated_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+def gated_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                 norm_weight: Optional[torch.Tensor] = None, eps: float = 0.0) -> torch.Tensor:
     """silu(gate) * up of gate, up = linear(x, weight, bias).chunk(2, -1) for
     at most 16 bf16 rows (the MLP's fused gate/up projection and activation,
     each op rounded to bf16 as torch rounds it): weight [2 I, K] stacks the
-    gate rows over the up rows; returns [..., I]."""
-    return _gemv(x, weight, bias, None, True, "gated_linear")
+    gate rows over the up rows; returns [..., I]. norm_weight, eps: as in
+    linear."""
+    return _gemv(x, weight, bias, None, True, "gated_linear", norm_weight, eps)
 
 
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:

@@ -252,6 +252,15 @@ def test_gemv_validation():
     assert lib.std_gemv_ex(16, 128, 16, 128, NULL, 16, 10, 16, 64, 1, 64, 128, 0, 1, NULL) == -3  # residual stride
     assert lib.std_gemv_ex(16, 132, 16, 128, NULL, NULL, 0, 16, 64, 2, 64, 128, 1, 1, NULL) == -5  # x row stride
     assert lib.std_gemv(NULL, 128, 16, 128, NULL, 16, 64, 1, 64, 128, 1, NULL, 0, NULL) == -1
+    # the projection with the input RMSNorm: one row of at most 3584, bf16, 16-byte aligned
+    assert lib.std_gemv_norm(NULL, 16, 1e-6, 16, 3584, NULL, NULL, 16, 64, 3584, 0, 1, NULL) == -1
+    assert lib.std_gemv_norm(16, NULL, 1e-6, 16, 3584, NULL, NULL, 16, 64, 3584, 0, 1, NULL) == -1
+    assert lib.std_gemv_norm(16, 16, 1e-6, 16, 3616, NULL, NULL, 16, 64, 3616, 0, 1, NULL) == -3
+    assert lib.std_gemv_norm(16, 16, 1e-6, 16, 3584, NULL, NULL, 16, 64, 3500, 1, 1, NULL) == -3
+    assert lib.std_gemv_norm(16, 16, 1e-6, 16, 100, NULL, NULL, 16, 64, 128, 0, 1, NULL) == -3
+    assert lib.std_gemv_norm(16, 16, 1e-6, 16, 3584, NULL, NULL, 16, 64, 3584, 0, 0, NULL) == -2
+    assert lib.std_gemv_norm(16, 24, 1e-6, 16, 3584, NULL, NULL, 16, 64, 3584, 0, 1, NULL) == -5
+    assert lib.std_gemv_norm(16, 16, 1e-6, 16, 3588, NULL, NULL, 16, 64, 3584, 0, 1, NULL) == -5
     # the fused q|k|v projection: bf16 only
     qkv = [16, 3584, 1, 3584, 16, 3584, NULL, 28, 4, 128, 16, 16, 16, 128 * 1024, 1024, 16, 16, 0, 16, NULL, 1e-6]
     assert lib.std_qkv_rope_append(*qkv, 2, NULL, NULL) == -2

@@ -164,3 +164,65 @@ def test_gemv_lds_ring_one_row(N, K, gated):
     again = ops.gated_linear(x, w) if gated else ops.linear(x, w)
     torch.cuda.synchronize()
     assert torch.equal(got, again)
+
+
+def _rms_norm_f32(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """Qwen2RMSNorm in float32 with its two bf16 roundings (x * rsqrt(mean(x^2)
+    + eps) to bf16, then times the weight to bf16): a reference written
+    independently of the HIP kernel's summation order."""
+    xf = x.float()
+    h = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+    return (w.float() * h.float()).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("N,K,gated,residual,bias", [(18944, 3584, True, False, False), (20000, 3584, False, True, True),
+                                                     (3584, 3584, False, True, False), (9504, 3584, False, False, True),
+                                                     (1000, 896, True, False, True), (700, 1024, False, True, False),
+                                                     (3000, 3552, True, False, False)])
+def test_gemv_norm_equals_rms_norm_then_gemv(N, K, gated, residual, bias):
+    """One row with the input RMSNorm in the projection's launch
+    (std_gemv_norm): the gate/up shape with the activation epilogue, plain
+    projections with bias and residual at four and eight ring waves, and
+    weights under 16 MiB. Where the plain projection also streams through the
+    LDS ring (16 MiB and more) the two paths are equal bit for bit; below it
+    they split K differently, and both are held to a float32 reference of the
+    normalised projection. Two rows take the norm as its own launch."""
+    announce(f"gemv norm N={N} K={K} gated={gated} residual={residual} bias={bias}")
+    g = torch.Generator(device=dev()).manual_seed(N + K + 17)
+    NW = 2 * N if gated else N
+    x = (torch.randn(1, 1, K, generator=g, device=dev()) * 3).to(torch.bfloat16)
+    nw = (1 + 0.2 * torch.randn(K, generator=g, device=dev())).to(torch.bfloat16)
+    w = (torch.randn(NW, K, generator=g, device=dev()) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(NW, generator=g, device=dev()) * 0.1).to(torch.bfloat16) if bias else None
+    r = (torch.randn(1, 1, N, generator=g, device=dev()) * 2).to(torch.bfloat16) if residual else None
+    h = ops.rms_norm(x, nw, 1e-6)
+    hr = _rms_norm_f32(x, nw, 1e-6).float()
+    if gated:
+        got = ops.gated_linear(x, w, b, norm_weight=nw, eps=1e-6)
+        want = ops.gated_linear(h, w, b)
+        gate, up = F.linear(hr, w.float(), b.float() if bias else None).chunk(2, dim=-1)
+        ref = F.silu(gate) * up
+    else:
+        got = ops.linear(x, w, b, residual=r, norm_weight=nw, eps=1e-6)
+        want = ops.linear(h, w, b, residual=r)
+        ref = F.linear(hr, w.float(), b.float() if bias else None)
+        if residual:
+            ref = ref + r.float()
+    torch.cuda.synchronize()
+    assert got.shape == want.shape
+    if NW * K * 2 >= 16 << 20:
+        assert torch.equal(got, want)
+    # with a residual (|r| up to ~8) the sum's bf16 rounding alone is up to
+    # half an ulp of 8 (2^-6), and near cancellations it is all of the
+    # relative error
+    torch.testing.assert_close(got.float(), ref, rtol=2e-2, atol=2e-2 if residual else 3e-3)
+    again = ops.gated_linear(x, w, b, norm_weight=nw, eps=1e-6) if gated else \
+        ops.linear(x, w, b, residual=r, norm_weight=nw, eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
+    # two rows: the norm as its own launch, then the projection
+    x2 = torch.cat([x, x * 0.5], dim=1)
+    two = ops.gated_linear(x2, w, b, norm_weight=nw, eps=1e-6) if gated else ops.linear(x2, w, b, norm_weight=nw,
+                                                                                      eps=1e-6)
+    h2 = ops.rms_norm(x2, nw, 1e-6)
+    assert torch.equal(two, ops.gated_linear(h2, w, b) if gated else ops.linear(h2, w, b))
