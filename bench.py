@@ -705,8 +705,9 @@ def run_gemv(args) -> None:
     """The Qwen2.5-VL-7B decoder's projections through the HIP GEMV at one
     (draft / AR / bonus step) and ten (verify step) rows: q/k/v with bias, o
     and down with the residual epilogue, gate/up with the activation epilogue,
-    lm_head, and at one row the decode steps' fused q/k/v launch (input
-    RMSNorm, projection, rotary embedding, K/V append). Weights ~ N(0, 0.02) bf16 in enough copies (>= 768 MB) that the
+    lm_head, and at one row the decode steps' launches with the RMSNorm
+    inside: q/k/v (input norm, projection, rotary embedding, K/V append),
+    gate/up (post-attention norm) and lm_head (final norm). Weights ~ N(0, 0.02) bf16 in enough copies (>= 768 MB) that the
     256 MB last-level cache holds none of them between launches; 24 launches
     cycling the copies are captured in one HIP graph and replayed (the graph
     launch is amortised over the 24), timed with events. Prints one JSON line."""
@@ -728,8 +729,10 @@ def run_gemv(args) -> None:
     inv_freq = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))).float().to(dev)
     norm_w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
     for rows in (1, 10):
-        for name, N, K, kind in shapes + ([("q/k/v fused", QKV, H, "norm+rotary+append")] if rows == 1 else []):
-            NW = 2 * N if kind == "gated" else N
+        fused = [("q/k/v fused", QKV, H, "norm+rotary+append"), ("gate/up with norm", I, H, "norm+gated"),
+                 ("lm_head with norm", V, H, "norm")]
+        for name, N, K, kind in shapes + (fused if rows == 1 else []):
+            NW = 2 * N if kind in ("gated", "norm+gated") else N
             nbytes = NW * K * 2
             copies = max(2, -(-768 * 2 ** 20 // nbytes))
             ws = [(torch.randn(NW, K, generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(copies)]
@@ -743,6 +746,10 @@ def run_gemv(args) -> None:
             def one(w):
                 if kind == "gated":
                     return ops.gated_linear(x, w)
+                if kind == "norm+gated":
+                    return ops.gated_linear(x, w, norm_weight=norm_w, eps=1e-6)
+                if kind == "norm":
+                    return ops.linear(x, w, norm_weight=norm_w, eps=1e-6)
                 if kind == "norm+rotary+append":
                     return ops.qkv_rope_append(x, w, b, 28, caches[0], caches[1], length, length, inv_freq,
                                                norm_weight=norm_w, eps=1e-6)

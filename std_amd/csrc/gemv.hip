@@ -360,6 +360,91 @@ gemv_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __re
   gemv_finish<WK, GATED, 16>(red, acc, wave, lane, n0, bias, residual, r_rs, y, 0, 1, N);
 }
 
+// Two to sixteen activation rows over a large weight (the ten-row verify
+// step): gemv_dma_kernel's ring, with each stage carrying, beside the weight
+// rows, a 16-row slab of the activation rows' same K range (rows past M
+// re-read row M - 1 and meet zero MFMA operands). The rows fill the MFMA's
+// 16 columns, so M costs no extra matrix work; the slab comes by DMA with the
+// default cache policy (every workgroup reads it), the weight non-temporally.
+// 64-k stages, three slots per wave (four for a plain projection at four
+// waves); eight waves where gemv_waves would run two (o, down).
+template <int WK, bool GATED>
+struct DmaRowsCfg {
+  static constexpr int KS = 64, NSTG = (GATED || WK == 8) ? 3 : 4;
+};
+
+template <int WK, bool GATED>
+__global__ void __launch_bounds__(64 * WK)
+gemv_dma_rows_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf16_t* __restrict__ x, long long x_rs,
+                     const bf16_t* __restrict__ bias, const bf16_t* __restrict__ residual, long long r_rs,
+                     bf16_t* __restrict__ y, long long y_rs, int M, int N, int K) {
+  constexpr int KS = DmaRowsCfg<WK, GATED>::KS, NSTG = DmaRowsCfg<WK, GATED>::NSTG;
+  constexpr int C = KS / 8, RPI = 64 / C, IPM = 16 / RPI;
+  constexpr int kMat = GATED ? 2 : 1;
+  constexpr int kMatB = 16 * KS * 2;
+  constexpr int kStageB = (kMat + 1) * kMatB;    // the weight row sets, then the activation slab
+  constexpr int kPer = (kMat + 1) * IPM;         // DMA instructions per stage
+  __shared__ __align__(16) char rings[WK * NSTG * kStageB];
+  __shared__ f32x4 red[kMat][WK][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int kw = (((K + WK - 1) / WK) + 31) / 32 * 32;
+  const int k_begin = min(K, wave * kw), k_end = min(K, k_begin + kw);
+  const int nk = k_end - k_begin;               // a multiple of 32
+  const int nst = (nk + KS - 1) / KS;
+  char* ring = rings + wave * NSTG * kStageB;
+  // DMA lane roles as in gemv_dma_kernel: instruction i covers rows
+  // RPI i + lane / C of a row set (weight rows past N re-read row N - 1,
+  // activation rows past M row M - 1), logical chunk lc[i]
+  int row_b[IPM], xrow_b[IPM], lc[IPM];
+#pragma unroll
+  for (int i = 0; i < IPM; ++i) {
+    const int r = RPI * i + lane / C;
+    lc[i] = (lane % C) ^ (r % C);
+    row_b[i] = (min(n0 + r, N - 1) - n0) * (int)(w_rs * 2);
+    xrow_b[i] = min(r, M - 1) * (int)(x_rs * 2);
+  }
+  const char* wb = reinterpret_cast<const char*>(w + (long long)n0 * w_rs + k_begin);
+  const char* xb = reinterpret_cast<const char*>(x + k_begin);
+  auto issue = [&](int s) {
+    const uint32_t dst = lds_addr(ring + (s % NSTG) * kStageB);
+#pragma unroll
+    for (int i = 0; i < IPM; ++i) {
+      const int kk = min(s * KS + 8 * lc[i], nk - 8);
+#pragma unroll
+      for (int j = 0; j < kMat; ++j)
+        lds_dma16_sbase<true>(wb + (long long)j * N * w_rs * 2, (uint32_t)(row_b[i] + kk * 2),
+                              dst + j * kMatB + i * 1024);
+      lds_dma16_sbase<false>(xb, (uint32_t)(xrow_b[i] + kk * 2), dst + kMat * kMatB + i * 1024);
+    }
+  };
+  f32x4 acc[kMat];
+#pragma unroll
+  for (int j = 0; j < kMat; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < NSTG - 1 && s < nst; ++s) issue(s);
+  const bool xm = ln < M;
+  for (int s = 0; s < nst; ++s) {
+    wait_vm_stages<kPer, NSTG - 1>(min(NSTG - 2, nst - 1 - s));
+    if (s + NSTG - 1 < nst) issue(s + NSTG - 1);
+    const char* st = ring + (s % NSTG) * kStageB;
+#pragma unroll
+    for (int u = 0; u < KS / 32; ++u) {
+      if (s * KS + 32 * u < nk) {
+        const int off = ln * (KS * 2) + (((4 * u + lg) ^ (ln % C)) << 4);
+        const bf16x8_t b = xm ? *reinterpret_cast<const bf16x8_t*>(st + kMat * kMatB + off) : bf16x8_t{};
+#pragma unroll
+        for (int j = 0; j < kMat; ++j) {
+          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(st + j * kMatB + off);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+        }
+      }
+    }
+  }
+  gemv_finish<WK, GATED, 16>(red, acc, wave, lane, n0, bias, residual, r_rs, y, y_rs, M, N);
+}
+
 // The gated projection at more than four rows (the ten-row verify step): one
 // wave per workgroup walks all of K, requesting the next step's loads before
 // the current step's MFMAs and draining them after (the copy into the
@@ -875,6 +960,20 @@ int launch_gemv(const void* x, long long x_rs, const void* w, long long w_rs, co
   static_assert((kShortMaxK / 4) / 32 <= kShortSteps, "four waves cover K in kShortSteps steps each");
   if (M == 1 && use_dma(GATED ? 2 * N : N, K, wk, GATED))
     return launch_dma<GATED, false>(wk == 4 ? 4 : 8, x, w, w_rs, bias, residual, r_rs, y, N, K, nullptr, 0.f, st);
+  if (M > 1 && (long long)(GATED ? 2 * N : N) * K * 2 >= kDmaMinBytes) {
+    // several rows: the ring with per-stage activation slabs, four waves
+    // where gemv_waves picks four at up to four rows (and for every gated
+    // launch), else eight
+    const bool four = GATED || gemv_waves(1, N, K) == 4;
+    void (*kern)(const bf16_t*, long long, const bf16_t*, long long, const bf16_t*, const bf16_t*, long long,
+                 bf16_t*, long long, int, int, int);
+    if constexpr (GATED) kern = gemv_dma_rows_kernel<4, true>;
+    else kern = four ? gemv_dma_rows_kernel<4, false> : gemv_dma_rows_kernel<8, false>;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(four ? 256 : 512), 0, st, static_cast<const bf16_t*>(w), w_rs,
+                       static_cast<const bf16_t*>(x), x_rs, static_cast<const bf16_t*>(bias),
+                       static_cast<const bf16_t*>(residual), r_rs, static_cast<bf16_t*>(y), y_rs, M, N, K);
+    return launch_status();
+  }
   if constexpr (GATED) {
     if (wk == 4) launch(gemv_bf16_kernel<4, true>, blocks, 4);
     else if (wk == 2) launch(gemv_bf16_kernel<2, true>, blocks, 2);

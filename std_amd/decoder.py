@@ -23,8 +23,7 @@ prefill, which is not part of the decode path) use torch's rotary embedding
 and chunked fp32 matrix products.
 
 Decode and verify rows (at most 16) run their projections, norms and the
-MLP on the HIP GEMV and RMSNorm kernels (std_gemv, std_rms_norm), with
-hipBLASLt only for the ten-row q/k/v and lm_head projections; the prompt
+MLP on the HIP GEMV and RMSNorm kernels (std_gemv, std_rms_norm); the prompt
 prefill uses torch.
 """
 from __future__ import annotations
@@ -126,13 +125,13 @@ class RandomDecoder:
         return x.dtype == torch.bfloat16 and x.numel() // x.shape[-1] <= max_rows
 
     def _linear(self, x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
-                residual: Optional[torch.Tensor] = None, max_rows: int = 1) -> torch.Tensor:
+                residual: Optional[torch.Tensor] = None, max_rows: int = 16) -> torch.Tensor:
         """linear(x) (+ residual). bf16 projections of at most max_rows rows
         stream the weights through the HIP GEMV, with the residual add in its
-        epilogue; larger ones (prefill) use torch. max_rows is 1 for the q/k/v
-        and lm_head projections, where hipBLASLt is as fast or faster at ten
-        verify rows, and 16 for o and the MLP (measured at ten rows: o 11.2
-        vs 12.9 us, gate/up with the activation 58 vs 67, down 40 vs 49)."""
+        epilogue; larger ones (prefill) use torch. At the ten verify rows the
+        HIP GEMV beats hipBLASLt on every 7B projection (cold weights,
+        graph-replayed: q/k/v 11.3 vs 12.5 us, o 8.1 vs 13.0, lm_head 180 vs
+        238)."""
         if self._hip_rows(x, max_rows):
             return ops.linear(x, weight, bias, residual=residual)
         y = F.linear(x, weight, bias)
@@ -241,7 +240,7 @@ class RandomDecoder:
             if host_lengths:
                 kc.advance(n)
                 vc.advance(n)
-            return self._linear(out.transpose(1, 2).reshape(1, n, hq * d), p["o_w"], residual=residual, max_rows=16)
+            return self._linear(out.transpose(1, 2).reshape(1, n, hq * d), p["o_w"], residual=residual)
         q = qkv[..., :hq * d].view(1, n, hq, d).transpose(1, 2)
         k = qkv[..., hq * d:(hq + hkv) * d].view(1, n, hkv, d).transpose(1, 2)
         v = qkv[..., (hq + hkv) * d:].view(1, n, hkv, d).transpose(1, 2)

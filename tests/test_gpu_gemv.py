@@ -226,3 +226,45 @@ def test_gemv_norm_equals_rms_norm_then_gemv(N, K, gated, residual, bias):
                                                                                       eps=1e-6)
     h2 = ops.rms_norm(x2, nw, 1e-6)
     assert torch.equal(two, ops.gated_linear(h2, w, b) if gated else ops.linear(h2, w, b))
+
+
+@pytest.mark.parametrize("M,N,K,gated", [(10, 18944, 3584, True), (10, 3584, 18944, False), (16, 4608, 3584, False),
+                                         (2, 20000, 3584, False), (5, 9470, 3552, True), (10, 3584, 3584, False),
+                                         (7, 2350, 3616, False)])
+def test_gemv_lds_ring_rows(M, N, K, gated):
+    """Two to sixteen rows over a weight of 16 MiB or more stream through the
+    LDS ring with per-stage activation slabs (four waves, or eight where the
+    plain projection has fewer than 256 column blocks): the 7B verify shapes,
+    ragged column counts and K ranges that end inside a stage, rows read
+    through a row stride, against a float32 reference; the gated output is
+    within one bf16 ulp of silu(gate) * up formed from the plain projection
+    of the stacked weight (the same four-wave sums; torch's silu rounds
+    differently), the residual sum is the plain projection plus the residual
+    rounded once, and repeated calls are bit-identical."""
+    announce(f"gemv lds ring rows M={M} N={N} K={K} gated={gated}")
+    g = torch.Generator(device=dev()).manual_seed(M * 100 + N + K)
+    xs = torch.randn(1, M, K + 64, generator=g, device=dev()).to(torch.bfloat16)
+    x = xs[..., :K]                                           # row stride K + 64
+    NW = 2 * N if gated else N
+    w = (torch.randn(NW, K, generator=g, device=dev()) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(NW, generator=g, device=dev()) * 0.1).to(torch.bfloat16)
+    if gated:
+        got = ops.gated_linear(x, w, b)
+        gate, up = F.linear(x.float(), w.float(), b.float()).chunk(2, dim=-1)
+        torch.testing.assert_close(got.float(), F.silu(gate) * up, rtol=2e-2, atol=2e-3)
+        if (2 * N) // 16 >= 256:                          # the stacked plain projection: the same four-wave ring
+            pg, pu = ops.linear(x, w, b).chunk(2, dim=-1)
+            want = (F.silu(pg.float()).to(torch.bfloat16).float() * pu.float()).to(torch.bfloat16)
+            assert ((got.float() - want.float()).abs() <= _bf16_ulp(want.float())).all()
+        again = ops.gated_linear(x, w, b)
+    else:
+        r = (torch.randn(1, M, N, generator=g, device=dev()) * 2).to(torch.bfloat16)
+        got = ops.linear(x, w, b, residual=r)
+        ref = F.linear(x.float(), w.float(), b.float()) + r.float()
+        torch.testing.assert_close(got.float(), ref, rtol=2e-2, atol=2e-2)
+        plain = ops.linear(x, w, b)
+        torch.testing.assert_close(plain.float(), F.linear(x.float(), w.float(), b.float()), rtol=1e-2, atol=3e-3)
+        assert torch.equal(got, (r.float() + plain.float()).to(torch.bfloat16))
+        again = ops.linear(x, w, b, residual=r)
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
