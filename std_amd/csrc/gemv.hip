@@ -893,11 +893,15 @@ gemv_qkv_rope_dma_kernel(const bf16_t* __restrict__ w, long long w_rs, const bf1
                                       : v[i]);
 }
 
-// Waves per workgroup (the K split), from kernel durations at one and ten
-// rows on the 7B projection shapes (16-column blocks: q/k/v 288, o and down
-// 224, gate/up 1184 of 2368 stacked, lm_head 9504). The split is chosen from
-// the non-gated projection of all N_rows weight rows, so a gated launch adds
-// exactly the sums of the plain projection of its stacked [gate; up] weight:
+// Waves per workgroup (the K split). The register kernels below serve the
+// weights under kDmaMinBytes -- every 7B projection streams through the LDS
+// ring kernels instead, which take four waves where this picks four and eight
+// otherwise. The rule was fitted on the register kernels' durations at one and
+// ten rows on the 7B shapes (16-column blocks: q/k/v 288, o and down 224,
+// gate/up 1184 of 2368 stacked, lm_head 9504), the figures below. The split is
+// chosen from the non-gated projection of all N_rows weight rows, so a gated
+// launch adds exactly the sums of the plain projection of its stacked
+// [gate; up] weight:
 //  - up to kShortRows rows, K <= kShortMaxK and >= 256 blocks: four waves
 //    (a K range of at most 1024 = kShortSteps steps per wave) -- the short
 //    kernel, eight-column workgroups below 1024 blocks so the work spreads
@@ -913,10 +917,11 @@ inline int gemv_waves(int M, int n_rows, int K) {
 }
 
 // One row over a weight of at least kDmaMinBytes goes through the LDS ring
-// (gemv_dma_kernel, four waves where gemv_waves picks four, else eight): every
-// projection of a 7B decode step -- q/k/v (33 MB: 8.5 us against 11.6 us in
-// the short kernel), o (26 MB: 7.4 against 7.9 us), gate/up (271 MB), down
-// (136 MB) and lm_head (1.09 GB). Smaller weights keep the register kernels,
+// (gemv_dma_kernel, four waves where gemv_waves picks four, else eight; two to
+// sixteen rows through gemv_dma_rows_kernel): every projection of a 7B decode
+// step -- q/k/v (33 MB: 8.5 us against 11.6 us in the short kernel), o (26 MB:
+// 7.4 against 7.9 us), gate/up (271 MB), down (136 MB) and lm_head (1.09 GB)
+// -- and of the ten-row verify step. Smaller weights keep the register kernels,
 // whose single load round trip suits a launch of a few microseconds. The
 // waves' activation slices must fit the dynamic LDS, and a wave's slice pieces
 // plus its stages in flight the 63 outstanding vector-memory operations it can

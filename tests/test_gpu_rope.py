@@ -256,3 +256,31 @@ def test_qkv_rope_append_norm_limits():
         with pytest.raises(_lib.StdHipError):
             ops.qkv_rope_append(x, w, None, NQ, kc, kc.clone(), _scalar(0), _scalar(0), inv,
                                 norm_weight=torch.ones(K, dtype=torch.bfloat16, device=dev()), eps=1e-6)
+
+
+def test_qkv_rope_append_misaligned_bias_and_norm_weight():
+    """The one-row ring launch DMAs the bias and the norm weight in 16-byte
+    pieces; views that start 2 bytes into their buffer take the register
+    kernel instead, with the same results bit for bit (7B shape: both split K
+    over four waves in the same order)."""
+    announce("qkv_rope_append one row, bias and norm weight 2 bytes off 16-byte alignment")
+    g = torch.Generator(device=dev()).manual_seed(4242)
+    K, n_q, n_kv = 3584, 28, 4
+    NW = (n_q + 2 * n_kv) * D
+    x = (torch.randn(1, 1, K, generator=g, device=dev()) * 3).to(torch.bfloat16)
+    nw_buf = (1 + 0.2 * torch.randn(K + 8, generator=g, device=dev())).to(torch.bfloat16)
+    w = (torch.randn(NW, K, generator=g, device=dev()) * 0.03).to(torch.bfloat16)
+    b_buf = (torch.randn(NW + 8, generator=g, device=dev()) * 0.5).to(torch.bfloat16)
+    inv = torch.from_numpy(ref_rope.inv_freq(1e6, D)).to(dev())
+    for off_b, off_n in ((1, 0), (0, 1), (1, 1)):
+        b_view, nw_view = b_buf[off_b:off_b + NW], nw_buf[off_n:off_n + K]
+        b_al, nw_al = b_view.clone(), nw_view.clone()           # fresh, aligned copies of the same values
+        caches = [torch.full((1, n_kv, 40, D), float("nan"), dtype=torch.bfloat16, device=dev()) for _ in range(4)]
+        q = ops.qkv_rope_append(x, w, b_view, n_q, caches[0], caches[1], _scalar(17), _scalar(5000), inv,
+                                norm_weight=nw_view, eps=1e-6)
+        want = ops.qkv_rope_append(x, w, b_al, n_q, caches[2], caches[3], _scalar(17), _scalar(5000), inv,
+                                   norm_weight=nw_al, eps=1e-6)
+        torch.cuda.synchronize()
+        assert torch.equal(q, want), (off_b, off_n)
+        for got, ref in ((caches[0], caches[2]), (caches[1], caches[3])):
+            assert torch.equal(got.nan_to_num(7.0), ref.nan_to_num(7.0)), (off_b, off_n)
