@@ -214,6 +214,35 @@ def test_verify_append_matches_oracle(dtype, kv_len):
     assert torch.equal(vb[:, :, kv_len - Q:kv_len].cpu(), v[:, :, kv_len - Q:])
     assert torch.isnan(vb[:, :, kv_len:].float()).all()
     assert_close(out, ref.verify_attention(q, k, v), dtype)
+    sep = ops.verify_attention(q.to(dev()), kb[:, :, :kv_len], vb[:, :, :kv_len])
+    torch.cuda.synchronize()
+    assert torch.equal(out, sep)
+
+
+@pytest.mark.parametrize("Q,kv_len", [(40, 1000), (33, 2081)])
+def test_verify_append_many_rows(Q, kv_len):
+    """A fused append of 33-40 rows (one query head per KV head), across tile
+    and split boundaries: the new cache rows bit copies of the inputs,
+    nothing written past them, outputs against the oracle and equal bit for
+    bit to a plain verify over the appended cache."""
+    dtype = torch.bfloat16
+    gen = torch.Generator().manual_seed(Q * 7 + kv_len)
+    k = torch.randn(1, 4, kv_len, 128, generator=gen).to(dtype)
+    v = torch.randn(1, 4, kv_len, 128, generator=gen).to(dtype)
+    q = torch.randn(1, 4, Q, 128, generator=gen).to(dtype)
+    announce(f"verify_append Q={Q} kv_len={kv_len} group 1")
+    kb = cache_buffer(k[:, :, :kv_len - Q], kv_len + 9)
+    vb = cache_buffer(v[:, :, :kv_len - Q], kv_len + 9)
+    nk, nv = k[:, :, kv_len - Q:].to(dev()), v[:, :, kv_len - Q:].to(dev())
+    out = ops.verify_attention_append(q.to(dev()), kb, vb, nk, nv, kv_len)
+    torch.cuda.synchronize()
+    assert torch.equal(kb[:, :, kv_len - Q:kv_len].cpu(), k[:, :, kv_len - Q:])
+    assert torch.equal(vb[:, :, kv_len - Q:kv_len].cpu(), v[:, :, kv_len - Q:])
+    assert torch.isnan(kb[:, :, kv_len:].float()).all()
+    assert_close(out, ref.verify_attention(q, k, v), dtype)
+    sep = ops.verify_attention(q.to(dev()), kb[:, :, :kv_len], vb[:, :, :kv_len])
+    torch.cuda.synchronize()
+    assert torch.equal(out, sep)
 
 
 @pytest.mark.parametrize("dtype,S,B", [(torch.bfloat16, 1034, 28), (torch.float32, 1024, 3), (torch.bfloat16, 16384, 4),
