@@ -124,7 +124,7 @@ def coll_extra_bytes(n_kv, q, n_vis):
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
+        print(json.dumps({"error": "the bench runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
                                    "design note, not a measured configuration)"}))
         sys.exit(2)
     import torch

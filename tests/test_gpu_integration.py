@@ -1,4 +1,5 @@
-"""The reference-side binding of INTEGRATION.md, run as written: the `hip`
+"""The reference-side binding snippets of the repository's integration guide,
+run as written: the `hip`
 branch of _sparse_aware_attention_forward (section 3, replacing
 src/std_repro/std_qwen25vl.py:395-431) and the verify patch of
 Qwen2_5_VLSdpaAttention.forward (section 4, replacing
