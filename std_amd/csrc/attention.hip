@@ -401,80 +401,8 @@ __device__ __forceinline__ void merge_row_wave(const PT* __restrict__ ws_o, cons
   }
 }
 
-// Merge, quarter-wave form (kWaveMergeMax < n_split <= kQuarterMergeMax: the
-// 128k verify and dense decode, 64 splits per KV head): one wave per row.
-// Quarter qq (lanes 16 qq .. 16 qq + 15) takes the splits qq, qq + 4, ...
-// (at most 16) and lane c of a quarter the row's columns 8c .. 8c + 7, so
-// every lane issues all of its loads -- 16 (m, l) pairs and 16 (fp16) or 32
-// (fp32) 16-byte partial loads -- before any arithmetic; loads past the last
-// split are masked by bounded buffer resources. The quarters combine through
-// two lane swaps (quarters 0 + 1 and 2 + 3, then the two pairs), with no LDS
-// and no barrier, in a fixed order, so the result is deterministic.
-constexpr int kQuarterMergeMax = 64;
-
-template <typename T, typename PT>
-__device__ __forceinline__ void merge_row_quarter(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
-                                                  T* __restrict__ out, int n_split, int q_len, int group,
-                                                  long long out_bs, int n_kv, int r, int g, int bz, int lane) {
-  constexpr int J = kQuarterMergeMax / 4;
-  const int c = lane & 15, qq = lane >> 4;
-  const int R = group * q_len;
-  out += bz * out_bs;
-  const long long base = ((long long)bz * n_kv + g) * n_split * R + r;
-  const uint32_t step_b = (uint32_t)(R * D * sizeof(PT));
-  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(ws_o + base * D), (short)0, (int)((n_split - 1) * step_b + D * sizeof(PT)), kBufWord3);
-  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(ws_ml + base), (short)0, (int)((n_split - 1) * R * 8 + 8), kBufWord3);
-  float2 ml[J];
-  f32x4 pa[J], pb[J];                              // columns 8c .. 8c + 3 and 8c + 4 .. 8c + 7
-  typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const uint32_t sp = qq + 4 * j;
-    ml[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rm, sp * R * 8, 0, 0));
-    if constexpr (sizeof(PT) == 4) {
-      pa[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, sp * step_b + 32 * c, 0, 0));
-      pb[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, sp * step_b + 32 * c + 16, 0, 0));
-    } else {
-      const half8_t h = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ro, sp * step_b + 16 * c, 0, 0));
-      pa[j] = __builtin_convertvector(__builtin_shufflevector(h, h, 0, 1, 2, 3), f32x4);
-      pb[j] = __builtin_convertvector(__builtin_shufflevector(h, h, 4, 5, 6, 7), f32x4);
-    }
-  }
-  float M = -1e30f, L = 0.f;
-#pragma unroll
-  for (int j = 0; j < J; ++j)
-    if (qq + 4 * j < n_split) M = fmaxf(M, ml[j].x);
-  M = xor32_max(xor16_max(M));
-  f32x4 oa = {0.f, 0.f, 0.f, 0.f}, ob = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < J; ++j)
-    if (qq + 4 * j < n_split) {
-      const float e = fast_exp2(ml[j].x - M);
-      L += ml[j].y * e;
-      oa += pa[j] * e;
-      ob += pb[j] * e;
-    }
-  L = xor32_sum(xor16_sum(L));
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    oa[e] = xor32_sum(xor16_sum(oa[e]));
-    ob[e] = xor32_sum(xor16_sum(ob[e]));
-  }
-  if (qq == 0) {
-    const int hl = r / q_len, i = r - hl * q_len;
-    T* dst = out + ((long long)(g * group + hl) * q_len + i) * D + 8 * c;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      dst[e] = from_f32<T>(oa[e] / L);
-      dst[4 + e] = from_f32<T>(ob[e] / L);
-    }
-  }
-}
-
-// Merge, block form (more than kQuarterMergeMax splits: verifies and dense
-// decodes over fewer than four KV heads): four waves per row, wave w taking the splits [w per, (w + 1) per)
+// Merge, block form (more than kWaveMergeMax splits: long verifies and dense
+// decodes): four waves per row, wave w taking the splits [w per, (w + 1) per)
 // with per = ceil(n_split / 4), in passes of 16 laid out as in the wave form
 // (buffer resources bounded at the wave's last split). Every wave first forms
 // the row's maximum over all splits from one (m, l) load per lane and a
@@ -561,8 +489,7 @@ __device__ __forceinline__ void merge_row_block(const PT* __restrict__ ws_o, con
 }
 
 // grid (R, n_kv, n_batch): block (r, g, b) merges row r of KV head g of
-// problem b; J == 0: the block form (kMergeThreads threads); J ==
-// kQuarterMergeMax: the quarter-wave form (one wave); otherwise the
+// problem b; J == 0: the block form (kMergeThreads threads), otherwise the
 // wave form (one wave).
 template <typename T, typename PT, int J>
 __global__ void __launch_bounds__(J == 0 ? kMergeThreads : 64)
@@ -573,9 +500,6 @@ attn_merge_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
 #endif
   if constexpr (J == 0)
     merge_row_block<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y);
-  else if constexpr (J == kQuarterMergeMax)
-    merge_row_quarter<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y,
-                             blockIdx.z, threadIdx.x);
   else
     merge_row_wave<T, PT, J>(ws_o, ws_ml, out, n_split, q_len, group, out_bs, n_kv, blockIdx.x, blockIdx.y,
                              blockIdx.z, threadIdx.x);
@@ -719,14 +643,9 @@ merge_coll_kernel(const PT* __restrict__ ws_o, const float2* __restrict__ ws_ml,
       merge_row_block<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, blockIdx.x, blockIdx.y);
     } else {
       const int r = 4 * blockIdx.x + (threadIdx.x >> 6);
-      if constexpr (J == kQuarterMergeMax) {
-        if (r < n_rows)
-          merge_row_quarter<T, PT>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, r, blockIdx.y, 0,
-                                   threadIdx.x & 63);
-      } else if (r < n_rows) {
+      if (r < n_rows)
         merge_row_wave<T, PT, J>(ws_o, ws_ml, out, n_split, q_len, group, 0LL, gridDim.y, r, blockIdx.y, 0,
                                  threadIdx.x & 63);
-      }
     }
   } else {
     coll_finish(logits, stats, co, q_len, n_split, n_vtiles, vis_begin, vis_end, blockIdx.x - n_row_blocks,
@@ -1809,22 +1728,17 @@ void launch_h16(const void* q, void* k, void* v, void* out, int q_len, int kv_le
                      GatherDev{ga.status, ga.idx_hs, ga.n_idx, ga.dense_rows, ga.k, ga.v, ga.k_hs, ga.v_hs}, ga.idx);
 }
 
-// The merge launch: the wave form up to kWaveMergeMax splits, the
-// quarter-wave form up to kQuarterMergeMax, the block form beyond.
+// The merge launch: the wave form up to kWaveMergeMax splits, the block
+// form beyond.
 template <typename T, typename PT>
 void launch_merge(const void* ws_o, const float2* ws_ml, void* out, int n_split, int q_len, int group, long long out_bs,
                   int n_kv, int R, int n_batch, hipStream_t st) {
   const dim3 grid(R, n_kv, n_batch);
   const PT* o = static_cast<const PT*>(ws_o);
   T* y = static_cast<T*>(out);
-  if (n_split > kQuarterMergeMax) {
+  if (n_split > kWaveMergeMax) {
     hipLaunchKernelGGL((attn_merge_kernel<T, PT, 0>), grid, dim3(kMergeThreads), 0, st, o, ws_ml, y, n_split, q_len,
                        group, out_bs, n_kv);
-    return;
-  }
-  if (n_split > kWaveMergeMax) {
-    hipLaunchKernelGGL((attn_merge_kernel<T, PT, kQuarterMergeMax>), grid, dim3(64), 0, st, o, ws_ml, y, n_split,
-                       q_len, group, out_bs, n_kv);
     return;
   }
   const int j = merge_j(n_split);
@@ -2054,13 +1968,12 @@ int verify_collect_entry(const void* q, void* k, void* v, void* out, int n_q, in
                          BatchStrides{0, 0, 0, 0, 0}, len_dev, ca, nullptr);
       const int s = launch_status();
       if (s != 0) return s;
-      const bool wave = p.n_split <= kQuarterMergeMax;
-      const int mj = p.n_split <= kWaveMergeMax ? merge_j(p.n_split) : wave ? kQuarterMergeMax : 0;
+      const bool wave = p.n_split <= kWaveMergeMax;
+      const int mj = wave ? merge_j(p.n_split) : 0;
       const dim3 mgrid((wave ? (n_rows + 3) / 4 : n_rows) + (cl.n_vtiles + 15) / 16, n_kv);
       auto mkern = mj == 0 ? merge_coll_kernel<E, PT, 0> : mj == 4 ? merge_coll_kernel<E, PT, 4>
                  : mj == 8 ? merge_coll_kernel<E, PT, 8> : mj == 9 ? merge_coll_kernel<E, PT, 9>
-                 : mj == 12 ? merge_coll_kernel<E, PT, 12> : mj == 16 ? merge_coll_kernel<E, PT, 16>
-                 : merge_coll_kernel<E, PT, kQuarterMergeMax>;
+                 : mj == 12 ? merge_coll_kernel<E, PT, 12> : merge_coll_kernel<E, PT, 16>;
       hipLaunchKernelGGL(mkern, mgrid, dim3(kMergeThreads), 0, st, static_cast<const PT*>(ws_o), ws_ml,
                          static_cast<E*>(oa), p.n_split, qc, group, n_rows, ca.logits, ca.stats, co, cl.n_vtiles,
                          vis_begin, vis_end);

@@ -1,13 +1,10 @@
-"""The split-partial merge in its three forms: one wave per row with the
-splits dealt to its two half-waves (at most 32 splits per KV head; loads past
-the last split fall outside a bounded buffer resource), one wave per row with
-the splits dealt to its four quarter-waves (33-64 splits, the 128k verify and
-dense decode) and one 256-thread block per row (more splits). Decodes and
+"""The split-partial merge in both of its forms: one wave per row (at most 32
+splits per KV head; its loads past the last split fall outside a bounded
+buffer resource) and one 256-thread block per row (more splits). Decodes and
 verifies at key counts whose split plans cover every wave-merge instance
-(4, 8, 9, 12 and 16 splits per half-wave), the quarter-wave form and the block
-form, against the fp64 oracle, with NaN past the valid cache rows; the
-collector verify equals the plain verify bit for bit in the wave and
-quarter-wave forms too."""
+(4, 8, 9, 12 and 16 splits per half-wave) and the block form, against the
+fp64 oracle, with NaN past the valid cache rows; the collector verify equals
+the plain verify bit for bit in the wave form too."""
 import numpy as np
 import pytest
 import torch
@@ -23,14 +20,12 @@ N_KV, GROUP = 4, 7
 
 
 def _wave_j(n_split):
-    """The wave merge's splits per half-wave (the library's merge_j),
-    "quarter" for the quarter-wave form, None for the block form."""
+    """The wave merge's splits per half-wave (the library's merge_j), None for
+    the block form."""
     if n_split <= 1:
         return "unsplit"
-    if n_split > 64:
-        return None
     if n_split > 32:
-        return "quarter"
+        return None
     return 4 if n_split <= 8 else 8 if n_split <= 16 else 9 if n_split <= 18 else 12 if n_split <= 24 else 16
 
 
@@ -44,9 +39,7 @@ DECODE_KV = (130, 500, 1000, 1030, 1090, 1500, 2000, 4100, 9000)
 
 def test_decode_lengths_cover_every_merge_form():
     forms = {_wave_j(_splits(GROUP, kv, torch.bfloat16)) for kv in DECODE_KV}
-    assert {4, 8, 9, 12, 16, "quarter"} <= forms, forms
-    # more than 64 splits per KV head: the fp32 kernel's plan (two workgroups per CU)
-    assert None in {_wave_j(_splits(GROUP, kv, torch.float32)) for kv in DECODE_KV}
+    assert {4, 8, 9, 12, 16, None} <= forms, forms
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -85,25 +78,3 @@ def test_verify_merge_forms_match_oracle_and_collector(kv, q_len):
     assert torch.equal(out_c, got), "collector verify differs from the plain verify"
     want = ref_coll.verification_scores(q, k, np.arange(vis_end))
     np.testing.assert_allclose(scores.double().cpu().numpy(), want, rtol=2e-4, atol=1e-9)
-
-
-@pytest.mark.parametrize("n_kv,dtype,kv", [(2, torch.bfloat16, 9000), (4, torch.float32, 9000),
-                                           (2, torch.bfloat16, 4106), (2, torch.bfloat16, 2058)])
-def test_verify_block_and_quarter_forms_over_other_head_counts(n_kv, dtype, kv):
-    """Verify with more than 64 splits per KV head (two KV heads in bf16 over
-    65 or more tiles, or the fp32 kernel's plan) takes the block form, two KV
-    heads over 33 tiles the quarter-wave form: against the oracle,
-    deterministic."""
-    q_len = 10
-    code = {torch.bfloat16: _lib.STD_BF16, torch.float32: _lib.STD_F32}[dtype]
-    n_split = _lib.load_library().std_attn_split_count(n_kv, GROUP * q_len, kv, code)
-    announce(f"merge verify n_kv={n_kv} {dtype} kv={kv} splits={n_split} form={_wave_j(n_split)}")
-    g = torch.Generator().manual_seed(9300 + kv + n_kv)
-    q = torch.randn(1, n_kv * GROUP, q_len, 128, generator=g).to(dtype)
-    k = torch.randn(1, n_kv, kv, 128, generator=g).to(dtype)
-    v = torch.randn(1, n_kv, kv, 128, generator=g).to(dtype)
-    kc, vc = cache_buffer(k, kv + 40), cache_buffer(v, kv + 40)
-    got = ops.verify_attention(q.to(dev()), kc[:, :, :kv], vc[:, :, :kv])
-    assert_close(got, ref.verify_attention(q, k, v), dtype)
-    again = ops.verify_attention(q.to(dev()), kc[:, :, :kv], vc[:, :, :kv])
-    assert torch.equal(got, again), "merge not deterministic"
