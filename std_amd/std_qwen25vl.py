@@ -344,8 +344,11 @@ class VerificationCollectorV3:
     gathered visual keys in separate GEMMs, each layer's scores here come out
     of the verify attention launch itself (``ops.verify_attention_collect``):
     the collector's query rows ride the verify kernel's padding rows, so the
-    visual keys are read once. Any ascending set of visual positions is
-    served (the hook gathers key_states at visual_positions); a verify of more
+    visual keys are read once. Any set of visual positions is served, in any
+    order and with repeats, as the hook gathers key_states at visual_positions:
+    the launches score the sorted distinct positions and the readback puts
+    their scores in the caller's order (a repeated position repeats its
+    score); a verify of more
     positions than one launch carries ((group + 1) * q_len > 80, e.g. gamma >=
     10 at seven query heads per KV head) runs in chunks of positions. Each
     layer's scores land in one persistent device buffer, so a verify step
@@ -362,9 +365,13 @@ class VerificationCollectorV3:
         self.visual_positions = pos
         self.visual_len = int(pos.numel())
         self.num_kv_heads = model.config.num_key_value_heads
-        self.visual = ops.visual_keys(pos, model.device)       # raises unless strictly ascending
+        # the launches score the sorted distinct positions; _order maps them
+        # back to the caller's order (None: the positions are already that)
+        distinct, inverse = torch.unique(pos, sorted=True, return_inverse=True)
+        self._order = None if distinct.numel() == pos.numel() and torch.equal(distinct, pos) else inverse
+        self.visual = ops.visual_keys(distinct, model.device)
         self.vis_begin, self.vis_end = self.visual.begin, self.visual.end
-        self.scores_dev = torch.zeros(model.config.num_hidden_layers, self.num_kv_heads, self.visual_len,
+        self.scores_dev = torch.zeros(model.config.num_hidden_layers, self.num_kv_heads, int(distinct.numel()),
                                       dtype=torch.float32, device=model.device)
         self.rounds: List[torch.Tensor] = []
         self.active = False
@@ -422,6 +429,8 @@ class VerificationCollectorV3:
             stacked = self.scores_dev.cpu()                                  # single sync
         else:
             stacked = self.scores_dev[torch.tensor(order, device=self.scores_dev.device)].cpu()
+        if self._order is not None:
+            stacked = stacked[:, :, self._order]
         self.collect_time += time.perf_counter() - t0
         self.rounds.append(stacked)
         self._layers = []

@@ -354,3 +354,43 @@ def test_collector_records_every_round_of_a_long_verify():
         q_rows = res.proposed_lengths[r] + res.pending_lengths[r]
         assert sc.shape == (cfg.num_hidden_layers, cfg.num_key_value_heads, positions.numel())
         np.testing.assert_allclose(sc.double().sum(-1).numpy(), q_rows, rtol=1e-4)
+
+
+def test_collector_class_takes_positions_in_any_order_with_repeats():
+    """The reference's hook gathers key_states at visual_positions as given
+    (dynamic_selection.py:515), so a collector built on a shuffled position
+    list with repeats reports, position for position, the scores that the
+    collector on the sorted distinct list reports for those positions (bit for
+    bit: the launches score the sorted distinct set either way)."""
+    from std_amd.decoder import DecoderConfig, RandomDecoder
+    from std_amd.kv_cache import initialize_past_key_values
+    from std_amd.std_qwen25vl import VerificationCollectorV3, prefill_prompt
+
+    announce("collector class: visual positions shuffled, with repeats")
+    cfg = DecoderConfig.tiny(layers=2)
+    model = RandomDecoder(cfg, dev(), torch.bfloat16, seed=5007)
+    gen = torch.Generator().manual_seed(23)
+    n_vis, n_text, Q = 900, 24, 10
+    ids = torch.cat([torch.full((n_vis,), cfg.video_token_id),
+                     torch.randint(0, cfg.vocab_size - 2, (n_text,), generator=gen)]).view(1, -1).to(dev())
+    vis = torch.randn(n_vis, cfg.hidden_size, generator=gen).to(dev(), torch.bfloat16)
+    P = n_vis + n_text
+    step = torch.randint(0, cfg.vocab_size - 2, (1, Q), generator=gen).to(dev())
+    sorted_pos = torch.arange(0, n_vis, 3)                       # every third visual position (a bit mask)
+    given = torch.cat([sorted_pos[torch.randperm(sorted_pos.numel(), generator=gen)], sorted_pos[:17].flip(0)])
+    scores = []
+    for positions in (sorted_pos, given):
+        pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.bfloat16, P + 32)
+        prefill_prompt(model, {"input_ids": ids, "visual_embeds": vis}, pkv, cfg.video_token_id)
+        coll = VerificationCollectorV3(model, positions)
+        coll.install()
+        coll.begin_verification(0)
+        model(step, pkv, all_logits=True)
+        coll.end_verification()
+        coll.uninstall()
+        scores.append(coll.latest_scores())
+        assert coll.visual_len == positions.numel()
+    base, got = scores
+    assert got.shape == (cfg.num_hidden_layers, cfg.num_key_value_heads, given.numel())
+    rank = torch.searchsorted(sorted_pos, given)
+    assert torch.equal(got, base[:, :, rank])
