@@ -20,20 +20,23 @@ bonus-token append. What changes underneath:
 * acceptance and rollback are computed on the device, and draft tokens stay
   on the device, so a round reads back a handful of int32 values once.
 
-Only ``verify_mode="parallel"`` with ``verify_fallback="none"`` (the
-reference defaults) is provided; the reference's optional sequential
-fallbacks and margin re-runs are outside the hot path and raise.
+``verify_mode="sequential"``, the sequential verify fallbacks and the
+margin checks (std_qwen25vl.py:780-893) run as the reference runs them, one
+dense q_len = 1 forward per verified token, in the eagerly launched loop
+(use_graphs=False, the default); the margin re-verification with the math
+SDPA backend is counted, since the HIP verify computes that definition.
 """
 from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
-from typing import Dict, List, Optional, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 
 from . import ops
 from .kv_cache import KVCache, fill_cache_length, initialize_past_key_values
+from .verification_policy import VERIFY_FALLBACKS, min_prediction_margin, needs_sequential_fallback
 
 # "hip" and the reference's three mode names (std_qwen25vl.py:239-240), which
 # all compute the same draft attention: each runs the HIP decode kernel here.
@@ -497,6 +500,41 @@ def _draft_tokens(model, first_token: torch.Tensor, gamma: int, past_key_values,
     return torch.cat(drafted)
 
 
+def _append_dense_tokens(model, tokens, past_key_values) -> torch.Tensor:
+    """One dense forward over ``tokens`` at the cache's length; returns the
+    [1, 1] next token (std_qwen25vl.py:467-471)."""
+    ids = torch.as_tensor(list(tokens) if not torch.is_tensor(tokens) else tokens, dtype=torch.long)
+    return _token_argmax(model(ids.reshape(1, -1).to(model.device), past_key_values))
+
+
+def _sequential_verify(model, draft: torch.Tensor, dense_next: torch.Tensor, dense_pkv) -> torch.Tensor:
+    """Verify the drafted tokens one dense q_len = 1 forward at a time from a
+    cache that holds everything before them (std_qwen25vl.py:885-893): the
+    accepted length a is the longest prefix of the draft that the dense model
+    predicts token by token, starting from dense_next; each accepted token is
+    forwarded (its K/V cached), and the prediction after the last one is the
+    bonus. Returns the device int32 pair (a, bonus)."""
+    drafted = draft.reshape(-1).tolist()
+    nxt = dense_next.reshape(1, 1)
+    a = 0
+    while a < len(drafted) and drafted[a] == int(nxt.reshape(-1)[0]):
+        nxt = _token_argmax(model(draft.reshape(-1)[a:a + 1].reshape(1, 1).to(torch.long), dense_pkv))
+        a += 1
+    return torch.tensor([a, int(nxt.reshape(-1)[0])], dtype=torch.int32, device=model.device)
+
+
+def _sequential_verify_draft(model, draft: torch.Tensor, dense_pending: Sequence[int], dense_next: torch.Tensor,
+                             dense_pkv, dense_lengths: torch.Tensor, dense_cached_len: int) -> Tuple[int, int]:
+    """Replay one round's verification sequentially (std_qwen25vl.py:504-528):
+    roll the dense cache back to dense_cached_len, cache the pending tokens
+    with one dense forward (its prediction replaces dense_next), then verify
+    the draft one token at a time. Returns (accepted length, bonus token)."""
+    fill_cache_length(dense_lengths, dense_cached_len)
+    nxt = _append_dense_tokens(model, dense_pending, dense_pkv) if dense_pending else dense_next
+    a, bonus = _sequential_verify(model, draft, nxt, dense_pkv).tolist()
+    return int(a), int(bonus)
+
+
 def _append_sparse_tokens(model, tokens: torch.Tensor, past_key_values, sparse_controller: SparseDraftController,
                           start_position: int) -> torch.Tensor:
     """Cache the bonus token in the sparse cache (std_qwen25vl.py:474-494)."""
@@ -645,6 +683,17 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     math re-verification does (std_qwen25vl.py:843-858); that re-run would
     return the same predictions, so ``fallback_accepted_extra`` stays 0.
 
+    verify_mode="sequential", verify_fallback and verify_margin_threshold:
+    as in the reference (std_qwen25vl.py:780-893): sequential verification
+    and the sequential replay of a round (counted in ``fallback_count``, its
+    extra accepted tokens in ``fallback_accepted_extra``) run one dense
+    q_len = 1 forward per verified token; a round whose smallest committed
+    top-1/top-2 logit margin falls below the threshold counts a math
+    re-verification in ``verify_margin_reruns`` (the HIP verify is that
+    definition already), and ``min_verify_margin`` is the smallest margin
+    seen. These host-side decisions need the eager loop: with use_graphs=True
+    they raise ValueError.
+
     sparse_kv: "compact" gathers the selected prompt rows into the sparse
     cache; "indexed" (bf16, fp16) has the draft read them from the dense cache
     through the per-head index lists instead (same keys, same results).
@@ -660,19 +709,28 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         raise ValueError(f"Unsupported sparse_kv={sparse_kv!r}; choose one of {sorted(SPARSE_KV_MODES)}.")
     if sparse_kv == "indexed" and model.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("the index-addressed sparse cache serves bf16 and fp16 models")
-    if verify_mode != "parallel":
-        raise ValueError(f"Unsupported verify_mode={verify_mode!r}; the HIP path implements 'parallel'.")
-    if verify_fallback != "none" or verify_margin_threshold is not None:
-        raise ValueError("verify fallbacks and margin re-runs are not part of the HIP decode path")
+    if verify_mode not in {"parallel", "sequential"}:
+        raise ValueError(f"Unsupported verify_mode={verify_mode!r}; expected 'parallel' or 'sequential'.")
+    if verify_fallback not in VERIFY_FALLBACKS:
+        raise ValueError("verify_fallback must be 'none', 'sequential_on_reject', "
+                         "'sequential_on_low_accept', 'sequential_on_low_margin', or 'sequential_guard'.")
+    if sequential_fallback_max_accept < 0:
+        raise ValueError("sequential_fallback_max_accept must be non-negative.")
+    if verify_fallback == "sequential_on_low_margin" and verify_margin_threshold is None:
+        raise ValueError("sequential_on_low_margin requires verify_margin_threshold.")
     if verify_attn_backend not in {"default", "math", "math_on_full_accept"}:
         raise ValueError("verify_attn_backend must be 'default', 'math', or 'math_on_full_accept'.")
+    if verify_margin_threshold is not None and verify_margin_threshold < 0:
+        raise ValueError("verify_margin_threshold must be non-negative.")
+    if use_graphs and (verify_mode != "parallel" or verify_fallback != "none" or verify_margin_threshold is not None):
+        raise ValueError("use_graphs=True replays the parallel verify with no host-side fallback; run "
+                         "verify_mode='sequential', verify fallbacks and margin checks with use_graphs=False")
     if adaptive_gamma_min is not None and not (1 <= adaptive_gamma_min <= gamma):
         raise ValueError("adaptive_gamma_min must be between 1 and gamma.")
     if adaptive_gamma_mode not in {"accept_len", "conservative"}:
         raise ValueError("adaptive_gamma_mode must be 'accept_len' or 'conservative'.")
     if not copy_sparse_prefill:
         raise ValueError("the sparse cache is always gathered from the dense prefill")
-    del sequential_fallback_max_accept
     dev = model.device
 
     torch.cuda.synchronize()
@@ -724,6 +782,8 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     gamma_history: List[int] = []
     dense_pending: List[int] = []
     accepted_total = proposed_total = decode_rounds = fallback_count = 0
+    fallback_accepted_extra = verify_margin_reruns = 0
+    verify_margins: List[float] = []
     draft_time = verify_time = bonus_time = cache_adjust_time = 0.0
     current_gamma = gamma
     dense_next_i32 = dense_next.reshape(1).to(torch.int32)
@@ -833,6 +893,15 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         replay = use_graphs and bool(dense_pending) and propose_len == gamma
         if replay and graphs is None:
             graphs = capture_round()
+        if verify_mode == "sequential" and dense_pending:
+            # sequential verification starts from a dense cache that holds the
+            # pending bonus token (std_qwen25vl.py:785-791)
+            stage = _profile_mark(profile_decode)
+            fill_cache_length(dense_lengths, dense_cached_len)
+            dense_next = _append_dense_tokens(model, dense_pending, dense_pkv)
+            dense_pending = []
+            dense_cached_len = context_len
+            cache_adjust_time += _profile_mark(profile_decode) - stage
 
         stage = _profile_mark(profile_decode)
         if replay:
@@ -849,7 +918,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         pending_lengths.append(len(dense_pending))
 
         stage = _profile_mark(profile_decode)
-        trace = _TRACE_COLLECTOR
+        trace = _TRACE_COLLECTOR if verify_mode == "parallel" else None
         if trace is not None:
             trace.begin_verification(decode_rounds)
         current = getattr(model, "verify_collector", None)
@@ -870,6 +939,8 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
             last_logits[0] = graphs[3][0]
         elif use_graphs:
             res = verify_phase(draft_dev, bool(dense_pending))
+        elif verify_mode == "sequential":
+            res = _sequential_verify(model, draft_dev, dense_next, dense_pkv)
         else:
             if dense_pending:
                 pend = torch.tensor(dense_pending, dtype=torch.long).to(dev, non_blocking=True)
@@ -885,10 +956,33 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         host = torch.cat([res[:2], status, draft_dev.to(torch.int32)]).tolist()     # the round's one readback
         accept_len, bonus_token, draft = host[0], host[1], host[3:]
         _check_decode_status(host[2])
+        if verify_mode == "parallel":
+            low_margin = False
+            if verify_margin_threshold is not None:
+                margin = min_prediction_margin(last_logits[0].unsqueeze(0), range(accept_len + 1),
+                                               has_dense_pending=bool(dense_pending))
+                if margin is not None:
+                    verify_margins.append(margin)
+                low_margin = margin is not None and margin < verify_margin_threshold
+                if low_margin and verify_fallback != "sequential_on_low_margin":
+                    # the reference re-verifies with the math SDPA backend
+                    # (std_qwen25vl.py:824-840); the HIP verify computes the
+                    # math definition, so that re-run predicts these tokens
+                    verify_margin_reruns += 1
+            fallback_count += math_reverify_count(verify_attn_backend, accept_len, propose_len)
+            if needs_sequential_fallback(verify_fallback, accept_len=accept_len, draft_len=len(draft),
+                                         sequential_fallback_max_accept=sequential_fallback_max_accept,
+                                         low_margin=low_margin):
+                fallback_count += 1
+                if low_margin and verify_fallback == "sequential_on_low_margin":
+                    verify_margin_reruns += 1
+                seq_accept, seq_bonus = _sequential_verify_draft(model, draft_dev, dense_pending, dense_next,
+                                                                 dense_pkv, dense_lengths, dense_cached_len)
+                fallback_accepted_extra += max(0, seq_accept - accept_len)
+                accept_len, bonus_token = seq_accept, seq_bonus
         verify_time += _profile_mark(profile_decode) - stage
         accept_lengths.append(accept_len)
         accepted_total += accept_len
-        fallback_count += math_reverify_count(verify_attn_backend, accept_len, propose_len)
         if adaptive_gamma_min is not None:
             if accept_len < propose_len:
                 if adaptive_gamma_mode == "accept_len":
@@ -951,7 +1045,9 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         draft_time=draft_time, verify_time=verify_time, bonus_time=bonus_time, cache_adjust_time=cache_adjust_time,
         cache_init_time=cache_init_time, prefill_time=selection_prefill_time,
         selection_prefill_time=selection_prefill_time, selection_time=selection_time, dense_prefill_time=0.0,
-        sparse_cache_time=sparse_cache_time, fallback_count=fallback_count)
+        sparse_cache_time=sparse_cache_time, fallback_count=fallback_count,
+        fallback_accepted_extra=fallback_accepted_extra, verify_margin_reruns=verify_margin_reruns,
+        min_verify_margin=min(verify_margins) if verify_margins else 0.0)
     return result, selection
 
 

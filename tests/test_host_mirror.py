@@ -98,11 +98,31 @@ def test_controller_validates_mode():
     assert c.enabled
 
 
-@pytest.mark.parametrize("kwargs", [dict(verify_mode="sequential"), dict(verify_fallback="sequential_on_reject"),
+@pytest.mark.parametrize("kwargs", [dict(verify_mode="tree"), dict(verify_fallback="always"),
+                                    dict(sequential_fallback_max_accept=-1),
+                                    dict(verify_fallback="sequential_on_low_margin"),
+                                    dict(verify_margin_threshold=-0.5),
+                                    dict(verify_mode="sequential", use_graphs=True),
+                                    dict(verify_fallback="sequential_on_reject", use_graphs=True),
+                                    dict(verify_margin_threshold=0.5, use_graphs=True),
                                     dict(adaptive_gamma_min=0), dict(verify_attn_backend="flash"),
                                     dict(copy_sparse_prefill=False), dict(sparse_kv="paged")])
 def test_std_generate_rejects_unsupported_options(kwargs):
     with pytest.raises(ValueError):
+        std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
+
+
+@pytest.mark.parametrize("kwargs", [dict(verify_mode="sequential"), dict(verify_fallback="sequential_on_reject"),
+                                    dict(verify_fallback="sequential_on_low_accept",
+                                         sequential_fallback_max_accept=0),
+                                    dict(verify_fallback="sequential_guard"),
+                                    dict(verify_fallback="sequential_on_low_margin", verify_margin_threshold=0.1),
+                                    dict(verify_margin_threshold=0.0)])
+def test_std_generate_accepts_the_reference_verify_options(kwargs):
+    """The reference's verify modes, fallbacks and margin threshold
+    (std_qwen25vl.py:634-660) pass validation: the call then fails on the
+    missing model, not on the option."""
+    with pytest.raises(AttributeError):
         std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
 
 
