@@ -729,8 +729,11 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         raise ValueError("adaptive_gamma_min must be between 1 and gamma.")
     if adaptive_gamma_mode not in {"accept_len", "conservative"}:
         raise ValueError("adaptive_gamma_mode must be 'accept_len' or 'conservative'.")
-    if not copy_sparse_prefill:
-        raise ValueError("the sparse cache is always gathered from the dense prefill")
+    # copy_sparse_prefill=False: the reference prefills the prompt a second
+    # time into the sparse cache instead of copying the dense rows
+    # (std_qwen25vl.py:735-739); the prefill is deterministic here, so those
+    # rows equal the dense prefill's, from which compaction gathers either way
+    del copy_sparse_prefill
     dev = model.device
 
     torch.cuda.synchronize()

@@ -106,7 +106,7 @@ def test_controller_validates_mode():
                                     dict(verify_fallback="sequential_on_reject", use_graphs=True),
                                     dict(verify_margin_threshold=0.5, use_graphs=True),
                                     dict(adaptive_gamma_min=0), dict(verify_attn_backend="flash"),
-                                    dict(copy_sparse_prefill=False), dict(sparse_kv="paged")])
+                                    dict(sparse_kv="paged")])
 def test_std_generate_rejects_unsupported_options(kwargs):
     with pytest.raises(ValueError):
         std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
@@ -117,11 +117,11 @@ def test_std_generate_rejects_unsupported_options(kwargs):
                                          sequential_fallback_max_accept=0),
                                     dict(verify_fallback="sequential_guard"),
                                     dict(verify_fallback="sequential_on_low_margin", verify_margin_threshold=0.1),
-                                    dict(verify_margin_threshold=0.0)])
+                                    dict(verify_margin_threshold=0.0), dict(copy_sparse_prefill=False)])
 def test_std_generate_accepts_the_reference_verify_options(kwargs):
-    """The reference's verify modes, fallbacks and margin threshold
-    (std_qwen25vl.py:634-660) pass validation: the call then fails on the
-    missing model, not on the option."""
+    """The reference's verify modes, fallbacks, margin threshold
+    (std_qwen25vl.py:634-660) and copy_sparse_prefill=False pass validation:
+    the call then fails on the missing model, not on the option."""
     with pytest.raises(AttributeError):
         std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
 
