@@ -113,6 +113,10 @@ class RandomDecoder:
         self.verify_collector = None      # set by VerificationCollectorV3.install()
         self.capture_text_queries = False
         self.captured_queries: List[Optional[torch.Tensor]] = [None] * c.num_hidden_layers
+        # output_attentions of a prompt prefill step: each layer's softmax
+        # probabilities [1, n_q, n, past + n] (zero past the causal limit)
+        self.output_attentions = False
+        self.captured_attentions: List[Optional[torch.Tensor]] = [None] * c.num_hidden_layers
         # Device status word of the decode steps: the appends and attention
         # launches OR ops' cache-overflow bit into it when a device length would
         # place a row, or the attended keys, past a cache's capacity (nothing is
@@ -161,8 +165,10 @@ class RandomDecoder:
                 x[0, vis] = visual_embeds[:n_vis].to(x.dtype)
         return x
 
-    def _prefill_attention(self, q, k_new, v_new, kc: KVCache, vc: KVCache, chunk: int = 512) -> torch.Tensor:
-        """Causal attention of n prompt rows over the cache (torch, fp32)."""
+    def _prefill_attention(self, q, k_new, v_new, kc: KVCache, vc: KVCache, chunk: int = 512,
+                           probs: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Causal attention of n prompt rows over the cache (torch, fp32);
+        probs (optional, [1, n_q, n, past + n]) receives the probabilities."""
         c = self.config
         g_size = c.num_attention_heads // c.num_key_value_heads
         past = kc.length
@@ -170,6 +176,8 @@ class RandomDecoder:
         kc.cat(k_new)
         vc.cat(v_new)
         out = torch.empty_like(q)
+        if probs is not None:
+            probs.zero_()
         scale = 1.0 / math.sqrt(c.head_dim)
         for g in range(c.num_key_value_heads):
             for c0 in range(0, n, chunk):
@@ -183,14 +191,18 @@ class RandomDecoder:
                 kpos = torch.arange(s_len, device=q.device)
                 s.masked_fill_((kpos[None, :] > qpos[:, None])[None], float("-inf"))
                 p = torch.softmax(s, dim=-1)
+                if probs is not None:
+                    probs[0, g * g_size:(g + 1) * g_size, c0:c1, :s_len] = p.to(probs.dtype)
                 o = p.reshape(-1, s_len) @ vg
                 out[0, g * g_size:(g + 1) * g_size, c0:c1] = o.view(g_size, c1 - c0, c.head_dim).to(q.dtype)
         return out
 
     def fused_rows(self, n: int) -> bool:
-        """Whether n rows per step take the HIP rope/append + attention path."""
+        """Whether n rows per step take the HIP rope/append + attention path
+        (never while a prompt prefill step returns its attention
+        probabilities, which the torch prefill attention forms)."""
         c = self.config
-        return n * (c.num_attention_heads // c.num_key_value_heads) <= MAX_FUSED_ROWS
+        return not self.output_attentions and n * (c.num_attention_heads // c.num_key_value_heads) <= MAX_FUSED_ROWS
 
     def _attention(self, li: int, x: torch.Tensor, cos, sin, kc: KVCache, vc: KVCache,
                    state: Optional[torch.Tensor], host_lengths: bool) -> torch.Tensor:
@@ -251,7 +263,11 @@ class RandomDecoder:
             self.captured_queries[li] = q
         if not host_lengths:
             raise ValueError("a device-state step must have at most 96 query rows per KV head")
-        out = self._prefill_attention(q, k, v, kc, vc)
+        probs = None
+        if self.output_attentions:
+            probs = torch.empty(1, hq, n, kc.length + n, dtype=q.dtype, device=q.device)
+            self.captured_attentions[li] = probs
+        out = self._prefill_attention(q, k, v, kc, vc, probs=probs)
         collector = self.verify_collector
         if collector is not None and collector.collecting and n > 1 and q.dtype in (torch.bfloat16, torch.float16):
             # a verify longer than the fused launches serve (more than 96 query rows per KV head): the

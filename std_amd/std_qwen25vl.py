@@ -175,22 +175,32 @@ def split_video_text_inputs(input_ids: torch.Tensor, video_token_id: int) -> Tup
 
 
 def prefill_prompt(model, inputs: Dict[str, torch.Tensor], past_key_values, video_token_id: int,
-                   capture_text_queries: bool = False):
+                   output_attentions: bool = False, capture_text_queries: bool = False):
     """Video-prefix prefill, then the text suffix (std_qwen25vl.py:150-172).
-    Returns (prompt ids, next token [1, 1] on the device, text_start); with
-    capture_text_queries the text suffix's per-layer queries are kept on the
-    model for selection."""
+    Returns, as the reference does, (prompt ids, next token [1, 1] on the
+    device, attentions, text_start): with output_attentions the text suffix's
+    per-layer softmax probabilities [1, n_q, T, P] in the model dtype (the
+    input of build_sparse_selection), else None. With capture_text_queries
+    the text suffix's per-layer queries are kept on the model instead, for
+    build_sparse_selection_from_queries (which never materialises the
+    probabilities)."""
     input_ids = inputs["input_ids"].to(model.device)
     visual = inputs.get("visual_embeds")
     text_start, video_ids, text_ids = split_video_text_inputs(input_ids, video_token_id)
     model(video_ids, past_key_values, visual_embeds=visual)
     model.capture_text_queries = capture_text_queries
+    model.output_attentions = bool(output_attentions)
     try:
         logits = model(text_ids, past_key_values)
     finally:
         model.capture_text_queries = False
+        model.output_attentions = False
+    attentions = None
+    if output_attentions:
+        attentions = tuple(model.captured_attentions)
+        model.captured_attentions = [None] * len(model.captured_attentions)
     next_token = _token_argmax(logits)
-    return input_ids, next_token, text_start
+    return input_ids, next_token, attentions, text_start
 
 
 # ---------------------------------------------------------------------------
@@ -609,7 +619,7 @@ def ar_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id:
                                                  _cache_capacity(prompt_len, max_new_tokens, 0))
     cache_init_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
     stage = _profile_mark(profile_prefill)
-    prompt_ids, next_token, _ = prefill_prompt(model, inputs, pkv, video_token_id)
+    prompt_ids, next_token, _, _ = prefill_prompt(model, inputs, pkv, video_token_id)
     prefill_time = _profile_mark(profile_prefill) - stage if profile_prefill else 0.0
 
     generated: List[torch.Tensor] = []
@@ -748,7 +758,7 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     trace = _TRACE_COLLECTOR
     if trace is not None:
         trace.begin_prefill()
-    prompt_ids, dense_next, text_start = prefill_prompt(model, inputs, dense_pkv, video_token_id,
+    prompt_ids, dense_next, _, text_start = prefill_prompt(model, inputs, dense_pkv, video_token_id,
                                                         capture_text_queries=True)
     if trace is not None:
         trace.end_prefill()

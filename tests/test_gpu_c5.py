@@ -47,7 +47,7 @@ def test_c5_selection_and_compaction(c5):
     P = N_VIS + N_TEXT
     announce(f"c5: prefill of {P} tokens and selection")
     pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.bfloat16, P + 8)
-    prompt_ids, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
+    prompt_ids, _, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
     queries = list(model.captured_queries)
     model.captured_queries = [None] * cfg.num_hidden_layers
     sel = build_sparse_selection_from_queries(queries, [layer[0].data for layer in pkv], prompt_ids,

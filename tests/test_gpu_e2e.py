@@ -40,7 +40,7 @@ def test_selection_and_compaction_from_prefill(tiny32):
     P = inputs["input_ids"].shape[1]
     announce(f"e2e selection tiny fp32 P={P}")
     pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.float32, P + 8)
-    prompt_ids, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
+    prompt_ids, _, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
     queries = list(model.captured_queries)
     assert text_start == N_VISUAL and queries[0].shape == (1, 7, N_TEXT, 128)
     sel = build_sparse_selection_from_queries(queries, [layer[0].data for layer in pkv], prompt_ids,
@@ -71,7 +71,7 @@ def test_compaction_from_a_reference_built_selection(tiny32):
     P = inputs["input_ids"].shape[1]
     announce(f"e2e compaction from a reference-built selection P={P}")
     pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.float32, P + 8)
-    prompt_ids, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
+    prompt_ids, _, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
     sel = build_sparse_selection_from_queries(list(model.captured_queries), [layer[0].data for layer in pkv],
                                               prompt_ids, cfg.video_token_id, text_start, target_k_plus_text=TARGET,
                                               num_key_value_heads=1)
@@ -279,3 +279,43 @@ def test_cache_overflow_raises_instead_of_dropping_rows(tiny32, monkeypatch, use
     std, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, max_new_tokens=12, gamma=5,
                                    target_k_plus_text=TARGET, ignore_eos=True, use_graphs=use_graphs)
     assert std.generate_len == 12 and int(model.decode_status) == 0
+
+
+@pytest.mark.parametrize("n_text", [N_TEXT, 9])
+def test_prefill_output_attentions_feed_the_reference_selection(tiny32, n_text):
+    """prefill_prompt(..., output_attentions=True) returns, as the reference's
+    does (std_qwen25vl.py:150-172), each layer's text-suffix probabilities
+    [1, n_q, T, P]: the causal softmax of the captured queries against the
+    cached keys (fp64 recomputation, zero past each row's limit), and
+    build_sparse_selection on them selects what the oracle selects from the
+    same probabilities. Nine text rows fit the fused decode launch, which a
+    prefill asked for its probabilities must not take."""
+    from oracle import selection as ref_sel
+    from std_amd.std_qwen25vl import build_sparse_selection
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 17, n_text=n_text)
+    P = inputs["input_ids"].shape[1]
+    announce(f"prefill output_attentions tiny fp32 P={P} T={n_text}")
+    pkv, _, _ = initialize_past_key_values(cfg, dev(), torch.float32, P + 8)
+    prompt_ids, nxt, attn, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, True,
+                                                       capture_text_queries=True)
+    assert text_start == N_VISUAL and len(attn) == cfg.num_hidden_layers
+    pkv2, _, _ = initialize_past_key_values(cfg, dev(), torch.float32, P + 8)
+    _, nxt2, none, _ = prefill_prompt(model, inputs, pkv2, cfg.video_token_id)
+    assert none is None and torch.equal(nxt, nxt2)
+    g = cfg.num_attention_heads // cfg.num_key_value_heads
+    for li in range(cfg.num_hidden_layers):
+        a = attn[li]
+        assert a.shape == (1, cfg.num_attention_heads, n_text, P) and a.dtype == torch.float32
+        q = model.captured_queries[li].double().cpu()                   # [1, n_q, T, D]
+        k = pkv[li][0].data[:, :, :P].double().cpu()                     # [1, n_kv, P, D]
+        s = (q @ k.repeat_interleave(g, dim=1).transpose(-1, -2)) / np.sqrt(q.shape[-1])
+        rows = torch.arange(text_start, P)[:, None]
+        s = s.masked_fill(torch.arange(P)[None, :] > rows, float("-inf"))
+        np.testing.assert_allclose(a.double().cpu().numpy(), torch.softmax(s, -1).numpy(), rtol=1e-4, atol=1e-6)
+    sel = build_sparse_selection(attn, prompt_ids, cfg.video_token_id, text_start, target_k_plus_text=TARGET,
+                                 num_key_value_heads=cfg.num_key_value_heads)
+    for li in range(cfg.num_hidden_layers):
+        scores = ref_sel.scores_from_probs(attn[li].double().cpu().numpy(), cfg.num_key_value_heads)
+        want = ref_sel.topk_positions(scores, np.arange(text_start), sel.k)
+        np.testing.assert_array_equal(sel.topk_positions[li].numpy(), want)

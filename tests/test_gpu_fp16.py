@@ -254,7 +254,7 @@ def test_loop_selection_and_compaction_from_fp16_prefill():
     P = inputs["input_ids"].shape[1]
     announce(f"fp16 loop: selection from prefill P={P}")
     pkv, _, _ = initialize_past_key_values(cfg, dev(), F16, P + 8)
-    prompt_ids, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
+    prompt_ids, _, _, text_start = prefill_prompt(model, inputs, pkv, cfg.video_token_id, capture_text_queries=True)
     queries = list(model.captured_queries)
     assert queries[0].dtype == F16 and torch.isfinite(queries[0]).all()
     sel = build_sparse_selection_from_queries(queries, [layer[0].data for layer in pkv], prompt_ids,
