@@ -74,18 +74,18 @@ def default_max_cache_len(max_position_embeddings: int) -> int:
 
 
 def initialize_past_key_values(
-    config, device: torch.device = None, dtype: torch.dtype = None, max_cache_len: int = None
+    model, device: torch.device = None, dtype: torch.dtype = None, max_cache_len: int = None
 ) -> Tuple[List[List[KVCache]], torch.Tensor, torch.Tensor]:
     """Allocate one cache (kv_cache.py:72-165) on a single device.
 
-    ``config`` is a model config, or the model itself as the reference passes
-    it (``initialize_past_key_values(model)``): then the config, device and
-    dtype come from the model. Returns
+    ``model`` is the model, as the reference passes it
+    (``initialize_past_key_values(model)``), whose config, device and dtype
+    are used, or a model config with ``device`` and ``dtype`` given. Returns
     ``(past_key_values, data [2L, 1, Hkv, max_len, D], current_length_data [2L])``;
     ``past_key_values[l] = [K cache, V cache]``. Rows are zero-initialised as
     in the reference."""
-    if hasattr(config, "config"):                     # the reference's form: a model
-        model = config
+    config = model
+    if hasattr(model, "config"):                      # the reference's form: a model
         config = model.config
         device = model.device if device is None else device
         dtype = model.dtype if dtype is None else dtype

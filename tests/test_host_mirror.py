@@ -238,3 +238,21 @@ def test_sparse_selection_is_built_as_the_reference_builds_it():
         SparseSelection(layers, torch.tensor([7, 8]), 9, 7, 2, 3, topk_device=sel.topk_device)
     with pytest.raises(ValueError):
         SparseSelection(None, torch.tensor([7, 8]), 9, 7, 2, 3)
+
+
+def test_initialize_past_key_values_takes_the_model_as_the_reference_passes_it():
+    """initialize_past_key_values(model) (kv_cache.py:72): config, device and
+    dtype from the model, positionally or by the reference's keyword."""
+    cfg = DecoderConfig.tiny(layers=2)
+
+    class Model:
+        config = cfg
+        device = torch.device("cpu")
+        dtype = torch.float16
+
+    for pkv, data, lengths in (kv_cache.initialize_past_key_values(Model(), max_cache_len=8),
+                               kv_cache.initialize_past_key_values(model=Model(), max_cache_len=8)):
+        assert data.shape == (4, 1, 1, 8, 128) and data.dtype == torch.float16 and lengths.shape == (4,)
+        assert len(pkv) == 2 and pkv[1][1].capacity == 8
+    with pytest.raises(ValueError):
+        kv_cache.initialize_past_key_values(cfg, max_cache_len=8)          # a bare config needs device and dtype
