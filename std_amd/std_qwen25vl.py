@@ -317,8 +317,11 @@ class SparseDraftController:
                  use_compile: bool = False):
         if sparse_attn_mode not in SPARSE_ATTN_MODES:
             raise ValueError(f"Unsupported sparse_attn_mode={sparse_attn_mode!r}.")
-        if use_compile:
-            raise ValueError("use_compile is not supported: the HIP decode step is captured with HIP graphs instead")
+        # use_compile: the reference compiles the sparse step with
+        # torch.compile(mode="reduce-overhead"), i.e. CUDA-graph replay
+        # (std_qwen25vl.py:456-464); here the generate loop captures the step
+        # in a HIP graph instead (std_generate_qwen25vl turns use_graphs on)
+        self.use_compile = bool(use_compile)
         self.model = model
         self.selection = selection
         self.sparse_attn_mode = sparse_attn_mode
@@ -693,6 +696,10 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
     math re-verification does (std_qwen25vl.py:843-858); that re-run would
     return the same predictions, so ``fallback_accepted_extra`` stays 0.
 
+    use_compile: the reference compiles its sparse step into CUDA-graph
+    replays (std_qwen25vl.py:456-464); here it turns on use_graphs, unless a
+    sequential verify, fallback or margin check needs the eager loop.
+
     verify_mode="sequential", verify_fallback and verify_margin_threshold:
     as in the reference (std_qwen25vl.py:780-893): sequential verification
     and the sequential replay of a round (counted in ``fallback_count``, its
@@ -732,9 +739,13 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         raise ValueError("verify_attn_backend must be 'default', 'math', or 'math_on_full_accept'.")
     if verify_margin_threshold is not None and verify_margin_threshold < 0:
         raise ValueError("verify_margin_threshold must be non-negative.")
-    if use_graphs and (verify_mode != "parallel" or verify_fallback != "none" or verify_margin_threshold is not None):
+    host_policies = verify_mode != "parallel" or verify_fallback != "none" or verify_margin_threshold is not None
+    if use_graphs and host_policies:
         raise ValueError("use_graphs=True replays the parallel verify with no host-side fallback; run "
                          "verify_mode='sequential', verify fallbacks and margin checks with use_graphs=False")
+    # the reference's use_compile (a CUDA-graph-compiled sparse step) maps to
+    # the graph-replayed rounds, where the round has no host-side decision
+    use_graphs = use_graphs or (use_compile and not host_policies)
     if adaptive_gamma_min is not None and not (1 <= adaptive_gamma_min <= gamma):
         raise ValueError("adaptive_gamma_min must be between 1 and gamma.")
     if adaptive_gamma_mode not in {"accept_len", "conservative"}:

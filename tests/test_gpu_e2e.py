@@ -319,3 +319,18 @@ def test_prefill_output_attentions_feed_the_reference_selection(tiny32, n_text):
         scores = ref_sel.scores_from_probs(attn[li].double().cpu().numpy(), cfg.num_key_value_heads)
         want = ref_sel.topk_positions(scores, np.arange(text_start), sel.k)
         np.testing.assert_array_equal(sel.topk_positions[li].numpy(), want)
+
+
+def test_use_compile_runs_the_graph_replayed_rounds(tiny32):
+    """use_compile=True (the reference's CUDA-graph-compiled sparse step,
+    std_qwen25vl.py:456-464) takes the graph-replayed rounds: the same tokens
+    and accept lengths as use_graphs=True and as the eager loop."""
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 5)
+    announce("e2e use_compile vs use_graphs vs eager, tiny fp32")
+    kw = dict(max_new_tokens=24, gamma=4, target_k_plus_text=TARGET, ignore_eos=True)
+    eager, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, **kw)
+    graphs, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, use_graphs=True, **kw)
+    comp, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, use_compile=True, **kw)
+    for r in (graphs, comp):
+        assert torch.equal(r.output_ids, eager.output_ids) and r.accept_lengths == eager.accept_lengths

@@ -96,6 +96,7 @@ def test_controller_validates_mode():
         assert m.sparse_controller is c and not c.enabled
     c.set_enabled(True)
     assert c.enabled
+    assert SparseDraftController(Model(), sel, use_compile=True).use_compile      # the reference's flag is taken
 
 
 @pytest.mark.parametrize("kwargs", [dict(verify_mode="tree"), dict(verify_fallback="always"),
@@ -117,11 +118,12 @@ def test_std_generate_rejects_unsupported_options(kwargs):
                                          sequential_fallback_max_accept=0),
                                     dict(verify_fallback="sequential_guard"),
                                     dict(verify_fallback="sequential_on_low_margin", verify_margin_threshold=0.1),
-                                    dict(verify_margin_threshold=0.0), dict(copy_sparse_prefill=False)])
+                                    dict(verify_margin_threshold=0.0), dict(copy_sparse_prefill=False),
+                                    dict(use_compile=True), dict(use_compile=True, verify_mode="sequential")])
 def test_std_generate_accepts_the_reference_verify_options(kwargs):
     """The reference's verify modes, fallbacks, margin threshold
-    (std_qwen25vl.py:634-660) and copy_sparse_prefill=False pass validation:
-    the call then fails on the missing model, not on the option."""
+    (std_qwen25vl.py:634-660), copy_sparse_prefill=False and use_compile pass
+    validation: the call then fails on the missing model, not on the option."""
     with pytest.raises(AttributeError):
         std_generate_qwen25vl(None, {"input_ids": torch.zeros(1, 4, dtype=torch.long)}, 7, 8, **kwargs)
 
