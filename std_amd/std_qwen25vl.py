@@ -698,7 +698,8 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
 
     use_compile: the reference compiles its sparse step into CUDA-graph
     replays (std_qwen25vl.py:456-464); here it turns on use_graphs, unless a
-    sequential verify, fallback or margin check needs the eager loop.
+    sequential verify, fallback or margin check needs the eager loop or the
+    verify rows exceed the device-state launches (more than 96 per KV head).
 
     verify_mode="sequential", verify_fallback and verify_margin_threshold:
     as in the reference (std_qwen25vl.py:780-893): sequential verification
@@ -744,8 +745,11 @@ def std_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id
         raise ValueError("use_graphs=True replays the parallel verify with no host-side fallback; run "
                          "verify_mode='sequential', verify fallbacks and margin checks with use_graphs=False")
     # the reference's use_compile (a CUDA-graph-compiled sparse step) maps to
-    # the graph-replayed rounds, where the round has no host-side decision
-    use_graphs = use_graphs or (use_compile and not host_policies)
+    # the graph-replayed rounds, where the round has no host-side decision and
+    # the verify rows fit the device-state launches
+    if use_compile and not use_graphs and not host_policies:
+        fits = getattr(model, "fused_rows", None)
+        use_graphs = fits is not None and fits(gamma + 1)
     if adaptive_gamma_min is not None and not (1 <= adaptive_gamma_min <= gamma):
         raise ValueError("adaptive_gamma_min must be between 1 and gamma.")
     if adaptive_gamma_mode not in {"accept_len", "conservative"}:

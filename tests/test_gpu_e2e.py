@@ -334,3 +334,17 @@ def test_use_compile_runs_the_graph_replayed_rounds(tiny32):
     comp, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, use_compile=True, **kw)
     for r in (graphs, comp):
         assert torch.equal(r.output_ids, eager.output_ids) and r.accept_lengths == eager.accept_lengths
+
+
+def test_use_compile_beyond_the_device_state_rows_runs_eagerly(tiny32):
+    """With gamma = 13 the verify carries 14 x 7 = 98 rows per KV head, more
+    than the device-state launches serve: use_compile then keeps the eager
+    loop (the reference's compiled step has no such limit) and matches it."""
+    cfg, model = tiny32
+    inputs = _inputs(cfg, 6)
+    announce("e2e use_compile at gamma 13 (eager rounds), tiny fp32")
+    kw = dict(max_new_tokens=30, gamma=13, target_k_plus_text=TARGET, ignore_eos=True)
+    assert not model.fused_rows(14)
+    eager, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, **kw)
+    comp, _ = std_generate_qwen25vl(model, inputs, cfg.video_token_id, cfg.eos_token_id, use_compile=True, **kw)
+    assert torch.equal(comp.output_ids, eager.output_ids) and comp.accept_lengths == eager.accept_lengths
