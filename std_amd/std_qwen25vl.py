@@ -612,7 +612,10 @@ def ar_generate_qwen25vl(model, inputs: Dict[str, torch.Tensor], video_token_id:
     (std_qwen25vl.py:553-606); every decode step runs the HIP rope/append and
     attention launches of each layer over the full dense cache. With
     use_graphs the step (cache length and position on the device) is captured
-    once in a HIP graph and replayed per token."""
+    once in a HIP graph and replayed per token. output_attentions is taken and
+    changes nothing: the reference sets it so that the AR prefill runs the
+    STD selection prefill's attention path (std_qwen25vl.py:565-568), and here
+    both loops prefill through the same path without it."""
     del output_attentions
     torch.cuda.synchronize()
     start = time.time()
